@@ -1,0 +1,215 @@
+"""ctypes access to the CPU oracle (libsiq_oracle.so) and, when it was built,
+the compiled reference checker (_ref/libsiphon_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, always as the checker, never as the thing
+measured or shipped.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "libsiq_oracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libsiphon_ref.so")
+
+# ggml type ids and block geometry (reference quant.h:92-119)
+F32, F16, Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 6, 8, 10, 11, 12, 13, 14, 15
+GEOM = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34),
+        Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176),
+        Q6_K: (256, 210), Q8_K: (256, 292)}
+PAIR = {F16: F16, Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K,
+        Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
+NAMES = {F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K",
+         Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_K: "Q8_K"}
+WEIGHT_TYPES = [Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F16]
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_u32 = ctypes.c_uint32
+
+
+def row_bytes(wtype: int, n: int) -> int:
+    be, bb = GEOM[wtype]
+    return n // be * bb
+
+
+def pair_bytes(pair: int, n: int) -> int:
+    be, bb = GEOM[pair]
+    return n // be * bb
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def build_oracle() -> None:
+    subprocess.run(["make", "-s", "-C", HERE, "libsiq_oracle.so"], check=True)
+
+
+def build_ref() -> bool:
+    """Compile the reference checker when the reference tree is present."""
+    if not os.path.isdir("/root/reference/src"):
+        return False
+    subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+    return True
+
+
+class Oracle:
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            build_oracle()
+        L = ctypes.CDLL(path)
+        L.siq_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.siq_f16_to_f32.restype = ctypes.c_float
+        L.siq_f32_to_f16.argtypes = [ctypes.c_float]
+        L.siq_f32_to_f16.restype = ctypes.c_uint16
+        for fn in ("siq_quantize_q8_K", "siq_quantize_q8_0", "siq_quantize_q8_0_scalar",
+                   "siq_convert_f16"):
+            getattr(L, fn).argtypes = [_vp, _vp, _i64]
+            getattr(L, fn).restype = None
+        L.siq_quantize_pair.argtypes = [_u32, _vp, _vp, _i64]
+        L.siq_dequant_row.argtypes = [_u32, _vp, _vp, _i64]
+        L.siq_vec_dot.argtypes = [_u32, _i64, _vp, _vp, _vp, _vp]
+        L.siq_vec_dot_dequant.argtypes = [_u32, _i64, _vp, _vp, _vp, _vp]
+        L.siq_gemv.argtypes = [_u32, _vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_int]
+        L.siq_gemm.argtypes = [_u32, _vp, _i64, _i64, _vp, _i64, _vp, _vp, ctypes.c_int]
+        self.L = L
+
+    def f16_to_f32(self, h: int) -> float:
+        return self.L.siq_f16_to_f32(h)
+
+    def f32_to_f16(self, f: float) -> int:
+        return self.L.siq_f32_to_f16(f)
+
+    def quantize(self, pair: int, x: np.ndarray, scalar_q8_0: bool = False) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(pair_bytes(pair, x.size), dtype=np.uint8)
+        if pair == Q8_0 and scalar_q8_0:
+            self.L.siq_quantize_q8_0_scalar(_ptr(x), _ptr(out), x.size)
+        else:
+            assert self.L.siq_quantize_pair(pair, _ptr(x), _ptr(out), x.size)
+        return out
+
+    def dequant(self, wtype: int, w: np.ndarray, n: int) -> np.ndarray:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        out = np.zeros(n, dtype=np.float32)
+        assert self.L.siq_dequant_row(wtype, _ptr(w), _ptr(out), n)
+        return out
+
+    def vec_dot(self, wtype: int, n: int, w: np.ndarray, a: np.ndarray, dequant_form=False):
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        a = np.ascontiguousarray(a, dtype=np.uint8)
+        d = ctypes.c_double()
+        m = ctypes.c_double()
+        fn = self.L.siq_vec_dot_dequant if dequant_form else self.L.siq_vec_dot
+        assert fn(wtype, n, _ptr(w), _ptr(a), ctypes.byref(d), ctypes.byref(m))
+        return d.value, m.value
+
+    def gemv(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, x: np.ndarray, lanes: int = 8):
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(n_out, dtype=np.float32)
+        l1 = np.zeros(n_out, dtype=np.float64)
+        assert self.L.siq_gemv(wtype, _ptr(W), n_out, n_in, _ptr(x), _ptr(y), _ptr(l1), lanes)
+        return y, l1
+
+    def gemm(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, X: np.ndarray, lanes: int = 8):
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        M = X.shape[0]
+        Y = np.zeros((M, n_out), dtype=np.float32)
+        L1 = np.zeros((M, n_out), dtype=np.float64)
+        assert self.L.siq_gemm(wtype, _ptr(W), n_out, n_in, _ptr(X), M, _ptr(Y), _ptr(L1), lanes)
+        return Y, L1
+
+
+class Reference:
+    """The reference's own kernels (compiled from /root/reference/src by
+    oracle/Makefile); None-returning loader when it was not built."""
+
+    DOT_NAMES = {F16: "f16", Q4_0: "q4_0_q8_0", Q5_0: "q5_0_q8_0", Q8_0: "q8_0_q8_0",
+                 Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K",
+                 Q5_K: "q5_K_q8_K", Q6_K: "q6_K_q8_K"}
+
+    def __init__(self, path: str = REF_SO):
+        L = ctypes.CDLL(path)
+        L.ref_shim_impl.restype = ctypes.c_int
+        L.si_f32_to_f16.argtypes = [ctypes.c_float]
+        L.si_f32_to_f16.restype = ctypes.c_uint16
+        L.si_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.si_f16_to_f32.restype = ctypes.c_float
+        for fn in ("si_quant_row_q8_0", "si_quant_row_q8_K", "si_avx2_quant_row_q8_0"):
+            getattr(L, fn).argtypes = [_vp, _vp, ctypes.c_int]
+            getattr(L, fn).restype = None
+        L.si_dequant_row.argtypes = [_u32, _vp, _vp, ctypes.c_int]
+        L.si_dequant_row.restype = ctypes.c_bool
+        for name in self.DOT_NAMES.values():
+            for pre in ("si_dot_", "si_avx2_dot_"):
+                f = getattr(L, pre + name)
+                f.argtypes = [ctypes.c_int, _vp, _vp, _vp]
+                f.restype = None
+        L.ref_shim_gemv.argtypes = [_u32, _vp, _i64, _i64, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp]
+        L.ref_shim_gemv.restype = ctypes.c_int
+        self.L = L
+        self.avx2 = bool(L.ref_shim_impl())
+
+    @staticmethod
+    def load():
+        if not os.path.exists(REF_SO):
+            return None
+        return Reference()
+
+    def quant_q8_K(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(pair_bytes(Q8_K, x.size), dtype=np.uint8)
+        self.L.si_quant_row_q8_K(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def quant_q8_0(self, x: np.ndarray, simd: bool = True) -> np.ndarray:
+        """simd=True: the AVX2 quantizer production dispatches to on x86.
+        simd=False: the reference's dispatcher, which takes its scalar
+        branch only in a process started with SI_SCALAR=1 (self.avx2 is
+        then False)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(pair_bytes(Q8_0, x.size), dtype=np.uint8)
+        if simd:
+            self.L.si_avx2_quant_row_q8_0(_ptr(x), _ptr(out), x.size)
+        else:
+            assert not self.avx2, "scalar Q8_0 needs a process started with SI_SCALAR=1"
+            self.L.si_quant_row_q8_0(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def f16(self, x: np.ndarray) -> np.ndarray:
+        return np.array([self.L.si_f32_to_f16(float(v)) for v in np.asarray(x, np.float32)],
+                        dtype=np.uint16)
+
+    def dequant(self, wtype: int, w: np.ndarray, n: int) -> np.ndarray:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        out = np.zeros(n, dtype=np.float32)
+        assert self.L.si_dequant_row(wtype, _ptr(w), _ptr(out), n)
+        return out
+
+    def dot(self, wtype: int, n: int, w: np.ndarray, a: np.ndarray, simd: bool = True) -> float:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        a = np.ascontiguousarray(a, dtype=np.uint8)
+        s = ctypes.c_float()
+        f = getattr(self.L, ("si_avx2_dot_" if simd else "si_dot_") + self.DOT_NAMES[wtype])
+        f(n, ctypes.byref(s), _ptr(w), _ptr(a))
+        return s.value
+
+    def gemv_timed(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, x: np.ndarray,
+                   lanes: int, reps: int):
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(n_out, dtype=np.float32)
+        secs = np.zeros(reps, dtype=np.float64)
+        rc = self.L.ref_shim_gemv(wtype, _ptr(W), n_out, n_in, _ptr(x), _ptr(y), lanes, reps,
+                                  _ptr(secs))
+        assert rc == 0
+        return y, secs
