@@ -1,0 +1,144 @@
+/* sihip: C-ABI of libsiphon_hip.so, the MI355X (gfx950) backend for
+ * Siphon's quantized matvec / matmul path.
+ *
+ * The reference routes every weight x activation product through one
+ * vtable slot, si_backend.gemv (reference include/siphon/tensor.h:43-55),
+ * whose CPU implementation is cpu_gemv (reference src/backend.c:85-120):
+ * convert the f32 activation row once into the weight type's "dot pair"
+ * format (Q8_K for K-quants, Q8_0 for Q4_0/Q5_0/Q8_0, F16 for F16), then
+ * one full dot product per output row. This library is the device side of
+ * a second si_backend instance: the host (C17) dlopens it, uploads each
+ * weight tensor once, and forwards gemv calls here. Plain C types only;
+ * no HIP or torch types cross this boundary (streams are opaque void*).
+ *
+ * Conventions (mirroring the reference):
+ *  - return 0 (SI_OK) or a negative SI_* code (reference
+ *    include/siphon/common.h:25-34); SIHIP_EDEVICE is added for HIP
+ *    runtime failures. A human-readable message for the last failure on a
+ *    context is available from sihip_last_error (like si_errstr,
+ *    reference src/util.c:7-17, but per context).
+ *  - on failure, outputs are left untouched (reference backend.c:90-98).
+ *  - weight shapes follow the reference: W is [n_out x n_in] row-major,
+ *    ne[0] = n_in, each row n_in / block_elems consecutive GGUF blocks
+ *    (reference backend.c:88, 112; tensor.h:66-70).
+ *  - results are deterministic run to run: no split-K atomics, every
+ *    output is reduced in a fixed order.
+ */
+#ifndef SIHIP_H
+#define SIHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIHIP_ABI_VERSION 1
+
+/* error codes: the reference's SI_* values plus one for the device */
+#define SIHIP_OK        0
+#define SIHIP_ENOMEM   (-1)
+#define SIHIP_ENOTSUP  (-4)
+#define SIHIP_EINVAL   (-5)
+#define SIHIP_ERANGE   (-7)
+#define SIHIP_EDEVICE  (-8)
+
+typedef struct sihip_ctx sihip_ctx;
+typedef struct sihip_weight sihip_weight;
+
+/* ---- lifecycle ------------------------------------------------------- */
+
+/* Returns SIHIP_ABI_VERSION; the loader refuses a library whose value
+ * differs from the header it was compiled against. */
+int sihip_abi_version(void);
+
+/* Open a context on HIP device `device` (0-based). */
+int sihip_init(int device, sihip_ctx **out);
+/* Release the context and its staging buffers. Weights must be freed
+ * first. */
+void sihip_shutdown(sihip_ctx *ctx);
+/* Message of the most recent failure on ctx ("" if none). With ctx NULL,
+ * the most recent failure of sihip_init. */
+const char *sihip_last_error(const sihip_ctx *ctx);
+
+/* ---- weights --------------------------------------------------------- */
+
+/* Upload one weight matrix given as GGUF blocks (the bytes of an mmap'd
+ * tensor, reference si_tensor.data, tensor.h:30-38). ggml_type is the
+ * on-disk type id (reference quant.h:103-119): F16, Q4_0, Q5_0, Q8_0,
+ * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K. `bytes` must equal
+ * n_out * (n_in / block_elems) * block_bytes, and n_in must be a multiple
+ * of the block size (reference backend.c:158-164 rejects the same). The
+ * device keeps its own copy, repacked for the kernels; the host bytes
+ * stay owned by the caller. */
+int sihip_weight_upload(sihip_ctx *ctx, uint32_t ggml_type, uint64_t n_out,
+                        uint64_t n_in, const void *host_blocks,
+                        uint64_t bytes, sihip_weight **out);
+int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w);
+/* Device bytes the repacked weight occupies (>= the GGUF bytes). */
+uint64_t sihip_weight_device_bytes(const sihip_weight *w);
+/* Layout introspection: 32-element units per row handled side by side by
+ * one wavefront (1..64). Chosen at upload from the shape; the environment
+ * variable SIHIP_TILE_COLS forces it when valid for the shape (tests). */
+int sihip_weight_tile_cols(const sihip_weight *w);
+
+/* ---- matvec / matmul: host pointers, synchronous ---------------------
+ * Same semantics as the reference cpu_gemv (backend.c:85-120):
+ * y[i] = <W.row(i), pair(x)> for i < n_out, with pair(x) the activation
+ * converted by the bit-exact quantizer of the weight type's pair format.
+ * n_out may be smaller than the uploaded row count (reference gemv takes
+ * n_out from the caller, engine.c:317-378). */
+int sihip_gemv(sihip_ctx *ctx, const sihip_weight *w, const float *x,
+               float *y, int64_t n_out);
+/* Prefill: Y[m, :] = gemv(W, X[m, :]) for m < M; X is [M x n_in] and Y is
+ * [M x n_out], row-major. The reference has no GEMM (prompt tokens run one
+ * si_engine_forward each, reference cmd_run.c:275-283); this is its
+ * batched equivalent, with X quantized per row. */
+int sihip_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X,
+               int64_t M, float *Y);
+
+/* ---- device pointers, stream-ordered (no host synchronisation) -------
+ * x, y, X, Y point to device memory; stream is a hipStream_t (NULL for
+ * the default stream). */
+int sihip_gemv_dev(sihip_ctx *ctx, const sihip_weight *w, const float *x,
+                   float *y, int64_t n_out, void *stream);
+int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float *X,
+                   int64_t M, float *Y, void *stream);
+/* Several matrices that share one input x (q/k/v at reference
+ * engine.c:317-319, gate/up at 375-376) in one launch: y[i] receives
+ * gemv(w[i], x). All w[i] must have the same n_in; at most 4. */
+int sihip_gemv_multi_dev(sihip_ctx *ctx, int count,
+                         const sihip_weight *const *w, const float *x,
+                         float *const *y, void *stream);
+
+/* ---- building blocks exposed for parity tests ------------------------ */
+
+/* Activation quantizers on the device, host pointers. n must be a multiple
+ * of the block size. Output bytes are the reference block layouts:
+ *  Q8_K (reference kernels.c:561-595): f32 d, int8 qs[256], int16
+ *    bsums[16] per 256 (292 B); bsums of an all-zero block are written as 0.
+ *  Q8_0 (reference kernels_avx2.c:594-645, the SIMD path production
+ *    dispatches to on x86): f16 d, int8 qs[32] per 32 (34 B).
+ *  F16 pair conversion (reference backend.c:19-27): RNE binary16. */
+int sihip_quantize_q8_K(sihip_ctx *ctx, const float *x, void *out, int64_t n);
+int sihip_quantize_q8_0(sihip_ctx *ctx, const float *x, void *out, int64_t n);
+int sihip_convert_f16(sihip_ctx *ctx, const float *x, void *out, int64_t n);
+
+/* One dot product on the device with the per-row kernel ABI of the
+ * reference (si_vec_dot_fn, reference kernels.h:45): *s = <x, y> where x
+ * is one row of `wtype` blocks and y is already in the pair format. */
+int sihip_vec_dot(sihip_ctx *ctx, uint32_t wtype, int n, float *s,
+                  const void *x, const void *y);
+
+/* Matvec over n_rows consecutive weight rows (host bytes) against a
+ * pair-format activation (host bytes): the per-row dot of many rows in one
+ * launch, used by parity tests with the reference's own quantized input. */
+int sihip_gemv_pair(sihip_ctx *ctx, uint32_t wtype, int64_t n_rows,
+                    int64_t n_in, const void *rows, const void *xq,
+                    float *y);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIHIP_H */

@@ -1,0 +1,199 @@
+"""Python binding of libsiphon_hip.so (the C-ABI in include/sihip.h).
+
+The product is the C-ABI library; this module is plumbing for tests and the
+benchmark. It loads the in-tree build and raises if it is missing: there is
+no CPU fallback behind it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from .build import HIP_SO
+
+# ggml type ids (reference include/siphon/quant.h:103-119)
+F16, Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 1, 2, 6, 8, 10, 11, 12, 13, 14, 15
+GEOM = {F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q2_K: (256, 84),
+        Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
+        Q8_K: (256, 292)}
+PAIR = {F16: F16, Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K,
+        Q5_K: Q8_K, Q6_K: Q8_K}
+NAMES = {F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K",
+         Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_K: "Q8_K"}
+TYPES = {v: k for k, v in NAMES.items()}
+WEIGHT_TYPES = [Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F16]
+
+ABI_VERSION = 1
+
+
+def row_bytes(wtype: int, n_in: int) -> int:
+    be, bb = GEOM[wtype]
+    return n_in // be * bb
+
+
+class SihipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"sihip error {code}: {msg}")
+        self.code = code
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
+_lib = None
+
+
+def load_library(path: str = HIP_SO) -> ctypes.CDLL:
+    """Load libsiphon_hip.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is missing: build it with `python -m siphon_amd.build` "
+            "(there is no CPU fallback)")
+    L = ctypes.CDLL(path)
+    L.sihip_abi_version.restype = ctypes.c_int
+    L.sihip_init.argtypes = [ctypes.c_int, ctypes.POINTER(_vp)]
+    L.sihip_shutdown.argtypes = [_vp]
+    L.sihip_shutdown.restype = None
+    L.sihip_last_error.argtypes = [_vp]
+    L.sihip_last_error.restype = ctypes.c_char_p
+    L.sihip_weight_upload.argtypes = [_vp, _u32, _u64, _u64, _vp, _u64, ctypes.POINTER(_vp)]
+    L.sihip_weight_free.argtypes = [_vp, _vp]
+    L.sihip_weight_device_bytes.argtypes = [_vp]
+    L.sihip_weight_device_bytes.restype = _u64
+    L.sihip_weight_tile_cols.argtypes = [_vp]
+    L.sihip_gemv.argtypes = [_vp, _vp, _vp, _vp, _i64]
+    L.sihip_gemm.argtypes = [_vp, _vp, _vp, _i64, _vp]
+    L.sihip_gemv_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
+    L.sihip_gemm_dev.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
+    L.sihip_gemv_multi_dev.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(_vp), _vp,
+                                       ctypes.POINTER(_vp), _vp]
+    for fn in ("sihip_quantize_q8_K", "sihip_quantize_q8_0", "sihip_convert_f16"):
+        getattr(L, fn).argtypes = [_vp, _vp, _vp, _i64]
+    L.sihip_vec_dot.argtypes = [_vp, _u32, ctypes.c_int, _vp, _vp, _vp]
+    L.sihip_gemv_pair.argtypes = [_vp, _u32, _i64, _i64, _vp, _vp, _vp]
+    if L.sihip_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path}: ABI version {L.sihip_abi_version()} != {ABI_VERSION}")
+    _lib = L
+    return L
+
+
+def load_library_at(path: str) -> ctypes.CDLL:
+    """Load a specific build of the library (used to compare build variants)."""
+    global _lib
+    saved, _lib = _lib, None
+    try:
+        return load_library(path)
+    finally:
+        _lib = saved
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+class Weight:
+    def __init__(self, dev: "Device", handle: int, wtype: int, n_out: int, n_in: int):
+        self.dev, self.handle, self.type, self.n_out, self.n_in = dev, handle, wtype, n_out, n_in
+
+    @property
+    def device_bytes(self) -> int:
+        return int(self.dev.L.sihip_weight_device_bytes(self.handle))
+
+    @property
+    def tile_cols(self) -> int:
+        return int(self.dev.L.sihip_weight_tile_cols(self.handle))
+
+    @property
+    def gguf_bytes(self) -> int:
+        return self.n_out * row_bytes(self.type, self.n_in)
+
+    def free(self):
+        if self.handle:
+            self.dev.L.sihip_weight_free(self.dev.ctx, self.handle)
+            self.handle = None
+
+
+class Device:
+    """One sihip context on HIP device `device`."""
+
+    def __init__(self, device: int = 0, lib_path: str | None = None):
+        self.L = load_library() if lib_path is None else load_library_at(lib_path)
+        ctx = _vp()
+        rc = self.L.sihip_init(device, ctypes.byref(ctx))
+        if rc != 0:
+            raise SihipError(rc, self.L.sihip_last_error(None).decode())
+        self.ctx = ctx.value
+
+    def _check(self, rc: int):
+        if rc != 0:
+            raise SihipError(rc, self.L.sihip_last_error(self.ctx).decode())
+
+    def close(self):
+        if self.ctx:
+            self.L.sihip_shutdown(self.ctx)
+            self.ctx = None
+
+    def upload(self, wtype: int, n_out: int, n_in: int, blocks: np.ndarray) -> Weight:
+        blocks = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+        h = _vp()
+        self._check(self.L.sihip_weight_upload(self.ctx, wtype, n_out, n_in, _ptr(blocks),
+                                               blocks.size, ctypes.byref(h)))
+        return Weight(self, h.value, wtype, n_out, n_in)
+
+    def gemv(self, w: Weight, x: np.ndarray, n_out: int | None = None) -> np.ndarray:
+        n_out = w.n_out if n_out is None else n_out
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(n_out, dtype=np.float32)
+        self._check(self.L.sihip_gemv(self.ctx, w.handle, _ptr(x), _ptr(y), n_out))
+        return y
+
+    def gemm(self, w: Weight, X: np.ndarray) -> np.ndarray:
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        Y = np.zeros((X.shape[0], w.n_out), dtype=np.float32)
+        self._check(self.L.sihip_gemm(self.ctx, w.handle, _ptr(X), X.shape[0], _ptr(Y)))
+        return Y
+
+    # device-pointer variants (pointers as ints, stream as int or None)
+    def gemv_dev(self, w: Weight, x_ptr: int, y_ptr: int, n_out: int, stream: int | None = None):
+        self._check(self.L.sihip_gemv_dev(self.ctx, w.handle, x_ptr, y_ptr, n_out, stream))
+
+    def gemm_dev(self, w: Weight, X_ptr: int, M: int, Y_ptr: int, stream: int | None = None):
+        self._check(self.L.sihip_gemm_dev(self.ctx, w.handle, X_ptr, M, Y_ptr, stream))
+
+    def gemv_multi_dev(self, ws, x_ptr: int, y_ptrs, stream: int | None = None):
+        n = len(ws)
+        wa = (_vp * n)(*[w.handle for w in ws])
+        ya = (_vp * n)(*y_ptrs)
+        self._check(self.L.sihip_gemv_multi_dev(self.ctx, n, wa, x_ptr, ya, stream))
+
+    def quantize(self, pair: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        be, bb = GEOM[pair]
+        out = np.zeros(x.size // be * bb, dtype=np.uint8)
+        fn = {Q8_K: self.L.sihip_quantize_q8_K, Q8_0: self.L.sihip_quantize_q8_0,
+              F16: self.L.sihip_convert_f16}[pair]
+        self._check(fn(self.ctx, _ptr(x), _ptr(out), x.size))
+        return out
+
+    def vec_dot(self, wtype: int, n: int, w: np.ndarray, a: np.ndarray) -> float:
+        s = np.zeros(1, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        a = np.ascontiguousarray(a, dtype=np.uint8)
+        self._check(self.L.sihip_vec_dot(self.ctx, wtype, n, _ptr(s), _ptr(w), _ptr(a)))
+        return float(s[0])
+
+    def gemv_pair(self, wtype: int, n_rows: int, n_in: int, rows: np.ndarray,
+                  xq: np.ndarray) -> np.ndarray:
+        rows = np.ascontiguousarray(rows, dtype=np.uint8)
+        xq = np.ascontiguousarray(xq, dtype=np.uint8)
+        y = np.zeros(n_rows, dtype=np.float32)
+        self._check(self.L.sihip_gemv_pair(self.ctx, wtype, n_rows, n_in, _ptr(rows), _ptr(xq),
+                                           _ptr(y)))
+        return y

@@ -1,0 +1,88 @@
+"""Build the native parts in-tree:
+
+  siphon_amd/lib/libsiphon_hip.so      C-ABI HIP library (gfx950 kernels)
+  siphon_amd/lib/libsiphon_backend.so  C17 host adapter (si_backend "hip")
+  oracle/libsiq_oracle.so              CPU oracle (test infrastructure)
+  oracle/_ref/libsiphon_ref.so         compiled reference checker (only
+                                       where /root/reference exists)
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+LIB_DIR = os.path.join(PKG, "lib")
+HIP_SO = os.path.join(LIB_DIR, "libsiphon_hip.so")
+BACKEND_SO = os.path.join(LIB_DIR, "libsiphon_backend.so")
+
+ARCH = "gfx950"
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    # quantizers must be bit-exact: one rounding per float operation
+    "-ffp-contract=off",
+    # no packed-fp32 instructions in any kernel
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
+                    if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def hipcc() -> str:
+    for c in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("hipcc not found")
+
+
+def build_hip(verbose: bool = False) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = HIP_SO + ".tmp"
+    _run([hipcc(), *HIPCC_FLAGS, "-o", tmp, os.path.join(PKG, "csrc", "sihip.hip")], verbose)
+    os.replace(tmp, HIP_SO)
+    return HIP_SO
+
+
+def build_backend(verbose: bool = False) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    src = os.path.join(PKG, "host", "backend_hip.c")
+    if not os.path.exists(src):
+        return ""
+    tmp = BACKEND_SO + ".tmp"
+    _run(["gcc", "-std=c17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Werror",
+          "-D_POSIX_C_SOURCE=200809L", "-I", os.path.join(ROOT, "include"),
+          "-I", os.path.join(PKG, "host"), "-o", tmp, src, "-ldl"], verbose)
+    os.replace(tmp, BACKEND_SO)
+    return BACKEND_SO
+
+
+def build_oracle(verbose: bool = False) -> None:
+    odir = os.path.join(ROOT, "oracle")
+    _run(["make", "-s", "-C", odir, "libsiq_oracle.so"], verbose)
+    if os.path.isdir("/root/reference/src"):
+        _run(["make", "-s", "-C", odir, "ref"], verbose)
+
+
+def build_all(verbose: bool = False) -> None:
+    build_oracle(verbose)
+    build_backend(verbose)
+    build_hip(verbose)
+
+
+if __name__ == "__main__":
+    build_all(verbose="-v" in sys.argv)
+    print("built:", HIP_SO)

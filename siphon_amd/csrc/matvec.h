@@ -1,0 +1,364 @@
+// Batch-1 / small-M quantized matvec on gfx950 over the planar layout of
+// formats.h.
+//
+// One workgroup = 4 wavefronts. Each wave owns row tiles of R rows; lane
+// (r, g) streams units g, g+G, g+2G, ... of row r, so every load instruction
+// of a wave reads one contiguous 64 * P byte span of a plane (coalesced
+// 16-byte loads for the quant planes). Weight data arrives in batches of
+// kBatch steps, double buffered: while one batch is decoded the next one is
+// in flight, and the first batch is requested before the prologue so its
+// HBM latency overlaps the activation quantization.
+//
+// Prologue: the workgroup converts the f32 activation column(s) into the
+// weight type's pair format directly into LDS with the bit-exact quantizers
+// of quant.h (or copies an already quantized column), so no separate
+// quantization launch is needed.
+//
+// Decode and dot products are in unit.h: quants become 8 dwords of int8 and
+// meet the activation bytes (read from LDS, broadcast across the R rows of
+// the tile) in v_dot4_i32_i8; integer sums are exact and each unit's float
+// epilogue applies the block scales. The G partial sums of a row are
+// combined with lane shuffles in a fixed order, so results are deterministic
+// and need no atomics.
+//
+// Per-unit arithmetic restates the reference dots (reference
+// src/kernels.c:197-523, src/kernels_avx2.c:150-590):
+//   Q4_0/Q5_0/Q8_0: d_w*d_x*sum(q*x), with the -8/-16 bias folded as
+//                   sum(u*x) - bias*sum(x)
+//   Q2_K/Q4_K/Q5_K: d*d_x*sum_j sc_j*sum(q*x) - dmin*d_x*sum_j m_j*bsum_j
+//   Q3_K/Q6_K:      d*d_x*sum_g sc_g*(sum(u*x) - bias*bsum_g)
+//   F16:            sum f16(w)*f16(x) with f32 accumulation (v_dot2)
+#pragma once
+
+#include "formats.h"
+#include "quant.h"
+#include "unit.h"
+
+namespace sihip {
+
+constexpr int kWaves = 4;             // wavefronts per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxCols = 8;           // activation columns per launch
+#ifndef SIHIP_BATCH
+#define SIHIP_BATCH 4
+#endif
+constexpr int kBatch = SIHIP_BATCH;   // steps per weight batch
+
+// LDS bytes of one activation column in pair format.
+__host__ __device__ inline int64_t lds_col_bytes(uint32_t pair, int64_t n_in) {
+    if (pair == T_Q8_K) return n_in + (n_in / 256) * (4 + 32);
+    if (pair == T_Q8_0) return n_in + (n_in / 32) * 8;
+    return n_in * 2;  // F16
+}
+
+struct MVArgs {
+    const uint8_t *w;     // plane base
+    Layout L;
+    const float *x;       // f32 activations, column c at x + c * ldx (or null)
+    const uint8_t *xq;    // pair-format activations, column c at xq + c * ldxq
+    int64_t ldx, ldxq, ldy;
+    float *y;             // outputs, column c at y + c * ldy
+    int64_t n_out;        // rows to compute (<= L.n_out)
+    int nc;               // activation columns staged (== the kernel's NC)
+    int64_t col_bytes;    // LDS bytes per column
+};
+
+// ---- prologue: activations -> LDS ----------------------------------------
+//
+// Q8_K from f32 is split in two so the caller can issue its first weight
+// batch in between, from wave-uniform control flow: stage_q8k_first loads
+// the x values of the first pass (memory counters drain in order, so loads
+// issued before these would have to complete before the activations could be
+// used), stage_q8k_finish quantizes them and stages the remaining passes.
+
+struct XFirst {
+    float4 t[4];
+};
+
+// 16 lanes quantize one block: thread tid owns block (tid >> 4) of the pass,
+// elements 16 * (tid & 15) .. +15 of it.
+__device__ inline void stage_q8k_first(const MVArgs &a, XFirst &xf) {
+    const int tid = threadIdx.x;
+    const int64_t nb = a.L.n_in / 256;
+    const int64_t b = tid >> 4;
+    if (a.x && b < nb) {
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + b * 256 + (tid & 15) * 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) xf.t[i] = src[i];
+    }
+}
+
+__device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int lane16,
+                                       const float4 t4[4]) {
+    const int64_t nb = n / 256;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[4 * i] = t4[i].x; v[4 * i + 1] = t4[i].y; v[4 * i + 2] = t4[i].z; v[4 * i + 3] = t4[i].w;
+    }
+    const Q8KRow r = q8k_block_row16(v, lane16);
+    reinterpret_cast<uint4 *>(col + b * 256)[lane16] = r.q;
+    reinterpret_cast<int16_t *>(col + n + nb * 4)[b * 16 + lane16] = (int16_t)r.gsum;
+    if (lane16 == 0) reinterpret_cast<float *>(col + n)[b] = r.d;
+}
+
+template <uint32_t PAIR>
+__device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XFirst &xf) {
+    const int tid = threadIdx.x;
+    const int64_t n = a.L.n_in;
+    for (int c = 0; c < a.nc; c++) {
+        uint8_t *col = lds + c * a.col_bytes;
+        if constexpr (PAIR == T_Q8_K) {
+            const int64_t nb = n / 256;
+            float *dcol = reinterpret_cast<float *>(col + n);
+            int16_t *bcol = reinterpret_cast<int16_t *>(col + n + nb * 4);
+            if (a.x) {
+                const float *xc = a.x + c * a.ldx;
+                const int lane16 = tid & 15;
+                for (int64_t b = tid >> 4; b < nb; b += kThreads / 16) {
+                    if (c == 0 && b == (tid >> 4)) {
+                        q8k_stage_block(col, n, b, lane16, xf.t);  // loaded up front
+                        continue;
+                    }
+                    const float4 *src = reinterpret_cast<const float4 *>(xc + b * 256 + lane16 * 16);
+                    float4 t4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) t4[i] = src[i];
+                    q8k_stage_block(col, n, b, lane16, t4);
+                }
+            } else {
+                const uint8_t *src = a.xq + c * a.ldxq;
+                for (int64_t i = tid; i < nb * 73; i += kThreads) {
+                    const int64_t b = i / 73, w = i % 73;  // 73 dwords per 292-byte block
+                    const uint32_t v = reinterpret_cast<const uint32_t *>(src + b * 292)[w];
+                    if (w == 0) dcol[b] = __uint_as_float(v);
+                    else if (w < 65) reinterpret_cast<uint32_t *>(col + b * 256)[w - 1] = v;
+                    else reinterpret_cast<uint32_t *>(bcol + b * 16)[w - 65] = v;
+                }
+            }
+        } else if constexpr (PAIR == T_Q8_0) {
+            const int64_t nb = n / 32;
+            float *dcol = reinterpret_cast<float *>(col + n);
+            int *scol = reinterpret_cast<int *>(col + n + nb * 4);
+            for (int64_t b = tid; b < nb; b += kThreads) {
+                uint32_t q[8];
+                float d;
+                int sum;
+                if (a.x) {
+                    const Q80Block r = q80_block(a.x + c * a.ldx + b * 32);
+                    for (int t = 0; t < 8; t++) q[t] = r.q[t];
+                    d = r.d;
+                    sum = r.sum;
+                } else {
+                    const uint8_t *src = a.xq + c * a.ldxq + b * 34;
+                    d = f16_bits_to_f32((uint32_t)src[0] | ((uint32_t)src[1] << 8));
+                    sum = 0;
+                    for (int t = 0; t < 8; t++) {
+                        uint32_t w = 0;
+                        for (int k = 0; k < 4; k++) {
+                            const uint8_t byte = src[2 + 4 * t + k];
+                            sum += (int8_t)byte;
+                            w |= (uint32_t)byte << (8 * k);
+                        }
+                        q[t] = w;
+                    }
+                }
+                uint4 *dst = reinterpret_cast<uint4 *>(col + b * 32);
+                dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+                dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+                dcol[b] = d;
+                scol[b] = sum;
+            }
+        } else {  // F16
+            uint16_t *h = reinterpret_cast<uint16_t *>(col);
+            if (a.x) {
+                const float *xc = a.x + c * a.ldx;
+                for (int64_t i = tid; i < n; i += kThreads)
+                    h[i] = __builtin_bit_cast(uint16_t, (_Float16)xc[i]);
+            } else {
+                const uint16_t *src = reinterpret_cast<const uint16_t *>(a.xq + c * a.ldxq);
+                for (int64_t i = tid; i < n; i += kThreads) h[i] = src[i];
+            }
+        }
+    }
+}
+
+// ---- the kernel -------------------------------------------------------------
+//
+// Each wave walks a flat sequence of items (tile, step): tiles wave0,
+// wave0 + nwaves, ... and S steps per tile. All control flow in the loop is
+// wave-uniform (scalar): loads are never predicated per lane. Rows past
+// n_out inside the last tile and the lanes of a clamped final batch read
+// in-bounds records (tile padding is allocated and zero-filled at upload)
+// and their results are discarded. The upload guarantees nunits % G == 0,
+// so every step of a tile is a full step.
+
+struct Item {
+    uint32_t tile, s, rec;  // rec = (tile * S + s) * 64
+};
+
+__device__ inline float dpp_f32(float v, int ctrl) {
+    return __uint_as_float(dpp_u32(__float_as_uint(v), ctrl));
+}
+
+// Sum over the G lanes of a group in the order of reduce_partner (unit.h).
+__device__ inline float group_sum(float v, int G) {
+    if (G > 1) v += dpp_f32(v, kDppXor1);
+    if (G > 2) v += dpp_f32(v, kDppXor2);
+    if (G > 4) v += dpp_f32(v, kDppHalfMirror);
+    if (G > 8) v += dpp_f32(v, kDppMirror);
+    if (G > 16) v += __shfl_xor(v, 16, 64);
+    if (G > 32) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <uint32_t FMT, int NC>
+__global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr uint32_t PAIR = (FMT == T_F16) ? T_F16
+                              : (FMT == T_Q4_0 || FMT == T_Q5_0 || FMT == T_Q8_0) ? T_Q8_0
+                                                                                   : T_Q8_K;
+    const Layout &L = A.L;
+    const int lane = threadIdx.x & 63;
+    const int G = L.G;
+    const int g = lane & (G - 1);
+    const int r = lane >> L.logG;
+    const LaneK K = lane_consts(g & 7);
+    Planes P;
+#pragma unroll
+    for (int p = 0; p < 4; p++) P.p[p] = A.w + L.plane_off[p];
+    const uint32_t S = (uint32_t)L.S;
+    const uint32_t n_in = (uint32_t)L.n_in;
+    const uint32_t col_bytes = (uint32_t)A.col_bytes;
+    const uint32_t ntiles = (uint32_t)((A.n_out + L.R - 1) / L.R);
+    const uint32_t nwaves = gridDim.x * kWaves;
+    // wave-uniform: keep the whole item walk in scalar registers
+    const uint32_t wave0 =
+        blockIdx.x * kWaves + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t my_tiles = wave0 < ntiles ? (ntiles - 1 - wave0) / nwaves + 1 : 0;
+    const uint32_t total = my_tiles * S;  // items of this wave
+
+    auto step = [&](Item &it) {
+        if (++it.s == S) {
+            it.s = 0;
+            it.tile += nwaves;
+            it.rec = it.tile * S * 64u;
+        } else {
+            it.rec += 64u;
+        }
+    };
+    // issue the loads of kBatch items starting at item k; items past the end
+    // repeat the last item (in bounds, results unused)
+    Item in_it{wave0, 0, wave0 * S * 64u};
+    uint32_t issued = 0;  // items whose loads have been issued
+    auto issue = [&](Raw *buf) {
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) {
+            load_unit<FMT>(P, in_it.rec + (uint32_t)lane, (in_it.rec >> 3) + (uint32_t)(lane >> 3), K,
+                           buf[i]);
+            if (issued < total) {
+                issued++;
+                if (issued < total) step(in_it);
+            }
+        }
+    };
+    Item c_it{wave0, 0, wave0 * S * 64u};
+    uint32_t c_k = 0;
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) acc[c] = 0.0f;
+    auto consume = [&](const Raw *buf) {
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) {
+            if (c_k < total) {
+                const uint32_t u = c_it.s * (uint32_t)G + (uint32_t)g;
+                compute_unit<FMT, NC>(lds, col_bytes, n_in, u, K, buf[i], acc);
+                if (c_it.s == S - 1) {
+                    const int64_t row = (int64_t)c_it.tile * L.R + r;
+#pragma unroll
+                    for (int c = 0; c < NC; c++) {
+                        const float v = group_sum(acc[c], G);
+                        if (g == 0 && row < A.n_out) A.y[c * A.ldy + row] = v;
+                        acc[c] = 0.0f;
+                    }
+                }
+                step(c_it);
+                c_k++;
+            }
+        }
+    };
+
+    Raw bufA[kBatch], bufB[kBatch];
+    XFirst xf;
+    if constexpr (PAIR == T_Q8_K) stage_q8k_first(A, xf);
+    if (total) issue(bufA);
+    stage_activations<PAIR>(A, lds, xf);
+    if (total) issue(bufB);
+    __syncthreads();
+
+    // Two batches in flight: each buffer is refilled right after it has been
+    // decoded, so a refill never overwrites registers with a load pending and
+    // every wait covers one buffer only. Refills are unconditional (past the
+    // end they repeat the last item), keeping the loads straight-line code.
+    while (c_k < total) {
+        consume(bufA);
+        issue(bufA);
+        if (c_k >= total) break;
+        consume(bufB);
+        issue(bufB);
+    }
+}
+
+// ---- standalone quantizers (global output in the reference block layouts) --
+
+// 16 lanes per 256-block, the same code path as the matvec prologue.
+__global__ __launch_bounds__(kThreads) void quantize_q8K_kernel(const float *x, uint8_t *out,
+                                                                int64_t nb) {
+    const int lane16 = threadIdx.x & 15;
+    const int64_t b = (int64_t)blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+    if (b >= nb) return;  // whole 16-lane rows leave together
+    const float4 *src = reinterpret_cast<const float4 *>(x + b * 256 + lane16 * 16);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 t = src[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+    const Q8KRow r = q8k_block_row16(v, lane16);
+    uint8_t *o = out + b * 292;
+    uint32_t *qd = reinterpret_cast<uint32_t *>(o + 4 + lane16 * 16);
+    qd[0] = r.q.x; qd[1] = r.q.y; qd[2] = r.q.z; qd[3] = r.q.w;
+    reinterpret_cast<int16_t *>(o + 260)[lane16] = (int16_t)r.gsum;
+    if (lane16 == 0) *reinterpret_cast<float *>(o) = r.d;
+}
+
+__global__ __launch_bounds__(kThreads) void quantize_q80_kernel(const float *x, uint8_t *out,
+                                                                int64_t nb) {
+    const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (b >= nb) return;
+    const Q80Block r = q80_block(x + b * 32);
+    uint8_t *o = out + b * 34;
+    o[0] = (uint8_t)(r.dbits & 0xff);
+    o[1] = (uint8_t)(r.dbits >> 8);
+    for (int t = 0; t < 8; t++)
+        for (int k = 0; k < 4; k++) o[2 + 4 * t + k] = (uint8_t)(r.q[t] >> (8 * k));
+}
+
+__global__ __launch_bounds__(kThreads) void convert_f16_kernel(const float *x, uint16_t *out,
+                                                               int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) out[i] = __builtin_bit_cast(uint16_t, (_Float16)x[i]);
+}
+
+// ---- repack: GGUF blocks -> planes ------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void repack_kernel(Layout L, const uint8_t *src,
+                                                          uint8_t *dst, int64_t row_bytes,
+                                                          int64_t recs_per_row, int64_t rec_bytes) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= L.n_out * recs_per_row) return;
+    const int64_t row = i / recs_per_row, k = i % recs_per_row;
+    repack_block(L, dst, src + row * row_bytes + k * rec_bytes, row, k);
+}
+
+}  // namespace sihip

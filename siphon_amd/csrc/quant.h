@@ -1,0 +1,191 @@
+// Bit-exact activation quantizers on gfx950.
+//
+// The library is compiled with -ffp-contract=off and every float step below
+// is one IEEE operation with round-to-nearest-even, so quants, scales and
+// group sums equal the reference's bit for bit:
+//   Q8_K: reference src/kernels.c:561-595 (+ nearest_int, 528-533)
+//   Q8_0: reference src/kernels_avx2.c:594-645 (the SIMD quantizer x86
+//         production dispatches to; reference kernels.c:536-541)
+//   F16 : reference src/backend.c:19-27 via kernels.c:124-176
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sihip {
+
+// ---- IEEE binary16 ------------------------------------------------------
+
+__device__ inline float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// RNE narrowing done in integer arithmetic so the result does not depend on
+// the hardware's fp16 denormal mode. Used for the per-block Q8_0 scale.
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x7f800000u) {
+        if (a == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+        uint32_t m = (a >> 13) & 0x3ffu;
+        if (m == 0) m = 1;
+        return (uint16_t)(sign | 0x7c00u | 0x200u | m);
+    }
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+    if (a < 0x38800000u) {
+        const int e = (int)(a >> 23) - 127;
+        if (e < -25) return (uint16_t)sign;
+        const uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+        const int shift = -(e + 1);
+        uint32_t m = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (m & 1u))) m++;
+        return (uint16_t)(sign | m);
+    }
+    uint32_t r = a - 0x38000000u;
+    r += 0xfffu + ((r >> 13) & 1u);
+    return (uint16_t)(sign | (r >> 13));
+}
+
+// ---- Q8_K -----------------------------------------------------------------
+
+__device__ inline int nearest_int_magic(float v) {
+    const float t = __fadd_rn(v, 12582912.0f);
+    return (int)(__float_as_uint(t) & 0x7fffffu) - 0x400000;
+}
+
+// DPP row permutations (within 16-lane rows): quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror. Applied in this order they
+// pair every lane of a 16-lane row with lanes of every other quarter, so a
+// commutative, associative combine ends with the row total in all 16 lanes.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ inline uint32_t dpp_u32(uint32_t v, int ctrl) {
+    switch (ctrl) {
+        case kDppXor1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppXor1, 0xf, 0xf, false);
+        case kDppXor2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppXor2, 0xf, 0xf, false);
+        case kDppHalfMirror:
+            return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppHalfMirror, 0xf, 0xf, false);
+        default: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppMirror, 0xf, 0xf, false);
+    }
+}
+
+struct Q8KRow {
+    uint4 q;     // quants of this lane's 16 elements
+    float d;     // block scale
+    int gsum;    // sum of those 16 quants (= the block's bsums[lane16])
+};
+
+// 16 lanes quantize one 256-element block; lane16 holds elements
+// 16*lane16 .. 16*lane16+15 (x16). The abs-max key is (|x| bits, 255 - index,
+// sign): its maximum is the largest |x| at its first occurrence, exactly the
+// reference's "if (ax > amax)" scan; |x| of a non-negative float orders like
+// its bit pattern, and NaN never enters (it is never > amax).
+__device__ inline Q8KRow q8k_block_row16(const float x16[16], int lane16) {
+    uint32_t abits = 0, key = 0;
+    for (int k = 0; k < 16; k++) {
+        const float a = fabsf(x16[k]);
+        if (a > __uint_as_float(abits)) {
+            abits = __float_as_uint(a);
+            key = ((uint32_t)(255 - (16 * lane16 + k)) << 1) | (__float_as_uint(x16[k]) >> 31);
+        }
+    }
+    const int ctrls[4] = {kDppXor1, kDppXor2, kDppHalfMirror, kDppMirror};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t a2 = dpp_u32(abits, ctrls[i]);
+        const uint32_t k2 = dpp_u32(key, ctrls[i]);
+        if (a2 > abits || (a2 == abits && k2 > key)) { abits = a2; key = k2; }
+    }
+    Q8KRow r;
+    if (abits == 0) {
+        r.q = make_uint4(0, 0, 0, 0);
+        r.d = 0.0f;
+        r.gsum = 0;
+        return r;
+    }
+    const float vmax = __uint_as_float(abits | ((key & 1u) << 31));
+    const float iscale = -127.0f / vmax;
+    uint32_t w[4] = {0, 0, 0, 0};
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        int v = nearest_int_magic(__fmul_rn(iscale, x16[k]));
+        v = v < 127 ? v : 127;
+        s += (int)(int8_t)(uint8_t)(v & 0xff);
+        w[k >> 2] |= (uint32_t)(v & 0xff) << (8 * (k & 3));
+    }
+    r.q = make_uint4(w[0], w[1], w[2], w[3]);
+    r.d = 1.0f / iscale;
+    r.gsum = s;
+    return r;
+}
+
+// ---- Q8_0 -----------------------------------------------------------------
+
+__device__ inline float vmaxsel(float a, float b) { return a > b ? a : b; }
+
+// x86 cvtps_epi32 of an already rounded value: NaN or out of range gives
+// INT32_MIN, which the saturating packs then turn into -128.
+__device__ inline int cvt_i32_indef(float r) {
+    if (!(r >= -2147483648.0f && r < 2147483648.0f)) return (int)0x80000000u;
+    return (int)r;
+}
+
+// One thread quantizes one 32-block. The abs-max follows the SIMD
+// reduction tree (per-lane max over 4 vectors, then 8 -> 4 -> 2 -> 1 with
+// maxps operand order), which only matters for NaN inputs.
+struct Q80Block {
+    uint16_t dbits;
+    float d;          // f32 value of the stored f16 scale
+    int sum;          // sum of the 32 quants
+    uint32_t q[8];    // quants, byte k of q[t] = element 4t+k
+};
+
+__device__ inline Q80Block q80_block(const float *x) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 t = reinterpret_cast<const float4 *>(x)[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+    float lane[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        float m = fabsf(v[k]);
+        m = vmaxsel(m, fabsf(v[8 + k]));
+        m = vmaxsel(m, fabsf(v[16 + k]));
+        m = vmaxsel(m, fabsf(v[24 + k]));
+        lane[k] = m;
+    }
+    float m4[4], m2[2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) m4[k] = vmaxsel(lane[4 + k], lane[k]);
+#pragma unroll
+    for (int k = 0; k < 2; k++) m2[k] = vmaxsel(m4[k], m4[k + 2]);
+    const float mx = vmaxsel(m2[0], m2[1]);
+    Q80Block b;
+    b.dbits = f32_to_f16_bits(mx / 127.0f);
+    b.d = f16_bits_to_f32(b.dbits);
+    const float id = (mx != 0.0f) ? 127.0f / mx : 0.0f;
+    int s = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float r = __builtin_rintf(__fmul_rn(v[4 * t + k], id));
+            int q = cvt_i32_indef(r);
+            q = q > 127 ? 127 : (q < -128 ? -128 : q);
+            s += q;
+            w |= (uint32_t)(q & 0xff) << (8 * k);
+        }
+        b.q[t] = w;
+    }
+    b.sum = s;
+    return b;
+}
+
+}  // namespace sihip

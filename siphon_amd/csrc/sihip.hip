@@ -1,0 +1,484 @@
+// libsiphon_hip.so: C-ABI implementation (declarations in include/sihip.h).
+//
+// Owns device copies of the weights in the planar layout of formats.h and
+// launches the gfx950 kernels of matvec.h. Every entry point validates its
+// arguments on the host before any launch, so a kernel never sees a shape
+// its grid and LDS sizing do not cover.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/sihip.h"
+#include "formats.h"
+#include "matvec.h"
+#include "quant.h"
+
+using namespace sihip;
+
+struct sihip_ctx {
+    int device;
+    int n_cu;
+    size_t lds_limit;
+    hipStream_t stream;  // for host-pointer entry points
+    char err[512];
+    void *d_in = nullptr;
+    size_t d_in_cap = 0;
+    void *d_out = nullptr;
+    size_t d_out_cap = 0;
+    void *d_aux = nullptr;
+    size_t d_aux_cap = 0;
+};
+
+struct sihip_weight {
+    Layout L;
+    uint8_t *dev;
+};
+
+static char g_init_err[512];
+
+static int set_err(sihip_ctx *ctx, int code, const char *fmt, ...) {
+    char *dst = ctx ? ctx->err : g_init_err;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(dst, 512, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define HIP_OK(ctx, call)                                                              \
+    do {                                                                               \
+        hipError_t e_ = (call);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return set_err((ctx), SIHIP_EDEVICE, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+static int ensure(sihip_ctx *ctx, void **buf, size_t *cap, size_t bytes) {
+    if (*cap >= bytes) return SIHIP_OK;
+    if (*buf) HIP_OK(ctx, hipFree(*buf));
+    *buf = nullptr;
+    *cap = 0;
+    if (hipMalloc(buf, bytes) != hipSuccess) {
+        *buf = nullptr;
+        return set_err(ctx, SIHIP_ENOMEM, "device allocation of %zu bytes failed", bytes);
+    }
+    *cap = bytes;
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_abi_version(void) { return SIHIP_ABI_VERSION; }
+
+extern "C" int sihip_init(int device, sihip_ctx **out) {
+    if (!out) return set_err(nullptr, SIHIP_EINVAL, "sihip_init: out is NULL");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: no HIP device");
+    if (device < 0 || device >= n)
+        return set_err(nullptr, SIHIP_EINVAL, "sihip_init: device %d of %d", device, n);
+    if (hipSetDevice(device) != hipSuccess)
+        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: hipSetDevice(%d) failed", device);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: hipGetDeviceProperties failed");
+    sihip_ctx *c = new sihip_ctx();
+    c->device = device;
+    c->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    c->lds_limit = prop.sharedMemPerBlock;
+    c->err[0] = 0;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: stream creation failed");
+    }
+    *out = c;
+    return SIHIP_OK;
+}
+
+extern "C" void sihip_shutdown(sihip_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->d_in) (void)hipFree(ctx->d_in);
+    if (ctx->d_out) (void)hipFree(ctx->d_out);
+    if (ctx->d_aux) (void)hipFree(ctx->d_aux);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+extern "C" const char *sihip_last_error(const sihip_ctx *ctx) {
+    return ctx ? ctx->err : g_init_err;
+}
+
+// ---- weights ------------------------------------------------------------------
+
+static int wgs_per_cu() {
+    const char *e = getenv("SIHIP_WG_PER_CU");
+    const int v = e ? atoi(e) : 0;
+    return v > 0 ? v : 8;
+}
+
+static int wave_target() {
+    const char *e = getenv("SIHIP_WAVE_TARGET");
+    const int v = e ? atoi(e) : 0;
+    return v > 0 ? v : 2048;
+}
+
+// Unit-columns per wave tile: the smallest power of two that divides the row's
+// unit count and still gives about wave_target() row tiles, so that the whole
+// chip is busy while each lane keeps as many units (and as few shuffle steps)
+// as possible.
+static int choose_G(uint32_t type, int64_t n_out, int64_t nunits) {
+    if (const char *f = getenv("SIHIP_TILE_COLS")) {
+        const int G = atoi(f);
+        if (G >= 1 && G <= 64 && !(G & (G - 1)) && (!is_kquant(type) || G % 8 == 0) &&
+            nunits % G == 0)
+            return G;
+    }
+    const int64_t target = wave_target();
+    int best = -1;
+    for (int G = is_kquant(type) ? 8 : 1; G <= 64; G *= 2) {
+        if (nunits % G) continue;
+        best = G;
+        const int64_t tiles = (n_out + 64 / G - 1) / (64 / G);
+        if (tiles >= target) break;
+    }
+    return best;  // G = 1 (8 for K-quants) always divides nunits
+}
+
+extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out,
+                                   uint64_t n_in, const void *host_blocks, uint64_t bytes,
+                                   sihip_weight **out) {
+    if (!ctx || !out || !host_blocks) return set_err(ctx, SIHIP_EINVAL, "weight_upload: NULL argument");
+    uint32_t be, bb;
+    if (!geometry(type, &be, &bb) || type == T_Q8_K)
+        return set_err(ctx, SIHIP_ENOTSUP, "weight_upload: unsupported ggml type %u", type);
+    if (n_out == 0 || n_in == 0 || n_in % be != 0 || n_in % 32 != 0)
+        return set_err(ctx, SIHIP_EINVAL,
+                       "weight_upload: n_in %llu is not a multiple of the block size %u",
+                       (unsigned long long)n_in, be);
+    if (n_in > (1ull << 24) || n_out > (1ull << 31))
+        return set_err(ctx, SIHIP_ERANGE, "weight_upload: shape too large");
+    const uint64_t row_bytes = n_in / be * bb;
+    if (bytes != row_bytes * n_out)
+        return set_err(ctx, SIHIP_EINVAL, "weight_upload: %llu bytes given, %llu expected",
+                       (unsigned long long)bytes, (unsigned long long)(row_bytes * n_out));
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const int64_t nunits = (int64_t)n_in / 32;
+    Layout L;
+    if (!make_layout(type, (int64_t)n_out, (int64_t)n_in, choose_G(type, n_out, nunits), &L))
+        return set_err(ctx, SIHIP_EINVAL, "weight_upload: no layout for this shape");
+    uint8_t *dev = nullptr;
+    if (hipMalloc((void **)&dev, (size_t)L.total_bytes) != hipSuccess)
+        return set_err(ctx, SIHIP_ENOMEM, "weight_upload: %lld device bytes", (long long)L.total_bytes);
+    uint8_t *raw = nullptr;
+    if (hipMalloc((void **)&raw, (size_t)bytes) != hipSuccess) {
+        (void)hipFree(dev);
+        return set_err(ctx, SIHIP_ENOMEM, "weight_upload: %llu staging bytes",
+                       (unsigned long long)bytes);
+    }
+    int rc = SIHIP_OK;
+    const int64_t recs = (type == T_F16) ? nunits : (int64_t)(n_in / be);
+    const int64_t rec_bytes = (type == T_F16) ? 64 : bb;
+    const int64_t total = (int64_t)n_out * recs;
+    hipError_t e = hipMemsetAsync(dev, 0, (size_t)L.total_bytes, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(raw, host_blocks, (size_t)bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(repack_kernel, dim3((unsigned)((total + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, ctx->stream, L, raw, dev, (int64_t)row_bytes, recs,
+                           rec_bytes);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(raw);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return set_err(ctx, SIHIP_EDEVICE, "weight_upload: %s", hipGetErrorString(e));
+    }
+    sihip_weight *w = new sihip_weight();
+    w->L = L;
+    w->dev = dev;
+    *out = w;
+    return rc;
+}
+
+extern "C" int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w) {
+    if (!w) return SIHIP_OK;
+    if (ctx) HIP_OK(ctx, hipSetDevice(ctx->device));
+    (void)hipFree(w->dev);
+    delete w;
+    return SIHIP_OK;
+}
+
+extern "C" uint64_t sihip_weight_device_bytes(const sihip_weight *w) {
+    return w ? (uint64_t)w->L.total_bytes : 0;
+}
+
+extern "C" int sihip_weight_tile_cols(const sihip_weight *w) { return w ? w->L.G : 0; }
+
+// ---- launches -----------------------------------------------------------------
+
+template <uint32_t FMT, int NC>
+static hipError_t launch_nc(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((matvec_kernel<FMT, NC>), dim3(grid), dim3(kThreads), lds, st, A);
+    return hipGetLastError();
+}
+
+template <uint32_t FMT>
+static hipError_t launch_fmt(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
+    switch (A.nc) {
+        case 1: return launch_nc<FMT, 1>(A, grid, lds, st);
+        case 2: return launch_nc<FMT, 2>(A, grid, lds, st);
+        case 4: return launch_nc<FMT, 4>(A, grid, lds, st);
+        case 8: return launch_nc<FMT, 8>(A, grid, lds, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+static hipError_t launch_any(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
+    switch (A.L.type) {
+        case T_F16:  return launch_fmt<T_F16>(A, grid, lds, st);
+        case T_Q4_0: return launch_fmt<T_Q4_0>(A, grid, lds, st);
+        case T_Q5_0: return launch_fmt<T_Q5_0>(A, grid, lds, st);
+        case T_Q8_0: return launch_fmt<T_Q8_0>(A, grid, lds, st);
+        case T_Q2_K: return launch_fmt<T_Q2_K>(A, grid, lds, st);
+        case T_Q3_K: return launch_fmt<T_Q3_K>(A, grid, lds, st);
+        case T_Q4_K: return launch_fmt<T_Q4_K>(A, grid, lds, st);
+        case T_Q5_K: return launch_fmt<T_Q5_K>(A, grid, lds, st);
+        case T_Q6_K: return launch_fmt<T_Q6_K>(A, grid, lds, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+static int64_t col_bytes_aligned(uint32_t pair, int64_t n_in) {
+    return (lds_col_bytes(pair, n_in) + 15) & ~(int64_t)15;
+}
+
+// Largest supported column count (1, 2, 4 or 8) whose LDS fits.
+static int max_cols(const sihip_ctx *ctx, uint32_t pair, int64_t n_in) {
+    const int64_t cb = col_bytes_aligned(pair, n_in);
+    for (int nc = kMaxCols; nc >= 1; nc >>= 1)
+        if ((size_t)(cb * nc) <= ctx->lds_limit) return nc;
+    return 0;
+}
+
+// Run the matvec for columns [0, M) of x (f32, ldx) or xq (pair format,
+// ldxq) into y (ldy), splitting M into launches of 8/4/2/1 columns.
+static int run_matvec(sihip_ctx *ctx, const sihip_weight *w, const float *x, int64_t ldx,
+                      const uint8_t *xq, int64_t ldxq, int64_t M, float *y, int64_t ldy,
+                      int64_t n_out, hipStream_t st) {
+    const Layout &L = w->L;
+    const uint32_t pair = pair_of(L.type);
+    const int ncmax = max_cols(ctx, pair, L.n_in);
+    if (ncmax == 0)
+        return set_err(ctx, SIHIP_ERANGE, "activation row of %lld does not fit in LDS",
+                       (long long)L.n_in);
+    const int64_t cb = col_bytes_aligned(pair, L.n_in);
+    const int64_t R = L.R;
+    const int64_t ntiles = (n_out + R - 1) / R;
+    int64_t wgs = (ntiles + kWaves - 1) / kWaves;
+    const int64_t wg_cap = (int64_t)ctx->n_cu * wgs_per_cu();
+    if (wgs > wg_cap) wgs = wg_cap;
+    int64_t m = 0;
+    while (m < M) {
+        int nc = ncmax;
+        while (nc > 1 && m + nc > M) nc >>= 1;
+        MVArgs A;
+        A.w = w->dev;
+        A.L = L;
+        A.x = x ? x + m * ldx : nullptr;
+        A.xq = xq ? xq + m * ldxq : nullptr;
+        A.ldx = ldx;
+        A.ldxq = ldxq;
+        A.ldy = ldy;
+        A.y = y + m * ldy;
+        A.n_out = n_out;
+        A.nc = nc;
+        A.col_bytes = cb;
+        const hipError_t e = launch_any(A, (int)wgs, (size_t)(cb * nc), st);
+        if (e != hipSuccess)
+            return set_err(ctx, SIHIP_EDEVICE, "matvec launch: %s", hipGetErrorString(e));
+        m += nc;
+    }
+    return SIHIP_OK;
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int sihip_gemv_dev(sihip_ctx *ctx, const sihip_weight *w, const float *x, float *y,
+                              int64_t n_out, void *stream) {
+    if (!ctx || !w || !x || !y) return set_err(ctx, SIHIP_EINVAL, "gemv_dev: NULL argument");
+    if (n_out <= 0 || n_out > w->L.n_out)
+        return set_err(ctx, SIHIP_EINVAL, "gemv_dev: n_out %lld outside 1..%lld",
+                       (long long)n_out, (long long)w->L.n_out);
+    if (!aligned16(x)) return set_err(ctx, SIHIP_EINVAL, "gemv_dev: x must be 16-byte aligned");
+    return run_matvec(ctx, w, x, w->L.n_in, nullptr, 0, 1, y, w->L.n_out, n_out,
+                      (hipStream_t)stream);
+}
+
+extern "C" int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64_t M,
+                              float *Y, void *stream) {
+    if (!ctx || !w || !X || !Y) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: NULL argument");
+    if (M <= 0) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: M must be positive");
+    if (!aligned16(X)) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: X must be 16-byte aligned");
+    return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out,
+                      (hipStream_t)stream);
+}
+
+extern "C" int sihip_gemv_multi_dev(sihip_ctx *ctx, int count, const sihip_weight *const *w,
+                                    const float *x, float *const *y, void *stream) {
+    if (!ctx || !w || !x || !y || count < 1 || count > 4)
+        return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: bad arguments");
+    for (int i = 0; i < count; i++) {
+        if (!w[i] || !y[i]) return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: NULL weight/output");
+        if (w[i]->L.n_in != w[0]->L.n_in)
+            return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: n_in differs between weights");
+    }
+    for (int i = 0; i < count; i++) {
+        const int rc = sihip_gemv_dev(ctx, w[i], x, y[i], w[i]->L.n_out, stream);
+        if (rc) return rc;
+    }
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_gemv(sihip_ctx *ctx, const sihip_weight *w, const float *x, float *y,
+                          int64_t n_out) {
+    if (!ctx || !w || !x || !y) return set_err(ctx, SIHIP_EINVAL, "gemv: NULL argument");
+    if (n_out <= 0 || n_out > w->L.n_out)
+        return set_err(ctx, SIHIP_EINVAL, "gemv: n_out %lld outside 1..%lld", (long long)n_out,
+                       (long long)w->L.n_out);
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const size_t xb = (size_t)w->L.n_in * 4, yb = (size_t)n_out * 4;
+    int rc = ensure(ctx, &ctx->d_in, &ctx->d_in_cap, xb);
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, yb);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    rc = run_matvec(ctx, w, (const float *)ctx->d_in, w->L.n_in, nullptr, 0, 1,
+                    (float *)ctx->d_out, n_out, n_out, ctx->stream);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(y, ctx->d_out, yb, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64_t M,
+                          float *Y) {
+    if (!ctx || !w || !X || !Y) return set_err(ctx, SIHIP_EINVAL, "gemm: NULL argument");
+    if (M <= 0) return set_err(ctx, SIHIP_EINVAL, "gemm: M must be positive");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const size_t xb = (size_t)M * (size_t)w->L.n_in * 4;
+    const size_t yb = (size_t)M * (size_t)w->L.n_out * 4;
+    int rc = ensure(ctx, &ctx->d_in, &ctx->d_in_cap, xb);
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, yb);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, X, xb, hipMemcpyHostToDevice, ctx->stream));
+    rc = run_matvec(ctx, w, (const float *)ctx->d_in, w->L.n_in, nullptr, 0, M,
+                    (float *)ctx->d_out, w->L.n_out, w->L.n_out, ctx->stream);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(Y, ctx->d_out, yb, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
+// ---- quantizers and per-row dots (parity-test entry points) ---------------------
+
+extern "C" int sihip_quantize_q8_K(sihip_ctx *ctx, const float *x, void *out, int64_t n) {
+    if (!ctx || !x || !out) return set_err(ctx, SIHIP_EINVAL, "quantize_q8_K: NULL argument");
+    if (n <= 0 || n % 256) return set_err(ctx, SIHIP_EINVAL, "quantize_q8_K: n %% 256 != 0");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const int64_t nb = n / 256;
+    int rc = ensure(ctx, &ctx->d_in, &ctx->d_in_cap, (size_t)n * 4);
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, (size_t)nb * 292);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, x, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    hipLaunchKernelGGL(quantize_q8K_kernel,
+                       dim3((unsigned)((nb + kThreads / 16 - 1) / (kThreads / 16))),
+                       dim3(kThreads), 0, ctx->stream, (const float *)ctx->d_in,
+                       (uint8_t *)ctx->d_out, nb);
+    HIP_OK(ctx, hipGetLastError());
+    HIP_OK(ctx, hipMemcpyAsync(out, ctx->d_out, (size_t)nb * 292, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_quantize_q8_0(sihip_ctx *ctx, const float *x, void *out, int64_t n) {
+    if (!ctx || !x || !out) return set_err(ctx, SIHIP_EINVAL, "quantize_q8_0: NULL argument");
+    if (n <= 0 || n % 32) return set_err(ctx, SIHIP_EINVAL, "quantize_q8_0: n %% 32 != 0");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const int64_t nb = n / 32;
+    int rc = ensure(ctx, &ctx->d_in, &ctx->d_in_cap, (size_t)n * 4);
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, (size_t)nb * 34);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, x, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    hipLaunchKernelGGL(quantize_q80_kernel, dim3((unsigned)((nb + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, ctx->stream, (const float *)ctx->d_in,
+                       (uint8_t *)ctx->d_out, nb);
+    HIP_OK(ctx, hipGetLastError());
+    HIP_OK(ctx, hipMemcpyAsync(out, ctx->d_out, (size_t)nb * 34, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_convert_f16(sihip_ctx *ctx, const float *x, void *out, int64_t n) {
+    if (!ctx || !x || !out) return set_err(ctx, SIHIP_EINVAL, "convert_f16: NULL argument");
+    if (n <= 0) return set_err(ctx, SIHIP_EINVAL, "convert_f16: n must be positive");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    int rc = ensure(ctx, &ctx->d_in, &ctx->d_in_cap, (size_t)n * 4);
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, (size_t)n * 2);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, x, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    hipLaunchKernelGGL(convert_f16_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, ctx->stream, (const float *)ctx->d_in,
+                       (uint16_t *)ctx->d_out, n);
+    HIP_OK(ctx, hipGetLastError());
+    HIP_OK(ctx, hipMemcpyAsync(out, ctx->d_out, (size_t)n * 2, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_gemv_pair(sihip_ctx *ctx, uint32_t wtype, int64_t n_rows, int64_t n_in,
+                               const void *rows, const void *xq, float *y) {
+    if (!ctx || !rows || !xq || !y) return set_err(ctx, SIHIP_EINVAL, "gemv_pair: NULL argument");
+    uint32_t be, bb;
+    if (!geometry(wtype, &be, &bb) || wtype == T_Q8_K)
+        return set_err(ctx, SIHIP_ENOTSUP, "gemv_pair: unsupported type %u", wtype);
+    if (n_rows <= 0 || n_in <= 0 || n_in % be || n_in % 32)
+        return set_err(ctx, SIHIP_EINVAL, "gemv_pair: bad shape");
+    const uint32_t pair = pair_of(wtype);
+    uint32_t pe, pb;
+    geometry(pair, &pe, &pb);
+    const size_t xq_bytes = (size_t)(n_in / pe) * pb;
+    sihip_weight *w = nullptr;
+    int rc = sihip_weight_upload(ctx, wtype, (uint64_t)n_rows, (uint64_t)n_in, rows,
+                                 (uint64_t)(n_in / be * bb) * (uint64_t)n_rows, &w);
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_aux, &ctx->d_aux_cap, xq_bytes);
+    if (!rc) rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, (size_t)n_rows * 4);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(ctx->d_aux, xq, xq_bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) rc = set_err(ctx, SIHIP_EDEVICE, "gemv_pair: %s", hipGetErrorString(e));
+    }
+    if (!rc)
+        rc = run_matvec(ctx, w, nullptr, 0, (const uint8_t *)ctx->d_aux, (int64_t)xq_bytes, 1,
+                        (float *)ctx->d_out, n_rows, n_rows, ctx->stream);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(y, ctx->d_out, (size_t)n_rows * 4, hipMemcpyDeviceToHost,
+                                      ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) rc = set_err(ctx, SIHIP_EDEVICE, "gemv_pair: %s", hipGetErrorString(e));
+    }
+    sihip_weight_free(ctx, w);
+    return rc;
+}
+
+extern "C" int sihip_vec_dot(sihip_ctx *ctx, uint32_t wtype, int n, float *s, const void *x,
+                             const void *y) {
+    if (!s) return set_err(ctx, SIHIP_EINVAL, "vec_dot: NULL output");
+    return sihip_gemv_pair(ctx, wtype, 1, n, x, y, s);
+}
