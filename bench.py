@@ -1,0 +1,270 @@
+"""Benchmark of the quantized matvec path on one MI355X.
+
+Metric: "quant matvec weight-GB/s (% HBM peak) at 8B shapes;
+M=512 GEMM int8 TOPS".
+
+One step = one decode pass over the Llama-3-8B Q4_K_M layer set (config 2):
+32 layers x 7 matrices (wq, wk, wo, ffn_gate, ffn_up: Q4_K; wv, ffn_down:
+Q6_K), batch 1, each matvec converting its f32 activation to Q8_K inside the
+kernel, in the reference engine's order (engine.c:317-378). The pass is
+captured in a HIP graph; 4,444,913,664 weight bytes are streamed per pass.
+value = weight bytes / pass time (GB/s). Weights are seeded synthetic GGUF
+blocks (random fields, f16 scales in the configured ranges), activations
+N(0,1); both are resident in HBM before timing starts.
+
+Extra fields: the dominant kernel's roofline (Q4_K matvec, per-launch HIP
+events), the M=512 prefill GEMM (config 3) in TOPS, and the reference's own
+AVX2 gemv (oracle/_ref, through its lane pool) on a bounded sample of the
+same weights on the host cores.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-gemm]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5033.0         # MI355X dense int8 MFMA, TOPS (256 CU x 2.4 GHz x 8192)
+N_LAYERS = 32
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the M=512 GEMM")
+    ap.add_argument("--seed", type=int, default=2026)
+    return ap.parse_args()
+
+
+def build_layers(dev, rng, keep_host_layers):
+    """Upload 32 distinct layers; return device weights and the host bytes of
+    the first `keep_host_layers` layers (for the CPU baseline)."""
+    import siphon_amd as sa
+    from siphon_amd import synth
+    layers, host = [], []
+    for il in range(N_LAYERS):
+        mats = {}
+        hl = {}
+        for (name, wt, n_out, n_in) in synth.LLAMA3_8B_LAYER:
+            d_range = (1e-4, 2e-3) if wt == sa.Q6_K else (1e-4, 4e-3)
+            W = synth.make_weights(wt, n_out, n_in, rng, d_range=d_range)
+            mats[name] = dev.upload(wt, n_out, n_in, W)
+            if il < keep_host_layers:
+                hl[name] = W
+        layers.append(mats)
+        if il < keep_host_layers:
+            host.append(hl)
+    return layers, host
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every GPU box here has one MI355X and the "
+              f"path is single-GPU by design (requested --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import siphon_amd as sa
+    from siphon_amd import synth
+
+    torch.cuda.init()
+    dev = sa.Device(0)
+    rng = np.random.default_rng(args.seed)
+    t0 = time.time()
+    cpu_layers = 0 if args.no_cpu else 2
+    layers, host_layers = build_layers(dev, rng, cpu_layers)
+    log(f"uploaded 32 layers in {time.time() - t0:.1f} s")
+    pass_bytes = sum(l[name].gguf_bytes for l in layers for name in l)
+
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    # activations: one f32 vector per (layer, stage), N(0,1), resident in HBM
+    acts = [[torch.randn(n, device="cuda") for n in (4096, 4096, 4096, 14336)]
+            for _ in range(N_LAYERS)]
+    outs = {name: torch.empty(n_out, device="cuda")
+            for (name, _, n_out, _) in synth.LLAMA3_8B_LAYER}
+    stage_of = {"wq": 0, "wk": 0, "wv": 0, "wo": 1, "ffn_gate": 2, "ffn_up": 2, "ffn_down": 3}
+    order = [name for (name, _, _, _) in synth.LLAMA3_8B_LAYER]
+
+    def decode_pass(events=None):
+        for il in range(N_LAYERS):
+            for name in order:
+                w = layers[il][name]
+                x = acts[il][stage_of[name]]
+                if events is not None:
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                dev.gemv_dev(w, x.data_ptr(), outs[name].data_ptr(), w.n_out, sp)
+                if events is not None:
+                    e1.record(stream)
+                    events.append((w, e0, e1))
+
+    # eager reference output, then capture the pass in a graph
+    with torch.cuda.stream(stream):
+        decode_pass()
+    torch.cuda.synchronize()
+    eager = {k: v.clone() for k, v in outs.items()}
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        decode_pass()
+    for _ in range(3):  # replays must reproduce the eager results exactly
+        graph.replay()
+        torch.cuda.synchronize()
+        for k in outs:
+            assert torch.equal(outs[k], eager[k]), f"graph replay differs on {k}"
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = pass_bytes / (elapsed / args.steps) / 1e9
+
+    # roofline of the dominant kernel (Q4_K matvec): per-launch HIP events on
+    # the launch stream over two eager passes
+    events = []
+    with torch.cuda.stream(stream):
+        decode_pass(events)
+        decode_pass(events)
+    torch.cuda.synchronize()
+    q4k_bytes = q4k_ms = 0.0
+    q6k_bytes = q6k_ms = 0.0
+    n_q4k = 0
+    for (w, e0, e1) in events:
+        ms = e0.elapsed_time(e1)
+        nbytes = w.gguf_bytes + 4 * (w.n_in + w.n_out)
+        if w.type == sa.Q4_K:
+            q4k_bytes += nbytes
+            q4k_ms += ms
+            n_q4k += 1
+        else:
+            q6k_bytes += nbytes
+            q6k_ms += ms
+    achieved = q4k_bytes / (q4k_ms / 1e3) / 1e9
+    roofline = {
+        "kernel": "sihip::matvec_kernel<Q4_K,1> (decode pass, 160 launches per pass)",
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "avg_launch_us": round(q4k_ms * 1e3 / max(n_q4k, 1), 2),
+        "algorithmic_bytes_per_launch": round(q4k_bytes / max(n_q4k, 1)),
+        "traffic": None,
+        "q6k_achieved": round(q6k_bytes / (q6k_ms / 1e3) / 1e9, 1),
+    }
+
+    result = {
+        "metric": "quant matvec weight-GB/s (% HBM peak) at 8B shapes; M=512 GEMM int8 TOPS",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_K/q6_K x q8_K (int8 dot, f32 acc)",
+        "data": "synthetic (seeded random GGUF blocks, N(0,1) activations)",
+        "config": {"workload": "Llama-3-8B Q4_K_M decode layer set, 32 layers x 7 matvecs, "
+                               "batch 1, HIP graph", "weight_bytes_per_step": pass_bytes,
+                   "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+    }
+
+    if not args.no_gemm:
+        result["gemm_m512"] = bench_gemm(dev, torch, stream, rng)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(host_layers, pass_bytes)
+
+    for l in layers:
+        for w in l.values():
+            w.free()
+    dev.close()
+    print(json.dumps(result), flush=True)
+
+
+def bench_gemm(dev, torch, stream, rng):
+    """Config 3: Q4_K W[14336 x 4096] x X[512 x 4096] -> Y[512 x 14336]."""
+    import siphon_amd as sa
+    from siphon_amd import synth
+    n_out, n_in, M = 14336, 4096, 512
+    W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
+    w = dev.upload(sa.Q4_K, n_out, n_in, W)
+    X = torch.randn(M, n_in, device="cuda")
+    Y = torch.empty(M, n_out, device="cuda")
+    sp = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record(stream)
+        for _ in range(reps):
+            dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / reps
+    ops = 2.0 * M * n_out * n_in
+    w.free()
+    tops = ops / t / 1e12
+    return {"value": round(tops, 2), "unit": "TOPS", "M": M, "shape": [n_out, n_in],
+            "us_per_call": round(t * 1e6, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 5)}}
+
+
+def cpu_baseline(host_layers, pass_bytes):
+    """The reference's own AVX2 gemv (compiled from the reference sources into
+    oracle/_ref) through its lane pool, on a bounded sample: the 7 matrices of
+    the first 2 layers, repeated."""
+    from oracle import siq
+    ref = siq.Reference.load()
+    kind = "reference"
+    lanes = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+    import siphon_amd as sa
+    from siphon_amd import synth
+    shapes = {name: (wt, n_out, n_in) for (name, wt, n_out, n_in) in synth.LLAMA3_8B_LAYER}
+    rng = np.random.default_rng(7)
+    total_bytes = 0
+    total_s = 0.0
+    reps = 3
+    t_start = time.time()
+    for hl in host_layers:
+        for name, W in hl.items():
+            wt, n_out, n_in = shapes[name]
+            x = rng.standard_normal(n_in).astype(np.float32)
+            if ref is not None:
+                _, secs = ref.gemv_timed(wt, W, n_out, n_in, x, lanes, reps)
+                t = float(np.median(secs))
+            else:
+                kind = "port"
+                o = siq.Oracle()
+                t1 = time.perf_counter()
+                o.gemv(wt, W, n_out, n_in, x, lanes)
+                t = time.perf_counter() - t1
+            total_bytes += W.nbytes
+            total_s += t
+    gbs = total_bytes / total_s / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": lanes, "kind": kind,
+            "impl": "avx2" if (ref is not None and ref.avx2) else "scalar",
+            "sample": f"{len(host_layers)} layers x 7 matrices ({total_bytes} weight bytes), "
+                      f"median of {reps} gemv calls each, {time.time() - t_start:.1f} s wall",
+            "gpu_over_cpu": None}
+
+
+if __name__ == "__main__":
+    main()

@@ -9,13 +9,9 @@
 //
 //   unit   = 32 consecutive elements of a row (one 32-block for Q4_0/Q5_0/
 //            Q8_0/F16, one eighth of a 256-element super-block for K-quants)
-//   wave tile = R rows x G unit-columns handled by the 64 lanes of a wave,
-//            lane = r * G + g (R * G = 64); at step s lane (r, g) consumes
-//            unit u = s * G + g of row tile * R + r.
-//   unit plane  byte offset = ((tile * S + s) * 64 + lane) * P
-//   block plane (K-quants, one record per super-block of 8 units; needs
-//            G % 8 == 0 so the 8 lanes of a super-block are adjacent):
-//            byte offset = ((tile * S + s) * 8 + lane / 8) * P
+//   column = what one lane handles per round: a whole super-block (K-quants,
+//            8 units, so its scales are loaded and unpacked once) or a unit
+//   (tile geometry and record order: see Layout below)
 //
 // Inside a unit the quantized values are re-packed to one canonical order so
 // that every format decodes to 8 dwords q[t], byte k of q[t] = element 4t+k,
@@ -69,7 +65,7 @@ SIHD inline uint32_t pair_of(uint32_t t) {
     }
 }
 
-SIHD inline bool is_kquant(uint32_t t) {
+SIHD constexpr inline bool is_kquant(uint32_t t) {
     return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K;
 }
 
@@ -97,23 +93,35 @@ SIHD inline PlaneSpec planes_of(uint32_t t) {
 }
 
 // Geometry of one uploaded matrix in the planar layout.
+//
+// A row is a sequence of COLUMNS: super-blocks of 256 elements for the
+// K-quants, 32-element units for Q4_0/Q5_0/Q8_0/F16. A wave tile covers R
+// rows x G columns (R * G = 64, lane = r * G + g); round s of the tile gives
+// lane (r, g) column c = s * G + g of row tile * R + r. Rounds past the last
+// column (when G does not divide the column count) read zero-filled padding.
+//   column-level plane record = (tile * S + s) * 64 + lane
+//   unit-level plane record (K-quants, unit k = 0..7 of the super-block)
+//                            = ((tile * S + s) * 8 + k) * 64 + lane
+// so every load instruction of a wave reads 64 consecutive records.
 struct Layout {
     uint32_t type;
     int64_t n_out, n_in;
     int64_t nunits;   // n_in / 32
-    int G, R;         // unit-columns and rows per wave tile (G * R = 64)
+    int64_t ncols;    // columns per row: n_in / 256 (K-quants) or n_in / 32
+    int G, R;         // columns and rows per wave tile (G * R = 64)
     int logG;
-    int64_t S;        // steps per tile = ceil(nunits / G)
+    int64_t S;        // rounds per tile = ceil(ncols / G)
     int64_t ntiles;   // ceil(n_out / R)
     int nplanes;
     int64_t plane_off[4];
     int plane_bytes[4];
-    int plane_blk[4];
+    int plane_blk[4];  // 1: one record per super-block (K-quants)
     int64_t total_bytes;
 };
 
 SIHD inline int64_t plane_records(const Layout &L, int p) {
-    return L.ntiles * L.S * (L.plane_blk[p] ? 8 : 64);
+    const bool unit_level = is_kquant(L.type) && !L.plane_blk[p];
+    return L.ntiles * L.S * 64 * (unit_level ? 8 : 1);
 }
 
 inline bool make_layout(uint32_t type, int64_t n_out, int64_t n_in, int G, Layout *L) {
@@ -121,16 +129,16 @@ inline bool make_layout(uint32_t type, int64_t n_out, int64_t n_in, int G, Layou
     if (!geometry(type, &be, &bb) || type == T_Q8_K) return false;
     if (n_in <= 0 || n_out <= 0 || n_in % 32 != 0 || n_in % be != 0) return false;
     if (G < 1 || G > 64 || (G & (G - 1))) return false;
-    if (is_kquant(type) && G % 8 != 0) return false;
     L->type = type;
     L->n_out = n_out;
     L->n_in = n_in;
     L->nunits = n_in / 32;
+    L->ncols = is_kquant(type) ? n_in / 256 : n_in / 32;
     L->G = G;
     L->R = 64 / G;
     L->logG = 0;
     while ((1 << L->logG) < G) L->logG++;
-    L->S = (L->nunits + G - 1) / G;
+    L->S = (L->ncols + G - 1) / G;
     L->ntiles = (n_out + L->R - 1) / L->R;
     const PlaneSpec ps = planes_of(type);
     L->nplanes = ps.n;
@@ -150,18 +158,26 @@ inline bool make_layout(uint32_t type, int64_t n_out, int64_t n_in, int G, Layou
     return true;
 }
 
+// Record index of column c of row `row` (column-level planes).
+SIHD inline int64_t col_rec(const Layout &L, int64_t row, int64_t c) {
+    const int64_t tile = row / L.R, r = row % L.R;
+    const int64_t s = c >> L.logG, g = c & (L.G - 1);
+    return (tile * L.S + s) * 64 + r * L.G + g;
+}
+
 // Byte offset of unit u of row `row` in unit plane p.
 SIHD inline int64_t unit_off(const Layout &L, int p, int64_t row, int64_t u) {
-    const int64_t tile = row / L.R, r = row % L.R;
-    const int64_t s = u >> L.logG, g = u & (L.G - 1);
-    return L.plane_off[p] + ((tile * L.S + s) * 64 + r * L.G + g) * L.plane_bytes[p];
+    if (is_kquant(L.type)) {
+        const int64_t cr = col_rec(L, row, u >> 3);  // (tile*S + s)*64 + lane
+        const int64_t rec = ((cr >> 6) * 8 + (u & 7)) * 64 + (cr & 63);
+        return L.plane_off[p] + rec * L.plane_bytes[p];
+    }
+    return L.plane_off[p] + col_rec(L, row, u) * L.plane_bytes[p];
 }
 
 // Byte offset of the super-block containing unit u in block plane p.
 SIHD inline int64_t block_off(const Layout &L, int p, int64_t row, int64_t u) {
-    const int64_t tile = row / L.R, r = row % L.R;
-    const int64_t s = u >> L.logG, g = u & (L.G - 1);
-    return L.plane_off[p] + ((tile * L.S + s) * 8 + ((r * L.G + g) >> 3)) * L.plane_bytes[p];
+    return L.plane_off[p] + col_rec(L, row, u >> 3) * L.plane_bytes[p];
 }
 
 // ---- canonical packers (one unit of 32 values) ---------------------------

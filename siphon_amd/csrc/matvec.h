@@ -97,7 +97,8 @@ __device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int l
         v[4 * i] = t4[i].x; v[4 * i + 1] = t4[i].y; v[4 * i + 2] = t4[i].z; v[4 * i + 3] = t4[i].w;
     }
     const Q8KRow r = q8k_block_row16(v, lane16);
-    reinterpret_cast<uint4 *>(col + b * 256)[lane16] = r.q;
+    *reinterpret_cast<uint4 *>(col + q8k_lds_unit((uint32_t)nb, (uint32_t)b, lane16 >> 1) +
+                               16 * (lane16 & 1)) = r.q;
     reinterpret_cast<int16_t *>(col + n + nb * 4)[b * 16 + lane16] = (int16_t)r.gsum;
     if (lane16 == 0) reinterpret_cast<float *>(col + n)[b] = r.d;
 }
@@ -132,7 +133,10 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
                     const int64_t b = i / 73, w = i % 73;  // 73 dwords per 292-byte block
                     const uint32_t v = reinterpret_cast<const uint32_t *>(src + b * 292)[w];
                     if (w == 0) dcol[b] = __uint_as_float(v);
-                    else if (w < 65) reinterpret_cast<uint32_t *>(col + b * 256)[w - 1] = v;
+                    else if (w < 65)
+                        *reinterpret_cast<uint32_t *>(
+                            col + q8k_lds_unit((uint32_t)nb, (uint32_t)b, (uint32_t)(w - 1) >> 3) +
+                            4 * ((w - 1) & 7)) = v;
                     else reinterpret_cast<uint32_t *>(bcol + b * 16)[w - 65] = v;
                 }
             }
@@ -185,13 +189,13 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
 
 // ---- the kernel -------------------------------------------------------------
 //
-// Each wave walks a flat sequence of items (tile, step): tiles wave0,
-// wave0 + nwaves, ... and S steps per tile. All control flow in the loop is
-// wave-uniform (scalar): loads are never predicated per lane. Rows past
-// n_out inside the last tile and the lanes of a clamped final batch read
-// in-bounds records (tile padding is allocated and zero-filled at upload)
-// and their results are discarded. The upload guarantees nunits % G == 0,
-// so every step of a tile is a full step.
+// Each wave walks a flat sequence of rounds (tile, s): tiles wave0,
+// wave0 + nwaves, ... and S rounds per tile. One round is one super-block per
+// lane for the K-quants and kBatch units per lane otherwise. All control
+// flow in the loop is wave-uniform (scalar); loads are never predicated per
+// lane: rows past n_out in the last tile and columns past the end of a row
+// read the zero-filled padding that the upload allocates, and their LDS
+// activation reads are clamped into the row, so they contribute exactly 0.
 
 struct Item {
     uint32_t tile, s, rec;  // rec = (tile * S + s) * 64
@@ -212,31 +216,41 @@ __device__ inline float group_sum(float v, int G) {
     return v;
 }
 
+template <uint32_t FMT>
+struct Buf {
+    static constexpr bool kq = is_kquant(FMT);
+    static constexpr int items = kq ? 1 : kBatch;  // rounds per buffer
+    KRaw k;
+    Raw u[kBatch];
+};
+
 template <uint32_t FMT, int NC>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr bool KQ = is_kquant(FMT);
     constexpr uint32_t PAIR = (FMT == T_F16) ? T_F16
                               : (FMT == T_Q4_0 || FMT == T_Q5_0 || FMT == T_Q8_0) ? T_Q8_0
                                                                                    : T_Q8_K;
+    constexpr int ITEMS = Buf<FMT>::items;
     const Layout &L = A.L;
     const int lane = threadIdx.x & 63;
     const int G = L.G;
     const int g = lane & (G - 1);
     const int r = lane >> L.logG;
-    const LaneK K = lane_consts(g & 7);
     Planes P;
 #pragma unroll
     for (int p = 0; p < 4; p++) P.p[p] = A.w + L.plane_off[p];
     const uint32_t S = (uint32_t)L.S;
     const uint32_t n_in = (uint32_t)L.n_in;
+    const uint32_t last_col = (uint32_t)L.ncols - 1;
     const uint32_t col_bytes = (uint32_t)A.col_bytes;
     const uint32_t ntiles = (uint32_t)((A.n_out + L.R - 1) / L.R);
     const uint32_t nwaves = gridDim.x * kWaves;
-    // wave-uniform: keep the whole item walk in scalar registers
+    // wave-uniform: keep the whole walk in scalar registers
     const uint32_t wave0 =
         blockIdx.x * kWaves + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t my_tiles = wave0 < ntiles ? (ntiles - 1 - wave0) / nwaves + 1 : 0;
-    const uint32_t total = my_tiles * S;  // items of this wave
+    const uint32_t total = my_tiles * S;  // rounds of this wave
 
     auto step = [&](Item &it) {
         if (++it.s == S) {
@@ -247,15 +261,20 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
             it.rec += 64u;
         }
     };
-    // issue the loads of kBatch items starting at item k; items past the end
-    // repeat the last item (in bounds, results unused)
-    Item in_it{wave0, 0, wave0 * S * 64u};
-    uint32_t issued = 0;  // items whose loads have been issued
-    auto issue = [&](Raw *buf) {
+    // issue the loads of the next ITEMS rounds; rounds past the end repeat
+    // the last round (in bounds, results unused)
+    // a wave without rows (only in the last workgroup) still loads, from
+    // tile 0, so that the loads before the barrier are unconditional
+    const uint32_t t0 = total ? wave0 : 0u;
+    Item in_it{t0, 0, t0 * S * 64u};
+    uint32_t issued = 0;
+    auto issue = [&](Buf<FMT> &b) {
 #pragma unroll
-        for (int i = 0; i < kBatch; i++) {
-            load_unit<FMT>(P, in_it.rec + (uint32_t)lane, (in_it.rec >> 3) + (uint32_t)(lane >> 3), K,
-                           buf[i]);
+        for (int i = 0; i < ITEMS; i++) {
+            if constexpr (KQ)
+                load_kblock<FMT>(P, in_it.rec * 8u + (uint32_t)lane, in_it.rec + (uint32_t)lane, b.k);
+            else
+                load_unit<FMT>(P, in_it.rec + (uint32_t)lane, b.u[i]);
             if (issued < total) {
                 issued++;
                 if (issued < total) step(in_it);
@@ -267,12 +286,16 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = 0.0f;
-    auto consume = [&](const Raw *buf) {
+    auto consume = [&](const Buf<FMT> &b) {
 #pragma unroll
-        for (int i = 0; i < kBatch; i++) {
+        for (int i = 0; i < ITEMS; i++) {
             if (c_k < total) {
-                const uint32_t u = c_it.s * (uint32_t)G + (uint32_t)g;
-                compute_unit<FMT, NC>(lds, col_bytes, n_in, u, K, buf[i], acc);
+                uint32_t col = c_it.s * (uint32_t)G + (uint32_t)g;
+                col = col < last_col ? col : last_col;  // padding columns read a valid LDS slot
+                if constexpr (KQ)
+                    compute_kblock<FMT, NC>(lds, col_bytes, n_in, col, b.k, acc);
+                else
+                    compute_unit<FMT, NC>(lds, col_bytes, n_in, col, b.u[i], acc);
                 if (c_it.s == S - 1) {
                     const int64_t row = (int64_t)c_it.tile * L.R + r;
 #pragma unroll
@@ -288,25 +311,35 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
         }
     };
 
-    Raw bufA[kBatch], bufB[kBatch];
+    Buf<FMT> bufA, bufB;
     XFirst xf;
     if constexpr (PAIR == T_Q8_K) stage_q8k_first(A, xf);
-    if (total) issue(bufA);
+    issue(bufA);
     stage_activations<PAIR>(A, lds, xf);
-    if (total) issue(bufB);
+    issue(bufB);
     __syncthreads();
+    if (total == 0) return;  // a wave without rows only helped to stage
 
-    // Two batches in flight: each buffer is refilled right after it has been
+    // Two buffers in flight: each buffer is refilled right after it has been
     // decoded, so a refill never overwrites registers with a load pending and
-    // every wait covers one buffer only. Refills are unconditional (past the
-    // end they repeat the last item), keeping the loads straight-line code.
-    while (c_k < total) {
+    // every wait covers one buffer only. The steady-state loop has one exit
+    // at the top and unconditional refills, so the memory counters always
+    // hold the two buffers in the same order and each wait is for the older
+    // one alone. The last 1-3 buffers drain without redundant refills.
+    const uint32_t nbuf = (total + ITEMS - 1) / ITEMS;
+    uint32_t i = 0;  // next buffer to decode; A holds it, B the one after
+    while (i + 4 <= nbuf) {
         consume(bufA);
         issue(bufA);
-        if (c_k >= total) break;
         consume(bufB);
         issue(bufB);
+        i += 2;
     }
+    const uint32_t left = nbuf - i;  // 1..3
+    consume(bufA);
+    if (left == 3) issue(bufA);
+    if (left >= 2) consume(bufB);
+    if (left == 3) consume(bufA);
 }
 
 // ---- standalone quantizers (global output in the reference block layouts) --

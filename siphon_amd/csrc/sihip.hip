@@ -125,26 +125,27 @@ static int wave_target() {
     return v > 0 ? v : 2048;
 }
 
-// Unit-columns per wave tile: the smallest power of two that divides the row's
-// unit count and still gives about wave_target() row tiles, so that the whole
-// chip is busy while each lane keeps as many units (and as few shuffle steps)
-// as possible.
-static int choose_G(uint32_t type, int64_t n_out, int64_t nunits) {
+// Columns (super-blocks for K-quants, 32-element units otherwise) per wave
+// tile: the smallest power of two that keeps at least 80% of the lanes busy
+// and gives about wave_target() row tiles, so the whole chip is busy while
+// each lane keeps as many columns (and as few shuffle steps) as possible.
+static int choose_G(uint32_t type, int64_t n_out, int64_t n_in) {
+    const int64_t ncols = is_kquant(type) ? n_in / 256 : n_in / 32;
     if (const char *f = getenv("SIHIP_TILE_COLS")) {
         const int G = atoi(f);
-        if (G >= 1 && G <= 64 && !(G & (G - 1)) && (!is_kquant(type) || G % 8 == 0) &&
-            nunits % G == 0)
-            return G;
+        if (G >= 1 && G <= 64 && !(G & (G - 1))) return G;
     }
     const int64_t target = wave_target();
-    int best = -1;
-    for (int G = is_kquant(type) ? 8 : 1; G <= 64; G *= 2) {
-        if (nunits % G) continue;
-        best = G;
+    int best = 1;
+    int64_t best_tiles = 0;
+    for (int G = 1; G <= 64; G *= 2) {
+        const int64_t S = (ncols + G - 1) / G;
+        if (ncols * 10 < S * G * 8) continue;  // fewer than 80% of the lanes busy
         const int64_t tiles = (n_out + 64 / G - 1) / (64 / G);
+        if (tiles > best_tiles) { best = G; best_tiles = tiles; }
         if (tiles >= target) break;
     }
-    return best;  // G = 1 (8 for K-quants) always divides nunits
+    return best;
 }
 
 extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out,
@@ -167,7 +168,7 @@ extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out
     HIP_OK(ctx, hipSetDevice(ctx->device));
     const int64_t nunits = (int64_t)n_in / 32;
     Layout L;
-    if (!make_layout(type, (int64_t)n_out, (int64_t)n_in, choose_G(type, n_out, nunits), &L))
+    if (!make_layout(type, (int64_t)n_out, (int64_t)n_in, choose_G(type, n_out, n_in), &L))
         return set_err(ctx, SIHIP_EINVAL, "weight_upload: no layout for this shape");
     uint8_t *dev = nullptr;
     if (hipMalloc((void **)&dev, (size_t)L.total_bytes) != hipSuccess)

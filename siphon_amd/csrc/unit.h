@@ -6,7 +6,8 @@
 // records; compute_unit decodes them into 8 dwords q[t] (byte k = element
 // 4t+k, canonical order) and accumulates the unit's contribution against
 // NC activation columns held in LDS (pair format, layout of matvec.h):
-//   Q8_K column: int8 qs[n] | f32 d[n/256] | int16 bsums[n/16]
+//   Q8_K column: int8 qs[n] (unit-major, q8k_lds_unit) | f32 d[n/256] |
+//                int16 bsums[n/16]
 //   Q8_0 column: int8 qs[n] | f32 d[n/32]  | int32 qsum[n/32]
 //   F16  column: f16 h[n]
 // Record indices and byte offsets are 32-bit (a plane is < 4 GiB), so the
@@ -148,48 +149,6 @@ SIHD inline void two8_split(uint32_t h0, uint32_t h1, uint32_t q[8], int pos, bo
     }
 }
 
-// ---- per-lane constants ------------------------------------------------------
-
-// Everything that depends only on the lane's sub-block index j (0..7) of the
-// K-quant super-block, computed once per kernel so the unit loop holds no
-// lane-divergent branches.
-struct LaneK {
-    int j;
-    uint32_t k4_hi;                 // Q4_K/Q5_K: j >= 4
-    uint32_t sc_sh, sc_w, mn_sh, mn_w, h_sh, h_w;
-    uint32_t q3_lsh, q3_hsh0, q3_hsh1;
-    uint32_t pair_sh;               // 16 * (j & 1): Q2_K/Q6_K scale byte pair
-    uint32_t rec4;                  // byte offset of the dword holding scales 2j, 2j+1
-    uint32_t q3rec4;                // Q3_K: dword with the low nibbles of scales 2j, 2j+1
-};
-
-SIHD inline LaneK lane_consts(int j) {
-    LaneK K;
-    K.j = j;
-    // 6-bit scale/min of sub-block j (reference kernels.c:648-656):
-    //   j < 4: sc = s[j] & 63,             mn = s[j+4] & 63
-    //   j >=4: sc = lo4(s[j+4]) | hi2(s[j-4]) << 4, mn = hi4(s[j+4]) | hi2(s[j]) << 4
-    const uint32_t jj = (uint32_t)(j & 3);
-    K.k4_hi = j >= 4;
-    K.sc_sh = 8 * jj;
-    K.sc_w = j < 4 ? 6 : 4;
-    K.mn_sh = j < 4 ? 8 * jj : 8 * jj + 4;
-    K.mn_w = j < 4 ? 6 : 4;
-    K.h_sh = 8 * jj + 6;
-    K.h_w = j < 4 ? 0 : 2;
-    // Q3_K 6-bit scale k for k = 2j, 2j+1 (reference kernels.c:328-333):
-    // low nibble from byte k%8 (its high nibble when k >= 8), two high bits
-    // from byte 8 + k%4 at bit 2*(k/4)
-    const int k0 = 2 * j;
-    K.q3_lsh = (uint32_t)(8 * (k0 & 3) + (k0 >= 8 ? 4 : 0));
-    K.q3_hsh0 = (uint32_t)(8 * (k0 & 3) + 2 * (k0 >> 2));
-    K.q3_hsh1 = (uint32_t)(8 * ((k0 + 1) & 3) + 2 * ((k0 + 1) >> 2));
-    K.pair_sh = 16u * (uint32_t)(j & 1);
-    K.rec4 = 4u * (uint32_t)(j >> 1);
-    K.q3rec4 = 4u * (uint32_t)((j & 3) >> 1);
-    return K;
-}
-
 // ---- loads -------------------------------------------------------------------
 
 struct Planes {
@@ -203,82 +162,33 @@ struct Raw {
     uint32_t e, f;   // small unit-plane fields
 };
 
-// ur: unit-plane record index of this lane; br: block-plane record index.
+// ---- 32-element formats: one unit per column -----------------------------------
+
+// rec: plane record of this lane's unit
 template <uint32_t FMT>
-SIHD inline void load_unit(const Planes &P, uint32_t ur, uint32_t br, const LaneK &K, Raw &w) {
-    if constexpr (FMT == T_Q4_K) {
-        w.a = ldp<U4>(P.p[0] + ur * 16u);
-        w.m = ldp<U4>(P.p[1] + br * 16u);
-    } else if constexpr (FMT == T_Q5_K) {
-        w.a = ldp<U4>(P.p[0] + ur * 16u);
-        w.e = ldp<uint32_t>(P.p[1] + ur * 4u);
-        w.m = ldp<U4>(P.p[2] + br * 16u);
-    } else if constexpr (FMT == T_Q6_K) {
-        w.a = ldp<U4>(P.p[0] + ur * 16u);
-        const U2 h = ldp<U2>(P.p[1] + ur * 8u);
-        w.e = h.x; w.f = h.y;
-        w.m.x = ldp<uint32_t>(P.p[2] + br * 16u + K.rec4);  // int8 scales 2j, 2j+1
-        w.m.y = ldp<uint16_t>(P.p[3] + br * 2u);
-    } else if constexpr (FMT == T_Q3_K) {
-        const U2 h = ldp<U2>(P.p[0] + ur * 8u);
-        w.e = h.x; w.f = h.y;
-        w.m.x = ldp<uint32_t>(P.p[1] + ur * 4u);
-        const uint8_t *sc = P.p[2] + br * 12u;
-        w.m.y = ldp<uint32_t>(sc + K.q3rec4);  // low nibbles of scales 2j, 2j+1
-        w.m.z = ldp<uint32_t>(sc + 8);         // bytes 8..11: high bits
-        w.m.w = ldp<uint16_t>(P.p[3] + br * 2u);
-    } else if constexpr (FMT == T_Q2_K) {
-        const U2 h = ldp<U2>(P.p[0] + ur * 8u);
-        w.e = h.x; w.f = h.y;
-        w.m.x = ldp<uint32_t>(P.p[1] + br * 16u + K.rec4);  // scale|min bytes 2j, 2j+1
-        w.m.y = ldp<uint32_t>(P.p[2] + br * 4u);            // d, dmin
-    } else if constexpr (FMT == T_Q4_0) {
-        w.a = ldp<U4>(P.p[0] + ur * 16u);
-        w.e = ldp<uint16_t>(P.p[1] + ur * 2u);
+SIHD inline void load_unit(const Planes &P, uint32_t rec, Raw &w) {
+    if constexpr (FMT == T_Q4_0) {
+        w.a = ldp<U4>(P.p[0] + rec * 16u);
+        w.e = ldp<uint16_t>(P.p[1] + rec * 2u);
     } else if constexpr (FMT == T_Q5_0) {
-        w.a = ldp<U4>(P.p[0] + ur * 16u);
-        w.f = ldp<uint32_t>(P.p[1] + ur * 4u);
-        w.e = ldp<uint16_t>(P.p[2] + ur * 2u);
+        w.a = ldp<U4>(P.p[0] + rec * 16u);
+        w.f = ldp<uint32_t>(P.p[1] + rec * 4u);
+        w.e = ldp<uint16_t>(P.p[2] + rec * 2u);
     } else if constexpr (FMT == T_Q8_0) {
-        w.a = ldp<U4>(P.p[0] + ur * 32u);
-        w.b = ldp<U4>(P.p[0] + ur * 32u + 16u);
-        w.e = ldp<uint16_t>(P.p[1] + ur * 2u);
+        w.a = ldp<U4>(P.p[0] + rec * 32u);
+        w.b = ldp<U4>(P.p[0] + rec * 32u + 16u);
+        w.e = ldp<uint16_t>(P.p[1] + rec * 2u);
     } else {  // F16
-        const uint8_t *p = P.p[0] + ur * 64u;
+        const uint8_t *p = P.p[0] + rec * 64u;
         w.a = ldp<U4>(p); w.b = ldp<U4>(p + 16); w.c = ldp<U4>(p + 32); w.d = ldp<U4>(p + 48);
     }
 }
 
-// ---- decode --------------------------------------------------------------------
-
-// Decoded quants of the unit: unsigned biased values for Q4_0 (0..15),
-// Q5_0 (0..31), Q3_K (0..7), Q6_K (0..63); signed for Q8_0; unsigned
-// without bias for Q2_K (0..3), Q4_K (0..15), Q5_K (0..31).
-template <uint32_t FMT>
-SIHD inline void unit_quants(const Raw &w, uint32_t q[8]) {
-    if constexpr (FMT == T_Q4_K || FMT == T_Q4_0 || FMT == T_Q5_0 || FMT == T_Q5_K ||
-                  FMT == T_Q6_K) {
-        nib_split(w.a, q);
-    }
-    if constexpr (FMT == T_Q5_K) add_bit4(q, w.e, 4);
-    if constexpr (FMT == T_Q5_0) add_bit4(q, w.f, 4);
-    if constexpr (FMT == T_Q6_K) two8_split(w.e, w.f, q, 4, true);
-    if constexpr (FMT == T_Q3_K) {
-        two8_split(w.e, w.f, q, 0, false);
-        add_bit4(q, w.m.x, 2);
-    }
-    if constexpr (FMT == T_Q2_K) two8_split(w.e, w.f, q, 0, false);
-    if constexpr (FMT == T_Q8_0) {
-        q[0] = w.a.x; q[1] = w.a.y; q[2] = w.a.z; q[3] = w.a.w;
-        q[4] = w.b.x; q[5] = w.b.y; q[6] = w.b.z; q[7] = w.b.w;
-    }
-}
-
-// Accumulate unit u into acc[0..NC). lds holds NC activation columns of
-// col_bytes each; n is the row length.
+// Accumulate unit u (its LDS position; clamped into the row by the caller)
+// into acc[0..NC). lds holds NC activation columns of col_bytes each.
 template <uint32_t FMT, int NC>
 SIHD inline void compute_unit(const uint8_t *lds, uint32_t col_bytes, uint32_t n, uint32_t u,
-                              const LaneK &K, const Raw &w, float *acc) {
+                              const Raw &w, float *acc) {
     if constexpr (FMT == T_F16) {
         const uint32_t wv[16] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w,
                                  w.c.x, w.c.y, w.c.z, w.c.w, w.d.x, w.d.y, w.d.z, w.d.w};
@@ -293,12 +203,16 @@ SIHD inline void compute_unit(const uint8_t *lds, uint32_t col_bytes, uint32_t n
             acc[c] = s;
         }
         return;
-    }
-    uint32_t q[8];
-    unit_quants<FMT>(w, q);
-
-    if constexpr (FMT == T_Q4_0 || FMT == T_Q5_0 || FMT == T_Q8_0) {
+    } else {
         // 32-blocks: d_w * d_x * (sum(u * x) - bias * sum(x))
+        uint32_t q[8];
+        if constexpr (FMT == T_Q8_0) {
+            q[0] = w.a.x; q[1] = w.a.y; q[2] = w.a.z; q[3] = w.a.w;
+            q[4] = w.b.x; q[5] = w.b.y; q[6] = w.b.z; q[7] = w.b.w;
+        } else {
+            nib_split(w.a, q);
+            if constexpr (FMT == T_Q5_0) add_bit4(q, w.f, 4);
+        }
         const float dw = half_to_float(w.e);
         const uint32_t nb = n / 32;
         for (int c = 0; c < NC; c++) {
@@ -311,71 +225,181 @@ SIHD inline void compute_unit(const uint8_t *lds, uint32_t col_bytes, uint32_t n
             const float dx = ldp<float>(col + n + u * 4u);
             acc[c] = fma_f32(dw * dx, (float)isum, acc[c]);
         }
-        return;
     }
+}
 
-    // K-quants: super-block kb; the unit covers its 16-element groups 2j, 2j+1
-    const uint32_t kb = u >> 3;
-    const uint32_t nb = n / 256;
-    const uint32_t bs_off = n + nb * 4 + kb * 32 + (uint32_t)K.j * 4;
-    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
-        // one 6-bit scale and min for the whole unit
-        const uint32_t s03 = w.m.y, s47 = w.m.z, s811 = w.m.w;
-        const uint32_t A = K.k4_hi ? s811 : s03;
-        const uint32_t B = K.k4_hi ? s811 : s47;
-        const int sc = (int)(ubfe(A, K.sc_sh, K.sc_w) | (ubfe(s03, K.h_sh, K.h_w) << 4));
-        const uint32_t mn = ubfe(B, K.mn_sh, K.mn_w) | (ubfe(s47, K.h_sh, K.h_w) << 4);
-        const uint32_t mn2 = mn | (mn << 16);
-        const float d = half_to_float(w.m.x & 0xffffu);
-        const float dmin = half_to_float(w.m.x >> 16);
-        for (int c = 0; c < NC; c++) {
-            const uint8_t *col = lds + c * col_bytes;
-            int g1;
-            const int g0 = dot8(q, ldp<U4>(col + u * 32u), ldp<U4>(col + u * 32u + 16u), g1);
-            const int isum = sc * (g0 + g1);
-            const int imin = sdot2_i16(ldp<uint32_t>(col + bs_off), mn2, 0);  // m*(bs0+bs1)
-            const float dx = ldp<float>(col + n + kb * 4);
-            const float t = fma_f32(-dmin, (float)imin, d * (float)isum);
-            acc[c] = fma_f32(dx, t, acc[c]);
+// ---- K-quants: one super-block per column ------------------------------------------
+
+// LDS byte offset of unit k (elements 32k..32k+31) of super-block b in a Q8_K
+// column of nb super-blocks. Unit-major order: the lanes of a wave that read
+// unit k of consecutive super-blocks read consecutive 32-byte spans, so
+// their 16-byte LDS reads spread over all banks.
+SIHD inline uint32_t q8k_lds_unit(uint32_t nb, uint32_t b, uint32_t k) {
+    return (k * nb + b) * 32u;
+}
+
+struct KRaw {
+    U4 a[8];          // 16-byte unit records: Q4_K/Q5_K qs, Q6_K ql
+    U2 b[8];          // 8-byte unit records: Q6_K qh, Q3_K/Q2_K low 2 bits
+    uint32_t c[8];    // 4-byte unit records: Q5_K qh, Q3_K high bit
+    U4 m;             // block record: Q4_K/Q5_K d|dmin + scales, Q6_K/Q2_K scales
+    uint32_t e;       // Q6_K/Q3_K d, Q2_K d|dmin
+};
+
+// urec: unit-plane record of unit 0 of this lane's super-block (unit k is
+// 64 records further per k); brec: its block-plane record.
+template <uint32_t FMT>
+SIHD inline void load_kblock(const Planes &P, uint32_t urec, uint32_t brec, KRaw &w) {
+    for (int k = 0; k < 8; k++) {
+        const uint32_t r = urec + 64u * (uint32_t)k;
+        if constexpr (FMT == T_Q4_K) w.a[k] = ldp<U4>(P.p[0] + r * 16u);
+        if constexpr (FMT == T_Q5_K) {
+            w.a[k] = ldp<U4>(P.p[0] + r * 16u);
+            w.c[k] = ldp<uint32_t>(P.p[1] + r * 4u);
         }
-    } else if constexpr (FMT == T_Q2_K) {
-        const uint32_t sw = w.m.x >> K.pair_sh;  // bytes: scale|min << 4 of groups 2j, 2j+1
-        const int sc0 = (int)(sw & 15u), sc1 = (int)((sw >> 8) & 15u);
-        const uint32_t mn2 = ((sw >> 4) & 15u) | (((sw >> 12) & 15u) << 16);
-        const float d = half_to_float(w.m.y & 0xffffu);
-        const float dmin = half_to_float(w.m.y >> 16);
-        for (int c = 0; c < NC; c++) {
-            const uint8_t *col = lds + c * col_bytes;
-            int g1;
-            const int g0 = dot8(q, ldp<U4>(col + u * 32u), ldp<U4>(col + u * 32u + 16u), g1);
-            const int isum = sc0 * g0 + sc1 * g1;
-            const int imin = sdot2_i16(ldp<uint32_t>(col + bs_off), mn2, 0);
-            const float dx = ldp<float>(col + n + kb * 4);
-            const float t = fma_f32(-dmin, (float)imin, d * (float)isum);
-            acc[c] = fma_f32(dx, t, acc[c]);
-        }
-    } else {  // Q3_K, Q6_K: sum_g sc_g * (sum(u*x) - bias * bsum_g)
-        int sc0, sc1;
-        float d;
         if constexpr (FMT == T_Q6_K) {
-            sc0 = sbfe8(w.m.x, K.pair_sh);
-            sc1 = sbfe8(w.m.x, K.pair_sh + 8);
-            d = half_to_float(w.m.y);
-        } else {
-            sc0 = (int)(ubfe(w.m.y, K.q3_lsh, 4) | (ubfe(w.m.z, K.q3_hsh0, 2) << 4)) - 32;
-            sc1 = (int)(ubfe(w.m.y, K.q3_lsh + 8, 4) | (ubfe(w.m.z, K.q3_hsh1, 2) << 4)) - 32;
-            d = half_to_float(w.m.w);
+            w.a[k] = ldp<U4>(P.p[0] + r * 16u);
+            w.b[k] = ldp<U2>(P.p[1] + r * 8u);
         }
-        constexpr int bias = (FMT == T_Q6_K) ? 32 : 4;
-        const uint32_t sc2 = ((uint32_t)sc0 & 0xffffu) | ((uint32_t)sc1 << 16);
+        if constexpr (FMT == T_Q3_K) {
+            w.b[k] = ldp<U2>(P.p[0] + r * 8u);
+            w.c[k] = ldp<uint32_t>(P.p[1] + r * 4u);
+        }
+        if constexpr (FMT == T_Q2_K) w.b[k] = ldp<U2>(P.p[0] + r * 8u);
+    }
+    if constexpr (FMT == T_Q4_K) w.m = ldp<U4>(P.p[1] + brec * 16u);
+    if constexpr (FMT == T_Q5_K) w.m = ldp<U4>(P.p[2] + brec * 16u);
+    if constexpr (FMT == T_Q6_K) {
+        w.m = ldp<U4>(P.p[2] + brec * 16u);
+        w.e = ldp<uint16_t>(P.p[3] + brec * 2u);
+    }
+    if constexpr (FMT == T_Q3_K) {
+        const uint8_t *sc = P.p[2] + brec * 12u;
+        w.m.x = ldp<uint32_t>(sc);
+        w.m.y = ldp<uint32_t>(sc + 4);
+        w.m.z = ldp<uint32_t>(sc + 8);
+        w.e = ldp<uint16_t>(P.p[3] + brec * 2u);
+    }
+    if constexpr (FMT == T_Q2_K) {
+        w.m = ldp<U4>(P.p[1] + brec * 16u);
+        w.e = ldp<uint32_t>(P.p[2] + brec * 4u);
+    }
+}
+
+SIHD inline uint32_t u4_word(const U4 &v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// 6-bit scale and min of sub-block j of Q4_K/Q5_K (reference kernels.c:648-656)
+SIHD inline void k4_scale_min(const U4 &m, int j, int &sc, int &mn) {
+    if (j < 4) {
+        sc = (int)((m.y >> (8 * j)) & 63u);
+        mn = (int)((m.z >> (8 * j)) & 63u);
+    } else {
+        const int jj = j - 4;
+        sc = (int)(((m.w >> (8 * jj)) & 15u) | (((m.y >> (8 * jj + 6)) & 3u) << 4));
+        mn = (int)(((m.w >> (8 * jj + 4)) & 15u) | (((m.z >> (8 * jj + 6)) & 3u) << 4));
+    }
+}
+
+// signed 6-bit scale g of Q3_K (reference kernels.c:328-333): low nibble
+// from byte g%8 (its high nibble for g >= 8), two high bits from byte
+// 8 + g%4 at bit 2*(g/4); minus 32
+SIHD inline int k3_scale(const U4 &m, int g) {
+    const int lb = g & 7;
+    const uint32_t lo = (u4_word(m, lb >> 2) >> (8 * (lb & 3) + (g >= 8 ? 4 : 0))) & 15u;
+    const uint32_t hi = (m.z >> (8 * (g & 3) + 2 * (g >> 2))) & 3u;
+    return (int)(lo | (hi << 4)) - 32;
+}
+
+// Accumulate the super-block (kb: its index in the row, clamped by the
+// caller) into acc[0..NC). The integer sums of all 8 units accumulate
+// exactly; the block scales are applied once.
+template <uint32_t FMT, int NC>
+SIHD inline void compute_kblock(const uint8_t *lds, uint32_t col_bytes, uint32_t n, uint32_t kb,
+                                const KRaw &w, float *acc) {
+    const uint32_t nb = n / 256;
+    int isum[NC];
+    for (int c = 0; c < NC; c++) isum[c] = 0;
+    for (int k = 0; k < 8; k++) {
+        uint32_t q[8];
+        if constexpr (FMT == T_Q4_K || FMT == T_Q5_K || FMT == T_Q6_K) nib_split(w.a[k], q);
+        if constexpr (FMT == T_Q5_K) add_bit4(q, w.c[k], 4);
+        if constexpr (FMT == T_Q6_K) two8_split(w.b[k].x, w.b[k].y, q, 4, true);
+        if constexpr (FMT == T_Q3_K) {
+            two8_split(w.b[k].x, w.b[k].y, q, 0, false);
+            add_bit4(q, w.c[k], 2);
+        }
+        if constexpr (FMT == T_Q2_K) two8_split(w.b[k].x, w.b[k].y, q, 0, false);
+        // integer scales of this unit's two 16-groups (2k, 2k+1)
+        int s0, s1;
+        if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+            int mn;
+            k4_scale_min(w.m, k, s0, mn);
+            s1 = s0;
+        } else if constexpr (FMT == T_Q6_K) {
+            const uint32_t sw = u4_word(w.m, k >> 1);
+            s0 = sbfe8(sw, 16 * (k & 1));
+            s1 = sbfe8(sw, 16 * (k & 1) + 8);
+        } else if constexpr (FMT == T_Q3_K) {
+            s0 = k3_scale(w.m, 2 * k);
+            s1 = k3_scale(w.m, 2 * k + 1);
+        } else {  // Q2_K: low nibble of scale bytes 2k, 2k+1
+            const uint32_t sw = u4_word(w.m, k >> 1) >> (16 * (k & 1));
+            s0 = (int)(sw & 15u);
+            s1 = (int)((sw >> 8) & 15u);
+        }
         for (int c = 0; c < NC; c++) {
-            const uint8_t *col = lds + c * col_bytes;
+            const uint8_t *xp = lds + c * col_bytes + q8k_lds_unit(nb, kb, (uint32_t)k);
             int g1;
-            const int g0 = dot8(q, ldp<U4>(col + u * 32u), ldp<U4>(col + u * 32u + 16u), g1);
-            const int ib = sdot2_i16(ldp<uint32_t>(col + bs_off), sc2, 0);  // sc0*bs0 + sc1*bs1
-            const int isum = sc0 * g0 + sc1 * g1 - bias * ib;
-            const float dx = ldp<float>(col + n + kb * 4);
-            acc[c] = fma_f32(d * dx, (float)isum, acc[c]);
+            const int g0 = dot8(q, ldp<U4>(xp), ldp<U4>(xp + 16), g1);
+            isum[c] += s0 * g0 + s1 * g1;
+        }
+    }
+    // per-block terms: the mins (Q4_K/Q5_K/Q2_K) or the bias of the unsigned
+    // quants (Q3_K: 4, Q6_K: 32) against the activation group sums
+    uint32_t pair[8];  // packed 16-bit factors of groups (2j, 2j+1)
+    for (int j = 0; j < 8; j++) {
+        if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+            int sc, mn;
+            k4_scale_min(w.m, j, sc, mn);
+            pair[j] = (uint32_t)mn | ((uint32_t)mn << 16);
+        } else if constexpr (FMT == T_Q2_K) {
+            const uint32_t sw = u4_word(w.m, j >> 1) >> (16 * (j & 1));
+            pair[j] = ((sw >> 4) & 15u) | (((sw >> 12) & 15u) << 16);
+        } else if constexpr (FMT == T_Q6_K) {
+            const uint32_t sw = u4_word(w.m, j >> 1);
+            pair[j] = ((uint32_t)sbfe8(sw, 16 * (j & 1)) & 0xffffu) |
+                      ((uint32_t)sbfe8(sw, 16 * (j & 1) + 8) << 16);
+        } else {  // Q3_K
+            pair[j] = ((uint32_t)k3_scale(w.m, 2 * j) & 0xffffu) |
+                      ((uint32_t)k3_scale(w.m, 2 * j + 1) << 16);
+        }
+    }
+    float d, dmin = 0.0f;
+    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+        d = half_to_float(w.m.x & 0xffffu);
+        dmin = half_to_float(w.m.x >> 16);
+    } else if constexpr (FMT == T_Q2_K) {
+        d = half_to_float(w.e & 0xffffu);
+        dmin = half_to_float(w.e >> 16);
+    } else {
+        d = half_to_float(w.e);
+    }
+    for (int c = 0; c < NC; c++) {
+        const uint8_t *col = lds + c * col_bytes;
+        const U4 bs0 = ldp<U4>(col + n + nb * 4 + kb * 32u);
+        const U4 bs1 = ldp<U4>(col + n + nb * 4 + kb * 32u + 16u);
+        const uint32_t bsw[8] = {bs0.x, bs0.y, bs0.z, bs0.w, bs1.x, bs1.y, bs1.z, bs1.w};
+        int t = 0;
+        for (int j = 0; j < 8; j++) t = sdot2_i16(bsw[j], pair[j], t);
+        const float dx = ldp<float>(col + n + kb * 4u);
+        if constexpr (FMT == T_Q4_K || FMT == T_Q5_K || FMT == T_Q2_K) {
+            const float v = fma_f32(-dmin, (float)t, d * (float)isum[c]);  // t = sum m*bsum
+            acc[c] = fma_f32(dx, v, acc[c]);
+        } else {
+            constexpr int bias = (FMT == T_Q6_K) ? 32 : 4;
+            acc[c] = fma_f32(d * dx, (float)(isum[c] - bias * t), acc[c]);
         }
     }
 }

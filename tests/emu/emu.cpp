@@ -26,7 +26,9 @@ static void stage(uint32_t pair, int64_t n, const uint8_t *xq, uint8_t *col) {
         const int64_t nb = n / 256;
         for (int64_t b = 0; b < nb; b++) {
             memcpy(col + n + b * 4, xq + b * 292, 4);
-            memcpy(col + b * 256, xq + b * 292 + 4, 256);
+            for (int k = 0; k < 8; k++)
+                memcpy(col + q8k_lds_unit((uint32_t)nb, (uint32_t)b, (uint32_t)k),
+                       xq + b * 292 + 4 + 32 * k, 32);
             memcpy(col + n + nb * 4 + b * 32, xq + b * 292 + 260, 32);
         }
     } else if (pair == T_Q8_0) {
@@ -54,16 +56,25 @@ static void run(const Layout &L, const uint8_t *W, const uint8_t *lds, int64_t c
             const int64_t row = tile * L.R + r;
             std::vector<float> v(L.G, 0.0f);
             for (int g = 0; g < L.G; g++) {
-                const int lane = r * L.G + g;
-                const LaneK K = lane_consts(g & 7);
+                const uint32_t lane = (uint32_t)(r * L.G + g);
                 float acc[1] = {0.0f};
+                // every round of the tile, padding columns included (they
+                // hold zero weights and read the last column's activations)
                 for (int64_t s = 0; s < L.S; s++) {
-                    const int64_t u = s * L.G + g;
-                    if (row >= L.n_out || u >= L.nunits) continue;
+                    int64_t col = s * L.G + g;
+                    if (col > L.ncols - 1) col = L.ncols - 1;
                     const uint32_t rec = (uint32_t)((tile * L.S + s) * 64);
-                    Raw raw;
-                    load_unit<FMT>(P, rec + (uint32_t)lane, (rec >> 3) + (uint32_t)(lane >> 3), K, raw);
-                    compute_unit<FMT, 1>(lds, (uint32_t)cb, (uint32_t)L.n_in, (uint32_t)u, K, raw, acc);
+                    if constexpr (is_kquant(FMT)) {
+                        KRaw raw;
+                        load_kblock<FMT>(P, rec * 8u + lane, rec + lane, raw);
+                        compute_kblock<FMT, 1>(lds, (uint32_t)cb, (uint32_t)L.n_in, (uint32_t)col,
+                                               raw, acc);
+                    } else {
+                        Raw raw;
+                        load_unit<FMT>(P, rec + lane, raw);
+                        compute_unit<FMT, 1>(lds, (uint32_t)cb, (uint32_t)L.n_in, (uint32_t)col,
+                                             raw, acc);
+                    }
                 }
                 v[g] = acc[0];
             }
