@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define SIHIP_ABI_VERSION 1
+#define SIHIP_ABI_VERSION 2
 
 /* error codes: the reference's SI_* values plus one for the device */
 #define SIHIP_OK        0
@@ -77,9 +77,10 @@ int sihip_weight_upload(sihip_ctx *ctx, uint32_t ggml_type, uint64_t n_out,
 int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w);
 /* Device bytes the repacked weight occupies (>= the GGUF bytes). */
 uint64_t sihip_weight_device_bytes(const sihip_weight *w);
-/* Layout introspection: 32-element units per row handled side by side by
- * one wavefront (1..64). Chosen at upload from the shape; the environment
- * variable SIHIP_TILE_COLS forces it when valid for the shape (tests). */
+/* Layout introspection: row columns (256-element super-blocks for the
+ * K-quants, 32-element blocks otherwise) handled side by side by one
+ * wavefront, 1..64 (a power of two). Chosen at upload from the shape; the
+ * environment variable SIHIP_TILE_COLS forces it (tests, tuning). */
 int sihip_weight_tile_cols(const sihip_weight *w);
 
 /* ---- matvec / matmul: host pointers, synchronous ---------------------
@@ -110,6 +111,18 @@ int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float *X,
 int sihip_gemv_multi_dev(sihip_ctx *ctx, int count,
                          const sihip_weight *const *w, const float *x,
                          float *const *y, void *stream);
+
+/* ---- device memory for hosts without a HIP runtime of their own -------
+ * The reference host is plain C17 and never links HIP; these let it (and
+ * tests) hold activations and outputs on the device for the *_dev entry
+ * points. Copies are synchronous and ordered after all work on the
+ * device's default stream. */
+int sihip_dev_alloc(sihip_ctx *ctx, uint64_t bytes, void **dptr);
+int sihip_dev_free(sihip_ctx *ctx, void *dptr);
+int sihip_memcpy_htod(sihip_ctx *ctx, void *dst, const void *src, uint64_t bytes);
+int sihip_memcpy_dtoh(sihip_ctx *ctx, void *dst, const void *src, uint64_t bytes);
+/* Wait for all work on the context's device. */
+int sihip_synchronize(sihip_ctx *ctx);
 
 /* ---- building blocks exposed for parity tests ------------------------ */
 

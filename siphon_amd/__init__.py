@@ -25,7 +25,7 @@ NAMES = {F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_
 TYPES = {v: k for k, v in NAMES.items()}
 WEIGHT_TYPES = [Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F16]
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def row_bytes(wtype: int, n_in: int) -> int:
@@ -76,6 +76,11 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     for fn in ("sihip_quantize_q8_K", "sihip_quantize_q8_0", "sihip_convert_f16"):
         getattr(L, fn).argtypes = [_vp, _vp, _vp, _i64]
     L.sihip_vec_dot.argtypes = [_vp, _u32, ctypes.c_int, _vp, _vp, _vp]
+    L.sihip_dev_alloc.argtypes = [_vp, _u64, ctypes.POINTER(_vp)]
+    L.sihip_dev_free.argtypes = [_vp, _vp]
+    L.sihip_memcpy_htod.argtypes = [_vp, _vp, _vp, _u64]
+    L.sihip_memcpy_dtoh.argtypes = [_vp, _vp, _vp, _u64]
+    L.sihip_synchronize.argtypes = [_vp]
     L.sihip_gemv_pair.argtypes = [_vp, _u32, _i64, _i64, _vp, _vp, _vp]
     if L.sihip_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {L.sihip_abi_version()} != {ABI_VERSION}")
@@ -173,6 +178,21 @@ class Device:
         ya = (_vp * n)(*y_ptrs)
         self._check(self.L.sihip_gemv_multi_dev(self.ctx, n, wa, x_ptr, ya, stream))
 
+    # device memory through the library's own HIP runtime (no torch needed)
+    def alloc(self, nbytes: int) -> "DevBuf":
+        p = _vp()
+        self._check(self.L.sihip_dev_alloc(self.ctx, nbytes, ctypes.byref(p)))
+        return DevBuf(self, p.value, nbytes)
+
+    def to_device(self, a: np.ndarray) -> "DevBuf":
+        a = np.ascontiguousarray(a)
+        b = self.alloc(max(a.nbytes, 16))
+        self._check(self.L.sihip_memcpy_htod(self.ctx, b.ptr, _ptr(a), a.nbytes))
+        return b
+
+    def synchronize(self):
+        self._check(self.L.sihip_synchronize(self.ctx))
+
     def quantize(self, pair: int, x: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)
         be, bb = GEOM[pair]
@@ -197,3 +217,26 @@ class Device:
         self._check(self.L.sihip_gemv_pair(self.ctx, wtype, n_rows, n_in, _ptr(rows), _ptr(xq),
                                            _ptr(y)))
         return y
+
+
+class DevBuf:
+    """A device allocation made through the library (sihip_dev_alloc)."""
+
+    def __init__(self, dev: "Device", ptr: int, nbytes: int):
+        self.dev, self.ptr, self.nbytes = dev, ptr, nbytes
+
+    def to_host(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        self.dev._check(self.dev.L.sihip_memcpy_dtoh(self.dev.ctx, _ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def fill(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        self.dev._check(self.dev.L.sihip_memcpy_htod(self.dev.ctx, self.ptr, _ptr(a), a.nbytes))
+
+    def free(self):
+        if self.ptr:
+            self.dev._check(self.dev.L.sihip_dev_free(self.dev.ctx, self.ptr))
+            self.ptr = 0

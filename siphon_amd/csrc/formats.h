@@ -57,7 +57,7 @@ SIHD inline bool geometry(uint32_t t, uint32_t *be, uint32_t *bb) {
 }
 
 // Activation pair format (reference kernels.c:946-960).
-SIHD inline uint32_t pair_of(uint32_t t) {
+SIHD constexpr inline uint32_t pair_of(uint32_t t) {
     switch (t) {
         case T_F16: return T_F16;
         case T_Q4_0: case T_Q5_0: case T_Q8_0: return T_Q8_0;

@@ -51,14 +51,28 @@ __host__ __device__ inline int64_t lds_col_bytes(uint32_t pair, int64_t n_in) {
     return n_in * 2;  // F16
 }
 
-struct MVArgs {
+// One weight matrix of a launch. Several matrices that share the activation
+// (QKV, gate+up) run in one launch: each gets a contiguous range of
+// workgroups, and all of them stage the same activation into LDS.
+constexpr int kMaxSegs = 4;
+
+struct MVSeg {
     const uint8_t *w;     // plane base
     Layout L;
+    float *y;             // outputs, column c at y + c * ldy
+    int64_t ldy;
+    int64_t n_out;        // rows to compute (<= L.n_out)
+    uint32_t wg_begin;    // first workgroup of this matrix
+    uint32_t nwg;         // workgroups of this matrix
+};
+
+struct MVArgs {
+    MVSeg seg[kMaxSegs];
+    int nseg;
+    int64_t n_in;
     const float *x;       // f32 activations, column c at x + c * ldx (or null)
     const uint8_t *xq;    // pair-format activations, column c at xq + c * ldxq
-    int64_t ldx, ldxq, ldy;
-    float *y;             // outputs, column c at y + c * ldy
-    int64_t n_out;        // rows to compute (<= L.n_out)
+    int64_t ldx, ldxq;
     int nc;               // activation columns staged (== the kernel's NC)
     int64_t col_bytes;    // LDS bytes per column
 };
@@ -79,7 +93,7 @@ struct XFirst {
 // elements 16 * (tid & 15) .. +15 of it.
 __device__ inline void stage_q8k_first(const MVArgs &a, XFirst &xf) {
     const int tid = threadIdx.x;
-    const int64_t nb = a.L.n_in / 256;
+    const int64_t nb = a.n_in / 256;
     const int64_t b = tid >> 4;
     if (a.x && b < nb) {
         const float4 *src = reinterpret_cast<const float4 *>(a.x + b * 256 + (tid & 15) * 16);
@@ -106,7 +120,7 @@ __device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int l
 template <uint32_t PAIR>
 __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XFirst &xf) {
     const int tid = threadIdx.x;
-    const int64_t n = a.L.n_in;
+    const int64_t n = a.n_in;
     for (int c = 0; c < a.nc; c++) {
         uint8_t *col = lds + c * a.col_bytes;
         if constexpr (PAIR == T_Q8_K) {
@@ -224,31 +238,32 @@ struct Buf {
     Raw u[kBatch];
 };
 
+// The matvec of one matrix (segment sg) by the workgroups of its range.
 template <uint32_t FMT, int NC>
-__global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+__device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *lds) {
     constexpr bool KQ = is_kquant(FMT);
     constexpr uint32_t PAIR = (FMT == T_F16) ? T_F16
                               : (FMT == T_Q4_0 || FMT == T_Q5_0 || FMT == T_Q8_0) ? T_Q8_0
                                                                                    : T_Q8_K;
     constexpr int ITEMS = Buf<FMT>::items;
-    const Layout &L = A.L;
+    const Layout &L = sg.L;
     const int lane = threadIdx.x & 63;
     const int G = L.G;
     const int g = lane & (G - 1);
     const int r = lane >> L.logG;
     Planes P;
 #pragma unroll
-    for (int p = 0; p < 4; p++) P.p[p] = A.w + L.plane_off[p];
+    for (int p = 0; p < 4; p++) P.p[p] = sg.w + L.plane_off[p];
     const uint32_t S = (uint32_t)L.S;
     const uint32_t n_in = (uint32_t)L.n_in;
     const uint32_t last_col = (uint32_t)L.ncols - 1;
     const uint32_t col_bytes = (uint32_t)A.col_bytes;
-    const uint32_t ntiles = (uint32_t)((A.n_out + L.R - 1) / L.R);
-    const uint32_t nwaves = gridDim.x * kWaves;
+    const uint32_t ntiles = (uint32_t)((sg.n_out + L.R - 1) / L.R);
+    const uint32_t nwaves = sg.nwg * kWaves;
     // wave-uniform: keep the whole walk in scalar registers
     const uint32_t wave0 =
-        blockIdx.x * kWaves + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        (blockIdx.x - sg.wg_begin) * kWaves +
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t my_tiles = wave0 < ntiles ? (ntiles - 1 - wave0) / nwaves + 1 : 0;
     const uint32_t total = my_tiles * S;  // rounds of this wave
 
@@ -301,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
 #pragma unroll
                     for (int c = 0; c < NC; c++) {
                         const float v = group_sum(acc[c], G);
-                        if (g == 0 && row < A.n_out) A.y[c * A.ldy + row] = v;
+                        if (g == 0 && row < sg.n_out) sg.y[c * sg.ldy + row] = v;
                         acc[c] = 0.0f;
                     }
                 }
@@ -340,6 +355,22 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
     if (left == 3) issue(bufA);
     if (left >= 2) consume(bufB);
     if (left == 3) consume(bufA);
+}
+
+template <uint32_t F0, uint32_t F1, int NC>
+__global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    static_assert(pair_of(F0) == pair_of(F1), "one launch stages one activation format");
+    // segment of this workgroup (wave-uniform)
+    int s = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxSegs; i++)
+        if (i < A.nseg && blockIdx.x >= A.seg[i].wg_begin) s = i;
+    const MVSeg &sg = A.seg[s];
+    if (F0 == F1 || sg.L.type == F0)
+        matvec_body<F0, NC>(A, sg, lds);
+    else
+        matvec_body<F1, NC>(A, sg, lds);
 }
 
 // ---- standalone quantizers (global output in the reference block layouts) --

@@ -122,7 +122,7 @@ static int wgs_per_cu() {
 static int wave_target() {
     const char *e = getenv("SIHIP_WAVE_TARGET");
     const int v = e ? atoi(e) : 0;
-    return v > 0 ? v : 2048;
+    return v > 0 ? v : 1024;
 }
 
 // Columns (super-blocks for K-quants, 32-element units otherwise) per wave
@@ -220,34 +220,44 @@ extern "C" int sihip_weight_tile_cols(const sihip_weight *w) { return w ? w->L.G
 
 // ---- launches -----------------------------------------------------------------
 
-template <uint32_t FMT, int NC>
+template <uint32_t F0, uint32_t F1, int NC>
 static hipError_t launch_nc(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((matvec_kernel<FMT, NC>), dim3(grid), dim3(kThreads), lds, st, A);
+    hipLaunchKernelGGL((matvec_kernel<F0, F1, NC>), dim3(grid), dim3(kThreads), lds, st, A);
     return hipGetLastError();
 }
 
-template <uint32_t FMT>
+template <uint32_t F0, uint32_t F1>
 static hipError_t launch_fmt(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
     switch (A.nc) {
-        case 1: return launch_nc<FMT, 1>(A, grid, lds, st);
-        case 2: return launch_nc<FMT, 2>(A, grid, lds, st);
-        case 4: return launch_nc<FMT, 4>(A, grid, lds, st);
-        case 8: return launch_nc<FMT, 8>(A, grid, lds, st);
+        case 1: return launch_nc<F0, F1, 1>(A, grid, lds, st);
+        case 2: return launch_nc<F0, F1, 2>(A, grid, lds, st);
+        case 4: return launch_nc<F0, F1, 4>(A, grid, lds, st);
+        case 8: return launch_nc<F0, F1, 8>(A, grid, lds, st);
         default: return hipErrorInvalidValue;
     }
 }
 
-static hipError_t launch_any(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
-    switch (A.L.type) {
-        case T_F16:  return launch_fmt<T_F16>(A, grid, lds, st);
-        case T_Q4_0: return launch_fmt<T_Q4_0>(A, grid, lds, st);
-        case T_Q5_0: return launch_fmt<T_Q5_0>(A, grid, lds, st);
-        case T_Q8_0: return launch_fmt<T_Q8_0>(A, grid, lds, st);
-        case T_Q2_K: return launch_fmt<T_Q2_K>(A, grid, lds, st);
-        case T_Q3_K: return launch_fmt<T_Q3_K>(A, grid, lds, st);
-        case T_Q4_K: return launch_fmt<T_Q4_K>(A, grid, lds, st);
-        case T_Q5_K: return launch_fmt<T_Q5_K>(A, grid, lds, st);
-        case T_Q6_K: return launch_fmt<T_Q6_K>(A, grid, lds, st);
+// Format pairs one launch can mix (the K-quant mixes of Q4_K_M / Q5_K_M
+// models); f0 < f1.
+static bool mix_supported(uint32_t f0, uint32_t f1) {
+    return f0 == f1 || (f0 == T_Q4_K && f1 == T_Q6_K) || (f0 == T_Q5_K && f1 == T_Q6_K);
+}
+
+static hipError_t launch_any(const MVArgs &A, uint32_t f0, uint32_t f1, int grid, size_t lds,
+                             hipStream_t st) {
+    if (f0 == T_Q4_K && f1 == T_Q6_K) return launch_fmt<T_Q4_K, T_Q6_K>(A, grid, lds, st);
+    if (f0 == T_Q5_K && f1 == T_Q6_K) return launch_fmt<T_Q5_K, T_Q6_K>(A, grid, lds, st);
+    if (f0 != f1) return hipErrorInvalidValue;
+    switch (f0) {
+        case T_F16:  return launch_fmt<T_F16, T_F16>(A, grid, lds, st);
+        case T_Q4_0: return launch_fmt<T_Q4_0, T_Q4_0>(A, grid, lds, st);
+        case T_Q5_0: return launch_fmt<T_Q5_0, T_Q5_0>(A, grid, lds, st);
+        case T_Q8_0: return launch_fmt<T_Q8_0, T_Q8_0>(A, grid, lds, st);
+        case T_Q2_K: return launch_fmt<T_Q2_K, T_Q2_K>(A, grid, lds, st);
+        case T_Q3_K: return launch_fmt<T_Q3_K, T_Q3_K>(A, grid, lds, st);
+        case T_Q4_K: return launch_fmt<T_Q4_K, T_Q4_K>(A, grid, lds, st);
+        case T_Q5_K: return launch_fmt<T_Q5_K, T_Q5_K>(A, grid, lds, st);
+        case T_Q6_K: return launch_fmt<T_Q6_K, T_Q6_K>(A, grid, lds, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -264,45 +274,85 @@ static int max_cols(const sihip_ctx *ctx, uint32_t pair, int64_t n_in) {
     return 0;
 }
 
-// Run the matvec for columns [0, M) of x (f32, ldx) or xq (pair format,
-// ldxq) into y (ldy), splitting M into launches of 8/4/2/1 columns.
-static int run_matvec(sihip_ctx *ctx, const sihip_weight *w, const float *x, int64_t ldx,
-                      const uint8_t *xq, int64_t ldxq, int64_t M, float *y, int64_t ldy,
-                      int64_t n_out, hipStream_t st) {
-    const Layout &L = w->L;
-    const uint32_t pair = pair_of(L.type);
-    const int ncmax = max_cols(ctx, pair, L.n_in);
+// One launch computes `count` matrices against the same activation
+// columns [0, M) of x (f32, ldx) or xq (pair format, ldxq); matrix i writes
+// rows [0, n_out[i]) of y[i] (column stride ldy[i]). The caller checks that
+// the matrices share n_in and that mix_supported() holds for their formats.
+// M is split into launches of 8/4/2/1 columns.
+static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const *w,
+                            const int64_t *n_out, float *const *y, const int64_t *ldy,
+                            const float *x, int64_t ldx, const uint8_t *xq, int64_t ldxq,
+                            int64_t M, hipStream_t st) {
+    const int64_t n_in = w[0]->L.n_in;
+    const uint32_t pair = pair_of(w[0]->L.type);
+    uint32_t f0 = w[0]->L.type, f1 = w[0]->L.type;
+    for (int i = 1; i < count; i++) {
+        const uint32_t t = w[i]->L.type;
+        if (t < f0) f0 = t;
+        if (t > f1) f1 = t;
+    }
+    int ncmax = max_cols(ctx, pair, n_in);
     if (ncmax == 0)
         return set_err(ctx, SIHIP_ERANGE, "activation row of %lld does not fit in LDS",
-                       (long long)L.n_in);
-    const int64_t cb = col_bytes_aligned(pair, L.n_in);
-    const int64_t R = L.R;
-    const int64_t ntiles = (n_out + R - 1) / R;
-    int64_t wgs = (ntiles + kWaves - 1) / kWaves;
+                       (long long)n_in);
+    if (is_kquant(f1) && ncmax > 4) ncmax = 4;  // 8 K-quant columns exceed the VGPR file
+    const int64_t cb = col_bytes_aligned(pair, n_in);
+    // workgroups: one row tile per wave when the chip has room; otherwise
+    // each matrix gets a share of the cap proportional to its bytes
     const int64_t wg_cap = (int64_t)ctx->n_cu * wgs_per_cu();
-    if (wgs > wg_cap) wgs = wg_cap;
+    int64_t want[kMaxSegs], nwg[kMaxSegs], want_sum = 0, bytes_sum = 0;
+    for (int i = 0; i < count; i++) {
+        const int64_t ntiles = (n_out[i] + w[i]->L.R - 1) / w[i]->L.R;
+        want[i] = (ntiles + kWaves - 1) / kWaves;
+        want_sum += want[i];
+        bytes_sum += w[i]->L.total_bytes;
+    }
+    for (int i = 0; i < count; i++) {
+        nwg[i] = want[i];
+        if (want_sum > wg_cap) {
+            const int64_t share = (int64_t)((double)wg_cap * (double)w[i]->L.total_bytes /
+                                            (double)bytes_sum);
+            nwg[i] = share < 1 ? 1 : (share < want[i] ? share : want[i]);
+        }
+    }
     int64_t m = 0;
     while (m < M) {
         int nc = ncmax;
         while (nc > 1 && m + nc > M) nc >>= 1;
         MVArgs A;
-        A.w = w->dev;
-        A.L = L;
+        memset(&A, 0, sizeof(A));
+        uint32_t wg = 0;
+        for (int i = 0; i < count; i++) {
+            MVSeg &sg = A.seg[i];
+            sg.w = w[i]->dev;
+            sg.L = w[i]->L;
+            sg.y = y[i] + m * ldy[i];
+            sg.ldy = ldy[i];
+            sg.n_out = n_out[i];
+            sg.wg_begin = wg;
+            sg.nwg = (uint32_t)nwg[i];
+            wg += (uint32_t)nwg[i];
+        }
+        A.nseg = count;
+        A.n_in = n_in;
         A.x = x ? x + m * ldx : nullptr;
         A.xq = xq ? xq + m * ldxq : nullptr;
         A.ldx = ldx;
         A.ldxq = ldxq;
-        A.ldy = ldy;
-        A.y = y + m * ldy;
-        A.n_out = n_out;
         A.nc = nc;
         A.col_bytes = cb;
-        const hipError_t e = launch_any(A, (int)wgs, (size_t)(cb * nc), st);
+        const hipError_t e = launch_any(A, f0, f1, (int)wg, (size_t)(cb * nc), st);
         if (e != hipSuccess)
             return set_err(ctx, SIHIP_EDEVICE, "matvec launch: %s", hipGetErrorString(e));
         m += nc;
     }
     return SIHIP_OK;
+}
+
+static int run_matvec(sihip_ctx *ctx, const sihip_weight *w, const float *x, int64_t ldx,
+                      const uint8_t *xq, int64_t ldxq, int64_t M, float *y, int64_t ldy,
+                      int64_t n_out, hipStream_t st) {
+    return run_matvec_multi(ctx, 1, &w, &n_out, &y, &ldy, x, ldx, xq, ldxq, M, st);
 }
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -329,17 +379,77 @@ extern "C" int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float
 
 extern "C" int sihip_gemv_multi_dev(sihip_ctx *ctx, int count, const sihip_weight *const *w,
                                     const float *x, float *const *y, void *stream) {
-    if (!ctx || !w || !x || !y || count < 1 || count > 4)
+    if (!ctx || !w || !x || !y || count < 1 || count > kMaxSegs)
         return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: bad arguments");
+    if (!aligned16(x)) return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: x must be 16-byte aligned");
     for (int i = 0; i < count; i++) {
         if (!w[i] || !y[i]) return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: NULL weight/output");
         if (w[i]->L.n_in != w[0]->L.n_in)
             return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: n_in differs between weights");
+        if (pair_of(w[i]->L.type) != pair_of(w[0]->L.type))
+            return set_err(ctx, SIHIP_EINVAL, "gemv_multi_dev: activation formats differ");
     }
+    // formats one launch can mix; otherwise one launch per distinct format
+    uint32_t f0 = w[0]->L.type, f1 = w[0]->L.type;
+    for (int i = 1; i < count; i++) {
+        if (w[i]->L.type < f0) f0 = w[i]->L.type;
+        if (w[i]->L.type > f1) f1 = w[i]->L.type;
+    }
+    bool fused = mix_supported(f0, f1);
+    for (int i = 0; i < count && fused; i++)
+        fused = w[i]->L.type == f0 || w[i]->L.type == f1;
+    int64_t n_out[kMaxSegs], ldy[kMaxSegs];
+    for (int i = 0; i < count; i++) n_out[i] = ldy[i] = w[i]->L.n_out;
+    if (fused)
+        return run_matvec_multi(ctx, count, w, n_out, y, ldy, x, w[0]->L.n_in, nullptr, 0, 1,
+                                (hipStream_t)stream);
     for (int i = 0; i < count; i++) {
         const int rc = sihip_gemv_dev(ctx, w[i], x, y[i], w[i]->L.n_out, stream);
         if (rc) return rc;
     }
+    return SIHIP_OK;
+}
+
+// ---- device memory ---------------------------------------------------------------
+
+extern "C" int sihip_dev_alloc(sihip_ctx *ctx, uint64_t bytes, void **dptr) {
+    if (!ctx || !dptr || bytes == 0) return set_err(ctx, SIHIP_EINVAL, "dev_alloc: bad arguments");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    void *p = nullptr;
+    const hipError_t e = hipMalloc(&p, (size_t)bytes);
+    if (e != hipSuccess)
+        return set_err(ctx, SIHIP_ENOMEM, "dev_alloc(%llu): %s", (unsigned long long)bytes,
+                       hipGetErrorString(e));
+    *dptr = p;
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_dev_free(sihip_ctx *ctx, void *dptr) {
+    if (!ctx) return SIHIP_EINVAL;
+    if (!dptr) return SIHIP_OK;
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    HIP_OK(ctx, hipFree(dptr));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_memcpy_htod(sihip_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
+    if (!ctx || !dst || !src) return set_err(ctx, SIHIP_EINVAL, "memcpy_htod: NULL argument");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    HIP_OK(ctx, hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_memcpy_dtoh(sihip_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
+    if (!ctx || !dst || !src) return set_err(ctx, SIHIP_EINVAL, "memcpy_dtoh: NULL argument");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    HIP_OK(ctx, hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_synchronize(sihip_ctx *ctx) {
+    if (!ctx) return SIHIP_EINVAL;
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    HIP_OK(ctx, hipDeviceSynchronize());
     return SIHIP_OK;
 }
 

@@ -169,3 +169,42 @@ def test_errors_leave_outputs_untouched(dev):
             dev.gemv(w, np.zeros(256, np.float32), n_out=17)  # more rows than uploaded
     finally:
         w.free()
+
+
+@pytest.mark.parametrize("combo", [
+    (sa.Q4_K, sa.Q4_K, sa.Q6_K),        # Q4_K_M attention q, k, v: one mixed launch
+    (sa.Q4_K, sa.Q4_K),                 # ffn gate + up
+    (sa.Q8_0, sa.Q5_0, sa.Q4_0),        # no mixed kernel: one launch per matrix
+    (sa.Q5_K, sa.Q6_K, sa.Q5_K, sa.Q6_K),
+], ids=lambda c: "+".join(sa.NAMES[t] for t in c))
+def test_gemv_multi_matches_single_and_oracle(dev, oracle, combo):
+    """Several matrices sharing one activation in one call give bit-identical
+    results to one gemv per matrix (row tiles and their reduction order do
+    not depend on how workgroups are shared out), and match the oracle."""
+    rng = np.random.default_rng(77 + len(combo))
+    n_in = 2048
+    shapes = [(wt, int(n)) for wt, n in zip(combo, rng.integers(100, 1500, len(combo)))]
+    Ws = [synth.make_weights(wt, n, n_in, rng) for wt, n in shapes]
+    ws = [dev.upload(wt, n, n_in, W) for (wt, n), W in zip(shapes, Ws)]
+    bufs = []
+    try:
+        x = rng.standard_normal(n_in).astype(np.float32)
+        xd = dev.to_device(x)
+        nan = lambda n: np.full(n, np.nan, np.float32)  # noqa: E731
+        ys = [dev.to_device(nan(n)) for _, n in shapes]
+        singles = [dev.to_device(nan(n)) for _, n in shapes]
+        bufs = [xd, *ys, *singles]
+        dev.gemv_multi_dev(ws, xd.ptr, [y.ptr for y in ys])
+        for w, y, (_, n) in zip(ws, singles, shapes):
+            dev.gemv_dev(w, xd.ptr, y.ptr, n)
+        dev.synchronize()
+        for (wt, n), W, y, y1 in zip(shapes, Ws, ys, singles):
+            a, b = y.to_host(np.float32, n), y1.to_host(np.float32, n)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), sa.NAMES[wt]
+            ref, l1 = oracle.gemv(wt, W, n, n_in, x)
+            assert_close(a, ref.astype(np.float64), l1, f"multi {sa.NAMES[wt]} {n}x{n_in}")
+    finally:
+        for b in bufs:
+            b.free()
+        for w in ws:
+            w.free()
