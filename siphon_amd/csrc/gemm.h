@@ -1,0 +1,314 @@
+// Prefill GEMM on the matrix cores of gfx950: Y[M x n_out] = X[M x n_in] *
+// W^T for K-quant weights, with X quantized per row to Q8_K by the same
+// bit-exact quantizer as the matvec path (reference kernels.c:561-595).
+//
+// Arithmetic (per 256-element super-block c, weight row n, activation row
+// m), restating the reference dot (reference kernels.c:349-410 for Q4_K):
+//   S[m,n] = sum_j sc_j[n] * sum_{k in unit j} q[n,k] * x[m,k]      (exact int)
+//   T[m,n] = sum_g mn_{g/2}[n] * bsum_g[m]                            (exact)
+//   y[m,n] += dx[m,c] * d[n,c] * S - dx[m,c] * dmin[n,c] * T
+// S runs on v_mfma_i32_32x32x32_i8, one MFMA per 32-element unit. The 6-bit
+// unit scale is split as sc = 8 * sh + sl (sh, sl in 0..7) so that both
+// weight operands sh * q and sl * q fit in int8 (<= 105): two MFMAs per
+// unit accumulate 8 * H + L = S exactly in int32. T runs on one
+// v_mfma_f32_32x32x16_f16 per super-block (mins <= 63 and group sums
+// |bsum| <= 2032 are exact in f16, and every partial sum stays below 2^24,
+// so the f32 result is exact). Only the per-super-block f32 epilogue rounds.
+//
+// MFMA operand layout (gfx950, checked on the device): for the 32x32x32 i8
+// and 32x32x16 f16 forms lane l supplies row (l % 32) of A and column
+// (l % 32) of B at the k positions of its half h = l / 32; A and B use the
+// same k positions, so any consistent assignment of unit elements to the
+// (h, slot) pairs is valid. Accumulator register r of lane l holds
+// D[8 * (r / 4) + 4 * h + r % 4][l % 32]. Here A is the activation tile
+// (rows m) and B the weight tile (columns n), so every lane owns one weight
+// row n and its scales.
+//
+// Element assignment: lane half h takes unit elements 8h..8h+7 and
+// 16+8h..16+8h+7. For the weights these are exactly the low and high nibbles
+// of bytes 8h..8h+7 of the nib16 unit record (formats.h); the activation
+// quants are stored with each unit permuted to [0..7, 16..23, 8..15, 24..31]
+// so a lane's 16 bytes are contiguous.
+#pragma once
+
+#include "formats.h"
+#include "quant.h"
+#include "unit.h"
+
+namespace sihip {
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kGemmThreads = 256;
+#ifndef SIHIP_GEMM_MT
+#define SIHIP_GEMM_MT 2
+#endif
+constexpr int kGemmBM = 32 * SIHIP_GEMM_MT;    // activation rows per workgroup
+constexpr int kGemmBN = 128;                   // weight rows per workgroup (32 per wave)
+constexpr int kGemmMT = kGemmBM / 32;          // 32-row MFMA tiles per wave along m
+constexpr int kGemmWaves = kGemmMT <= 2 ? 2 : 1;  // waves per SIMD the registers allow
+constexpr int kXRow = 256 + 16;                // LDS bytes per activation row (padded)
+constexpr int kXQBytes = kGemmBM * kXRow;      // quant tile
+constexpr int kXDOff = kXQBytes;               // f32 dx[BM]
+constexpr int kXBOff = kXDOff + kGemmBM * 4;   // f16 bsums[BM][16]
+constexpr int kXTile = kXBOff + kGemmBM * 32;  // one LDS buffer
+
+// Activation planes written by gemm_quantize_x (Mp = M rounded up to BM;
+// rows M..Mp-1 are zero).
+struct GemmX {
+    int8_t *q;       // [Mp][K] quants, units permuted as described above
+    float *d;        // [K/256][Mp] block scales
+    _Float16 *bs;    // [K/256][Mp][16] group sums
+};
+
+struct GemmArgs {
+    const uint8_t *wq;   // unit plane (nib16 records)
+    const uint8_t *wm;   // block plane (d | dmin | scales[12])
+    int R, G, logG;
+    int64_t S;           // matvec layout rounds per tile
+    int64_t n_out, nb;   // weight rows, super-blocks per row
+    int64_t M, Mp;
+    GemmX X;
+    float *y;
+    int64_t ldy;
+    int MB, NB;          // workgroup tiles along m and n
+};
+
+__host__ __device__ inline int64_t gemm_x_bytes(int64_t Mp, int64_t K) {
+    return Mp * K + (K / 256) * Mp * 4 + (K / 256) * Mp * 32;
+}
+
+// One 16-lane row per Q8_K block of X (row m, super-block c); rows past M
+// write zeros. Grid: ceil(Mp * nb / 16) workgroups of 256.
+__global__ __launch_bounds__(kGemmThreads) void gemm_quantize_x(const float *x, int64_t ldx,
+                                                                int64_t M, int64_t Mp,
+                                                                int64_t nb, GemmX X) {
+    const int lane16 = threadIdx.x & 15;
+    const int64_t blk = (int64_t)blockIdx.x * (kGemmThreads / 16) + (threadIdx.x >> 4);
+    if (blk >= Mp * nb) return;  // whole 16-lane rows leave together
+    const int64_t m = blk / nb, c = blk % nb;
+    const int64_t K = nb * 256;
+    Q8KRow r;
+    if (m < M) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + m * ldx + c * 256 + lane16 * 16);
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 t = src[i];
+            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
+        r = q8k_block_row16(v, lane16);
+    } else {
+        r.q = make_uint4(0, 0, 0, 0);
+        r.gsum = 0;
+        r.d = 0.0f;
+    }
+    // this lane holds elements 16 * (lane16 & 1) .. +15 of unit lane16 / 2
+    int8_t *unit = X.q + m * K + c * 256 + (lane16 >> 1) * 32;
+    const int half = lane16 & 1;
+    *reinterpret_cast<uint2 *>(unit + 8 * half) = make_uint2(r.q.x, r.q.y);
+    *reinterpret_cast<uint2 *>(unit + 16 + 8 * half) = make_uint2(r.q.z, r.q.w);
+    X.bs[(c * Mp + m) * 16 + lane16] = (_Float16)(float)r.gsum;
+    if (lane16 == 0) X.d[c * Mp + m] = r.d;
+}
+
+// Weight data of one super-block for this lane's row: 8 unit halves and
+// the block record.
+struct GemmW {
+    uint2 u[8];
+    U4 m;
+};
+
+// Records of (row, c) in the matvec layout (formats.h col_rec): unit k at
+// ((tile * S + s) * 8 + k) * 64 + r * G + g and the block at
+// (tile * S + s) * 64 + r * G + g, with s = c >> logG, g = c & (G - 1).
+// ub = tile * S * 512 + r * G and bb = tile * S * 64 + r * G are per row.
+__device__ inline void gemm_load_w(const GemmArgs &A, uint32_t ub, uint32_t bb, int64_t c, int h,
+                                   GemmW &w) {
+    const uint32_t s = (uint32_t)(c >> A.logG), g = (uint32_t)(c & (A.G - 1));
+    const uint32_t urec = ub + s * 512u + g;
+    const uint32_t brec = bb + s * 64u + g;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        w.u[k] = *reinterpret_cast<const uint2 *>(A.wq + (urec + 64u * (uint32_t)k) * 16u + 8u * (uint32_t)h);
+    w.m = *reinterpret_cast<const U4 *>(A.wm + brec * 16u);
+}
+
+constexpr int kXPieces = kGemmBM * 16 / kGemmThreads;  // 16-byte quant pieces per thread
+constexpr int kXE = kGemmBM * 2 + kGemmBM / 4;  // 16-byte pieces of group sums + scales
+constexpr int kXEPieces = (kXE + kGemmThreads - 1) / kGemmThreads;
+
+__device__ inline uint32_t bytes_times(uint32_t q, uint32_t f) {
+    // bytewise q * f for bytes and products below 256 (no carries between bytes)
+    const u16x2_t a = __builtin_bit_cast(u16x2_t, q);
+    const u16x2_t b = {(unsigned short)f, (unsigned short)f};
+    return __builtin_bit_cast(uint32_t, (u16x2_t)(a * b));
+}
+
+template <uint32_t FMT>
+__global__ __launch_bounds__(kGemmThreads)
+__attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel(GemmArgs A) {
+    static_assert(FMT == T_Q4_K, "MFMA prefill: Q4_K");
+    __shared__ __attribute__((aligned(16))) uint8_t sx[2][kXTile];
+    // XCD-aware tile order: workgroups are dispatched round-robin over the 8
+    // XCDs, so the m-tiles of one n-tile (which read the same weights) are
+    // given to consecutive workgroups of the same XCD and share its L2.
+    const int b = blockIdx.x;
+    const int xcd = b & 7, t = b >> 3;
+    const int nblk = (t / A.MB) * 8 + xcd, mblk = t % A.MB;
+    if (nblk >= A.NB) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ln = lane & 31, h = lane >> 5;
+    const int64_t m0 = (int64_t)mblk * kGemmBM;
+    const int64_t n = (int64_t)nblk * kGemmBN + wave * 32 + ln;  // this lane's weight row
+    const int64_t nl = n < A.n_out ? n : A.n_out - 1;            // loads stay in the matrix
+    const uint32_t tS = (uint32_t)((nl / A.R) * A.S), rg = (uint32_t)((nl % A.R) * A.G);
+    const uint32_t ub = tS * 512u + rg, bb = tS * 64u + rg;
+
+    v16f_t y[kGemmMT];
+#pragma unroll
+    for (int i = 0; i < kGemmMT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) y[i][r] = 0.0f;
+
+    // one super-block: weights w (this lane's row), activation tile in buf
+    auto compute = [&](const uint8_t *buf, const GemmW &w) {
+        int sc[8], mn[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) k4_scale_min(w.m, j, sc[j], mn[j]);
+        const float d = half_to_float(w.m.x & 0xffffu);
+        const float dmin = half_to_float(w.m.x >> 16);
+        v16i_t acc_h[kGemmMT], acc_l[kGemmMT];
+#pragma unroll
+        for (int i = 0; i < kGemmMT; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc_h[i][r] = acc_l[i][r] = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
+            const uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
+            const uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
+            const uint32_t sh = (uint32_t)sc[j] >> 3, sl = (uint32_t)sc[j] & 7u;
+            const v4i_t bh = {(int)bytes_times(q0, sh), (int)bytes_times(q1, sh),
+                              (int)bytes_times(q2, sh), (int)bytes_times(q3, sh)};
+            const v4i_t bl = {(int)bytes_times(q0, sl), (int)bytes_times(q1, sl),
+                              (int)bytes_times(q2, sl), (int)bytes_times(q3, sl)};
+#pragma unroll
+            for (int i = 0; i < kGemmMT; i++) {
+                const v4i_t av = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 32 * j + 16 * h);
+                acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, acc_h[i], 0, 0, 0);
+                acc_l[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, acc_l[i], 0, 0, 0);
+            }
+        }
+        // mins against the group sums: slot s of half h is group 8h + s
+        v8h_t bm;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            // min of unit 4h + s (reference kernels.c:648-656), selected
+            // arithmetically so no private array is indexed by the lane half
+            const int lo = (int)((w.m.z >> (8 * s)) & 63u);
+            const int hi = (int)(((w.m.w >> (8 * s + 4)) & 15u) | (((w.m.z >> (8 * s + 6)) & 3u) << 4));
+            const _Float16 v = (_Float16)(float)(h ? hi : lo);
+            bm[2 * s] = v;
+            bm[2 * s + 1] = v;
+        }
+        const float *dx = reinterpret_cast<const float *>(buf + kXDOff);
+#pragma unroll
+        for (int i = 0; i < kGemmMT; i++) {
+            const v8h_t abs_ = *reinterpret_cast<const v8h_t *>(buf + kXBOff + (32 * i + ln) * 32 + 16 * h);
+            v16f_t tz;
+#pragma unroll
+            for (int r = 0; r < 16; r++) tz[r] = 0.0f;
+            const v16f_t T = __builtin_amdgcn_mfma_f32_32x32x16_f16(abs_, bm, tz, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float dxr = dx[32 * i + 8 * (r / 4) + 4 * h + (r % 4)];
+                const int S = 8 * acc_h[i][r] + acc_l[i][r];
+                // y += dx * (d * S - dmin * T)
+                const float u = fma_f32(-dmin, T[r], d * (float)S);
+                y[i][r] = fma_f32(dxr, u, y[i][r]);
+            }
+        }
+    };
+
+    // Activation tile of super-block c (rows m0..m0+BM-1) from the planes
+    // into registers: BM/16 pieces of 16 quant bytes per thread and one
+    // piece of the group sums (pieces 0..2BM-1) or scales (the next BM/4)
+    // per thread; threads past them load the last piece again and do not
+    // store it, so no load is predicated.
+    v4i_t xq[kXPieces], xe[kXEPieces];
+    const int tid = threadIdx.x;
+    const int64_t K = A.nb * 256;
+    auto load_x = [&](int64_t c) {
+#pragma unroll
+        for (int i = 0; i < kXPieces; i++) {
+            const int piece = tid + 256 * i, row = piece >> 4, col = piece & 15;
+            xq[i] = *reinterpret_cast<const v4i_t *>(A.X.q + (m0 + row) * K + c * 256 + col * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < kXEPieces; i++) {
+            const int t = tid + 256 * i;
+            const int p = t < kXE - 1 ? t : kXE - 1;
+            const v4i_t *e = p < 2 * kGemmBM
+                                 ? reinterpret_cast<const v4i_t *>(A.X.bs + (c * A.Mp + m0) * 16) + p
+                                 : reinterpret_cast<const v4i_t *>(A.X.d + c * A.Mp + m0) + (p - 2 * kGemmBM);
+            xe[i] = *e;
+        }
+    };
+    auto store_x = [&](uint8_t *buf) {
+#pragma unroll
+        for (int i = 0; i < kXPieces; i++) {
+            const int piece = tid + 256 * i, row = piece >> 4, col = piece & 15;
+            *reinterpret_cast<v4i_t *>(buf + row * kXRow + col * 16) = xq[i];
+        }
+        // group sums (pieces 0 .. 2BM-1) follow the scales (BM / 4 pieces)
+#pragma unroll
+        for (int i = 0; i < kXEPieces; i++) {
+            const int t = tid + 256 * i;
+            if (t < kXE)
+                reinterpret_cast<v4i_t *>(buf + kXDOff + (t < 2 * kGemmBM ? kGemmBM * 4 : -kGemmBM * 32))[t] = xe[i];
+        }
+    };
+
+    // Two weight buffers and two LDS activation buffers in ping-pong: the
+    // loads of super-block c + 1 are issued before super-block c is
+    // computed. Loads are unconditional (past the end they repeat the last
+    // super-block), so the memory counters always hold them in issue order.
+    const int64_t last = A.nb - 1;
+    GemmW wa, wb;
+    load_x(0);
+    gemm_load_w(A, ub, bb, 0, h, wa);
+    store_x(sx[0]);
+    __syncthreads();
+    for (int64_t c = 0;; c += 2) {
+        const int64_t c1 = c + 1 < last ? c + 1 : last;
+        load_x(c1);
+        gemm_load_w(A, ub, bb, c1, h, wb);
+        compute(sx[0], wa);
+        store_x(sx[1]);
+        __syncthreads();
+        if (c + 1 > last) break;
+        const int64_t c2 = c + 2 < last ? c + 2 : last;
+        load_x(c2);
+        gemm_load_w(A, ub, bb, c2, h, wa);
+        compute(sx[1], wb);
+        store_x(sx[0]);
+        __syncthreads();
+        if (c + 2 > last) break;
+    }
+    if (n < A.n_out) {
+#pragma unroll
+        for (int i = 0; i < kGemmMT; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = m0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
+                if (m < A.M) A.y[m * A.ldy + n] = y[i][r];
+            }
+    }
+}
+
+}  // namespace sihip

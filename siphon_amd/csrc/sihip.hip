@@ -15,6 +15,7 @@
 
 #include "../../include/sihip.h"
 #include "formats.h"
+#include "gemm.h"
 #include "matvec.h"
 #include "quant.h"
 
@@ -32,6 +33,8 @@ struct sihip_ctx {
     size_t d_out_cap = 0;
     void *d_aux = nullptr;
     size_t d_aux_cap = 0;
+    void *d_ws = nullptr;  // prefill GEMM: quantized activation planes
+    size_t d_ws_cap = 0;
 };
 
 struct sihip_weight {
@@ -103,6 +106,7 @@ extern "C" void sihip_shutdown(sihip_ctx *ctx) {
     if (ctx->d_in) (void)hipFree(ctx->d_in);
     if (ctx->d_out) (void)hipFree(ctx->d_out);
     if (ctx->d_aux) (void)hipFree(ctx->d_aux);
+    if (ctx->d_ws) (void)hipFree(ctx->d_ws);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -357,6 +361,70 @@ static int run_matvec(sihip_ctx *ctx, const sihip_weight *w, const float *x, int
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// ---- prefill GEMM on MFMA -----------------------------------------------------
+
+// Smallest M that takes the MFMA GEMM (below it the matvec kernel streams
+// the weights once per 1-4 columns, which is cheaper). SIHIP_GEMM_MIN_M
+// overrides it (tests force both paths).
+static int64_t gemm_min_m() {
+    const char *e = getenv("SIHIP_GEMM_MIN_M");
+    const long v = e ? atol(e) : 0;
+    return v > 0 ? v : 16;
+}
+
+static bool gemm_mfma_supported(uint32_t type) { return type == T_Q4_K; }
+
+// Y[m, :] = W x[m, :] for m < M on the matrix cores. The activation planes
+// live in the context's workspace, so calls on one context must not overlap.
+static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64_t ldx,
+                         int64_t M, float *Y, int64_t ldy, hipStream_t st) {
+    const Layout &L = w->L;
+    const int64_t K = L.n_in, nb = K / 256;
+    const int64_t Mp = (M + kGemmBM - 1) / kGemmBM * kGemmBM;
+    const int64_t ws = gemm_x_bytes(Mp, K);
+    int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)ws);
+    if (rc) return rc;
+    GemmX XP;
+    XP.q = (int8_t *)ctx->d_ws;
+    XP.d = (float *)((uint8_t *)ctx->d_ws + Mp * K);
+    XP.bs = (_Float16 *)((uint8_t *)ctx->d_ws + Mp * K + nb * Mp * 4);
+    const int64_t blocks = Mp * nb;
+    hipLaunchKernelGGL(gemm_quantize_x, dim3((unsigned)((blocks + 15) / 16)), dim3(kGemmThreads), 0,
+                       st, X, ldx, M, Mp, nb, XP);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm quantize: %s", hipGetErrorString(e));
+    GemmArgs A;
+    A.wq = w->dev + L.plane_off[0];
+    A.wm = w->dev + L.plane_off[1];
+    A.R = L.R;
+    A.G = L.G;
+    A.logG = L.logG;
+    A.S = L.S;
+    A.n_out = L.n_out;
+    A.nb = nb;
+    A.M = M;
+    A.Mp = Mp;
+    A.X = XP;
+    A.y = Y;
+    A.ldy = ldy;
+    A.MB = (int)(Mp / kGemmBM);
+    A.NB = (int)((L.n_out + kGemmBN - 1) / kGemmBN);
+    const int64_t grid = (int64_t)8 * ((A.NB + 7) / 8) * A.MB;
+    hipLaunchKernelGGL(gemm_kq_kernel<T_Q4_K>, dim3((unsigned)grid), dim3(kGemmThreads), 0, st, A);
+    e = hipGetLastError();
+    if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+    return SIHIP_OK;
+}
+
+// Prefill dispatch: MFMA GEMM where supported and M is large enough,
+// otherwise the matvec kernel over column groups.
+static int run_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64_t M, float *Y,
+                    hipStream_t st) {
+    if (gemm_mfma_supported(w->L.type) && M >= gemm_min_m())
+        return run_gemm_mfma(ctx, w, X, w->L.n_in, M, Y, w->L.n_out, st);
+    return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out, st);
+}
+
 extern "C" int sihip_gemv_dev(sihip_ctx *ctx, const sihip_weight *w, const float *x, float *y,
                               int64_t n_out, void *stream) {
     if (!ctx || !w || !x || !y) return set_err(ctx, SIHIP_EINVAL, "gemv_dev: NULL argument");
@@ -373,8 +441,7 @@ extern "C" int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float
     if (!ctx || !w || !X || !Y) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: NULL argument");
     if (M <= 0) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: M must be positive");
     if (!aligned16(X)) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: X must be 16-byte aligned");
-    return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out,
-                      (hipStream_t)stream);
+    return run_gemm(ctx, w, X, M, Y, (hipStream_t)stream);
 }
 
 extern "C" int sihip_gemv_multi_dev(sihip_ctx *ctx, int count, const sihip_weight *const *w,
@@ -486,8 +553,7 @@ extern "C" int sihip_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X,
     rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, yb);
     if (rc) return rc;
     HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, X, xb, hipMemcpyHostToDevice, ctx->stream));
-    rc = run_matvec(ctx, w, (const float *)ctx->d_in, w->L.n_in, nullptr, 0, M,
-                    (float *)ctx->d_out, w->L.n_out, w->L.n_out, ctx->stream);
+    rc = run_gemm(ctx, w, (const float *)ctx->d_in, M, (float *)ctx->d_out, ctx->stream);
     if (rc) return rc;
     HIP_OK(ctx, hipMemcpyAsync(Y, ctx->d_out, yb, hipMemcpyDeviceToHost, ctx->stream));
     HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
