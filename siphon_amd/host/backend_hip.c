@@ -1,0 +1,220 @@
+/* The "hip" si_backend: C17 adapter from Siphon's backend vtable to the
+ * C-ABI of libsiphon_hip.so (include/sihip.h). See si_hip_backend.h. */
+#include "si_hip_backend.h"
+
+#include <dlfcn.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "sihip.h"
+
+/* entry points resolved from the library */
+typedef struct {
+    int (*abi_version)(void);
+    int (*init)(int, sihip_ctx **);
+    void (*shutdown)(sihip_ctx *);
+    const char *(*last_error)(const sihip_ctx *);
+    int (*weight_upload)(sihip_ctx *, uint32_t, uint64_t, uint64_t, const void *, uint64_t,
+                         sihip_weight **);
+    int (*weight_free)(sihip_ctx *, sihip_weight *);
+    uint64_t (*weight_device_bytes)(const sihip_weight *);
+    int (*gemv)(sihip_ctx *, const sihip_weight *, const float *, float *, int64_t);
+    int (*gemm)(sihip_ctx *, const sihip_weight *, const float *, int64_t, float *);
+} hip_fns;
+
+/* one uploaded tensor, keyed by its mmap data pointer */
+typedef struct {
+    const void *data;
+    sihip_weight *w;
+} slot;
+
+typedef struct {
+    si_backend base;  /* first member: the engine sees a plain si_backend */
+    void *dl;
+    hip_fns f;
+    sihip_ctx *ctx;
+    slot *slots;      /* open addressing, capacity a power of two */
+    size_t cap, n;
+} hip_backend;
+
+static hip_backend *as_hip(si_backend *be) { return (hip_backend *)be; }
+
+static size_t slot_hash(const void *p, size_t cap) {
+    uint64_t v = (uint64_t)(uintptr_t)p;
+    v ^= v >> 33;
+    v *= 0xff51afd7ed558ccdULL;
+    v ^= v >> 33;
+    return (size_t)v & (cap - 1);
+}
+
+static slot *slot_find(hip_backend *hb, const void *data) {
+    if (!hb->cap) return NULL;
+    for (size_t i = slot_hash(data, hb->cap);; i = (i + 1) & (hb->cap - 1)) {
+        if (hb->slots[i].data == data) return &hb->slots[i];
+        if (!hb->slots[i].data) return NULL;
+    }
+}
+
+static int slot_insert(hip_backend *hb, const void *data, sihip_weight *w) {
+    if ((hb->n + 1) * 2 > hb->cap) {
+        const size_t ncap = hb->cap ? hb->cap * 2 : 64;
+        slot *ns = calloc(ncap, sizeof *ns);
+        if (!ns) return SI_ENOMEM;
+        for (size_t i = 0; i < hb->cap; i++) {
+            if (!hb->slots[i].data) continue;
+            size_t j = slot_hash(hb->slots[i].data, ncap);
+            while (ns[j].data) j = (j + 1) & (ncap - 1);
+            ns[j] = hb->slots[i];
+        }
+        free(hb->slots);
+        hb->slots = ns;
+        hb->cap = ncap;
+    }
+    size_t j = slot_hash(data, hb->cap);
+    while (hb->slots[j].data) j = (j + 1) & (hb->cap - 1);
+    hb->slots[j].data = data;
+    hb->slots[j].w = w;
+    hb->n++;
+    return SI_OK;
+}
+
+/* Map an SIHIP_* code (same values as SI_*; SIHIP_EDEVICE is extra) to SI_*. */
+static int si_code(int rc) { return rc == SIHIP_EDEVICE ? SI_EIO : rc; }
+
+/* The device copy of w, uploaded on first use. */
+static int device_weight(hip_backend *hb, const si_tensor *w, sihip_weight **out) {
+    slot *s = slot_find(hb, w->data);
+    if (s) {
+        *out = s->w;
+        return SI_OK;
+    }
+    const uint64_t n_in = w->ne[0], n_out = w->ne[1] ? w->ne[1] : 1;
+    sihip_weight *dw = NULL;
+    const int rc = hb->f.weight_upload(hb->ctx, w->type, n_out, n_in, w->data, w->n_bytes, &dw);
+    if (rc) {
+        si_set_err("hip: upload of a %llu x %llu tensor (type %u): %s",
+                   (unsigned long long)n_out, (unsigned long long)n_in, (unsigned)w->type,
+                   hb->f.last_error(hb->ctx));
+        return si_code(rc);
+    }
+    const int irc = slot_insert(hb, w->data, dw);
+    if (irc) {
+        hb->f.weight_free(hb->ctx, dw);
+        si_set_err("hip: out of host memory for the weight table");
+        return irc;
+    }
+    *out = dw;
+    return SI_OK;
+}
+
+static void hip_gemv(si_backend *be, const si_tensor *w, const float *x, float *y, int64_t n_out,
+                     si_tp *tp) {
+    (void)tp;
+    hip_backend *hb = as_hip(be);
+    sihip_weight *dw;
+    if (device_weight(hb, w, &dw)) return;
+    if (hb->f.gemv(hb->ctx, dw, x, y, n_out))
+        si_set_err("hip gemv: %s", hb->f.last_error(hb->ctx));
+}
+
+static void hip_row_to_f32(si_backend *be, const si_tensor *w, uint64_t row, float *out) {
+    (void)be;
+    si_backend *cpu = si_backend_cpu();
+    cpu->row_to_f32(cpu, w, row, out);
+}
+
+int si_backend_hip_gemm(si_backend *be, const si_tensor *w, const float *X, int64_t M, float *Y) {
+    if (!be || !w || !X || !Y || M <= 0) {
+        si_set_err("hip gemm: bad arguments");
+        return SI_EINVAL;
+    }
+    hip_backend *hb = as_hip(be);
+    sihip_weight *dw;
+    const int rc = device_weight(hb, w, &dw);
+    if (rc) return rc;
+    const int grc = hb->f.gemm(hb->ctx, dw, X, M, Y);
+    if (grc) {
+        si_set_err("hip gemm: %s", hb->f.last_error(hb->ctx));
+        return si_code(grc);
+    }
+    return SI_OK;
+}
+
+int si_backend_hip_weights(const si_backend *be, uint64_t *device_bytes) {
+    const hip_backend *hb = (const hip_backend *)be;
+    uint64_t total = 0;
+    for (size_t i = 0; i < hb->cap; i++)
+        if (hb->slots[i].data) total += hb->f.weight_device_bytes(hb->slots[i].w);
+    if (device_bytes) *device_bytes = total;
+    return (int)hb->n;
+}
+
+#define RESOLVE(field, name)                                                        \
+    do {                                                                            \
+        *(void **)(&hb->f.field) = dlsym(hb->dl, name);                             \
+        if (!hb->f.field) {                                                         \
+            si_set_err("hip: %s has no symbol %s", path, name);                     \
+            dlclose(hb->dl);                                                        \
+            free(hb);                                                               \
+            return SI_ENOENT;                                                       \
+        }                                                                           \
+    } while (0)
+
+int si_backend_hip_open(const char *lib_path, int device, si_backend **out) {
+    if (!out) {
+        si_set_err("hip: NULL output");
+        return SI_EINVAL;
+    }
+    const char *path = lib_path ? lib_path : getenv("SIPHON_HIP_LIB");
+    if (!path) path = "libsiphon_hip.so";
+    hip_backend *hb = calloc(1, sizeof *hb);
+    if (!hb) {
+        si_set_err("hip: out of host memory");
+        return SI_ENOMEM;
+    }
+    hb->dl = dlopen(path, RTLD_NOW | RTLD_LOCAL);
+    if (!hb->dl) {
+        si_set_err("hip: cannot load %s: %s", path, dlerror());
+        free(hb);
+        return SI_ENOENT;
+    }
+    RESOLVE(abi_version, "sihip_abi_version");
+    RESOLVE(init, "sihip_init");
+    RESOLVE(shutdown, "sihip_shutdown");
+    RESOLVE(last_error, "sihip_last_error");
+    RESOLVE(weight_upload, "sihip_weight_upload");
+    RESOLVE(weight_free, "sihip_weight_free");
+    RESOLVE(weight_device_bytes, "sihip_weight_device_bytes");
+    RESOLVE(gemv, "sihip_gemv");
+    RESOLVE(gemm, "sihip_gemm");
+    if (hb->f.abi_version() != SIHIP_ABI_VERSION) {
+        si_set_err("hip: %s has ABI version %d, this build expects %d", path,
+                   hb->f.abi_version(), SIHIP_ABI_VERSION);
+        dlclose(hb->dl);
+        free(hb);
+        return SI_ENOTSUP;
+    }
+    if (hb->f.init(device, &hb->ctx)) {
+        si_set_err("hip: device %d: %s", device, hb->f.last_error(NULL));
+        dlclose(hb->dl);
+        free(hb);
+        return SI_EIO;
+    }
+    hb->base.name = "hip";
+    hb->base.loc = SI_LOC_HOST;  /* inputs and outputs are host arrays */
+    hb->base.gemv = hip_gemv;
+    hb->base.row_to_f32 = hip_row_to_f32;
+    *out = &hb->base;
+    return SI_OK;
+}
+
+void si_backend_hip_close(si_backend *be) {
+    if (!be) return;
+    hip_backend *hb = as_hip(be);
+    for (size_t i = 0; i < hb->cap; i++)
+        if (hb->slots[i].data) hb->f.weight_free(hb->ctx, hb->slots[i].w);
+    free(hb->slots);
+    hb->f.shutdown(hb->ctx);
+    dlclose(hb->dl);
+    free(hb);
+}

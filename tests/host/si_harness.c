@@ -1,0 +1,89 @@
+/* Test harness for the "hip" si_backend adapter (siphon_amd/host).
+ * TEST INFRASTRUCTURE ONLY. It supplies what a Siphon build would: the
+ * error-string functions and a CPU backend whose row_to_f32 dequantizes
+ * with this repository's CPU oracle (oracle/siq_oracle.c), and exposes the
+ * vtable through plain functions for ctypes. */
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "si_hip_backend.h"
+#include "../../oracle/siq_oracle.h"
+
+static char g_err[512];
+
+const char *si_errstr(void) { return g_err; }
+
+void si_set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+static void cpu_row_to_f32(si_backend *be, const si_tensor *w, uint64_t row, float *out) {
+    (void)be;
+    uint32_t blk, bytes;
+    if (!siq_geometry(w->type, &blk, &bytes)) {
+        si_set_err("cpu row_to_f32: unsupported type %u", (unsigned)w->type);
+        return;
+    }
+    const uint64_t row_bytes = w->ne[0] / blk * bytes;
+    siq_dequant_row(w->type, (const char *)w->data + row * row_bytes, out, (int64_t)w->ne[0]);
+}
+
+static si_backend g_cpu = {"cpu", SI_LOC_HOST, NULL, cpu_row_to_f32};
+
+si_backend *si_backend_cpu(void) { return &g_cpu; }
+
+static si_tensor make_tensor(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in,
+                             const void *data, uint64_t bytes) {
+    si_tensor t;
+    memset(&t, 0, sizeof t);
+    t.type = type;
+    t.ne[0] = n_in;
+    t.ne[1] = n_out;
+    t.n_elems = n_in * n_out;
+    t.n_bytes = bytes;
+    t.data = data;
+    t.loc = SI_LOC_HOST;
+    t.be = be;
+    return t;
+}
+
+const char *th_errstr(void) { return g_err; }
+
+int th_open(const char *path, int device, si_backend **be) {
+    g_err[0] = 0;
+    return si_backend_hip_open(path, device, be);
+}
+
+void th_close(si_backend *be) { si_backend_hip_close(be); }
+
+const char *th_name(si_backend *be) { return be->name; }
+
+/* gemv through the vtable; returns 0, or -1 with th_errstr() set */
+int th_gemv(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, const void *data,
+            uint64_t bytes, const float *x, float *y, int64_t n) {
+    g_err[0] = 0;
+    const si_tensor t = make_tensor(be, type, n_out, n_in, data, bytes);
+    be->gemv(be, &t, x, y, n, NULL);
+    return g_err[0] ? -1 : 0;
+}
+
+int th_gemm(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, const void *data,
+            uint64_t bytes, const float *X, int64_t M, float *Y) {
+    g_err[0] = 0;
+    const si_tensor t = make_tensor(be, type, n_out, n_in, data, bytes);
+    return si_backend_hip_gemm(be, &t, X, M, Y);
+}
+
+int th_row_to_f32(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, const void *data,
+                  uint64_t bytes, uint64_t row, float *out) {
+    g_err[0] = 0;
+    const si_tensor t = make_tensor(be, type, n_out, n_in, data, bytes);
+    be->row_to_f32(be, &t, row, out);
+    return g_err[0] ? -1 : 0;
+}
+
+int th_weights(si_backend *be, uint64_t *bytes) { return si_backend_hip_weights(be, bytes); }

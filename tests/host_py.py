@@ -1,0 +1,58 @@
+"""ctypes access to the "hip" si_backend adapter through its test harness
+(tests/host: the adapter plus stand-ins for the Siphon functions it calls)."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "host")
+SO = os.path.join(HERE, "libsi_harness.so")
+
+
+class Harness:
+    def __init__(self):
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
+        L = ctypes.CDLL(SO)
+        vp, u32, u64, i64 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int64
+        L.th_errstr.restype = ctypes.c_char_p
+        L.th_open.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(vp)]
+        L.th_close.argtypes = [vp]
+        L.th_name.argtypes = [vp]
+        L.th_name.restype = ctypes.c_char_p
+        L.th_gemv.argtypes = [vp, u32, u64, u64, vp, u64, vp, vp, i64]
+        L.th_gemm.argtypes = [vp, u32, u64, u64, vp, u64, vp, i64, vp]
+        L.th_row_to_f32.argtypes = [vp, u32, u64, u64, vp, u64, u64, vp]
+        L.th_weights.argtypes = [vp, ctypes.POINTER(u64)]
+        self.L = L
+
+    def errstr(self) -> str:
+        return self.L.th_errstr().decode()
+
+    def open(self, path, device=0):
+        be = ctypes.c_void_p()
+        rc = self.L.th_open(path.encode() if path else None, device, ctypes.byref(be))
+        return rc, be.value
+
+    def close(self, be):
+        self.L.th_close(be)
+
+    def name(self, be):
+        return self.L.th_name(be).decode()
+
+    def gemv(self, be, wt, n_out, n_in, W, x, y, n):
+        return self.L.th_gemv(be, wt, n_out, n_in, W.ctypes.data, W.nbytes, x.ctypes.data,
+                              y.ctypes.data, n)
+
+    def gemm(self, be, wt, n_out, n_in, W, X, Y):
+        return self.L.th_gemm(be, wt, n_out, n_in, W.ctypes.data, W.nbytes, X.ctypes.data,
+                              X.shape[0], Y.ctypes.data)
+
+    def row_to_f32(self, be, wt, n_out, n_in, W, row, out):
+        return self.L.th_row_to_f32(be, wt, n_out, n_in, W.ctypes.data, W.nbytes, row,
+                                    out.ctypes.data)
+
+    def weights(self, be):
+        b = ctypes.c_uint64()
+        n = self.L.th_weights(be, ctypes.byref(b))
+        return n, b.value

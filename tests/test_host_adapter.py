@@ -1,0 +1,99 @@
+"""The C17 "hip" si_backend adapter (siphon_amd/host/backend_hip.c): the
+drop-in for the reference's backend vtable (reference
+include/siphon/tensor.h:43-55), driven through its test harness.
+
+CPU tests: loading and failure behaviour (missing library, no device).
+GPU tests: gemv / gemm / row_to_f32 through the vtable against the oracle,
+upload-once caching, and the reference's error contract (message set,
+output untouched)."""
+import numpy as np
+import pytest
+
+import siphon_amd as sa
+from siphon_amd import synth
+from siphon_amd.build import HIP_SO
+
+SI_ENOENT, SI_EIO = -6, -2
+
+
+@pytest.fixture(scope="module")
+def harness():
+    from tests import host_py
+    return host_py.Harness()
+
+
+def test_missing_library_is_reported(harness, tmp_path):
+    rc, be = harness.open(str(tmp_path / "libsiphon_hip.so"))
+    assert rc == SI_ENOENT and be is None
+    assert "cannot load" in harness.errstr()
+
+
+def test_open_reports_no_device_or_opens(harness):
+    """Without a GPU (this container) opening fails with SI_EIO and a
+    message; with one it succeeds and the backend is named "hip"."""
+    rc, be = harness.open(HIP_SO)
+    if rc == 0:
+        assert harness.name(be) == "hip"
+        harness.close(be)
+    else:
+        assert rc == SI_EIO, (rc, harness.errstr())
+        assert "device" in harness.errstr()
+
+
+@pytest.mark.gpu
+def test_vtable_gemv_gemm_row_to_f32(harness, oracle):
+    rc, be = harness.open(HIP_SO)
+    assert rc == 0, harness.errstr()
+    try:
+        rng = np.random.default_rng(17)
+        for wt, n_out, n_in in ((sa.Q4_K, 300, 2048), (sa.Q6_K, 129, 1024), (sa.Q8_0, 77, 896),
+                                (sa.F16, 64, 512)):
+            W = synth.make_weights(wt, n_out, n_in, rng)
+            x = rng.standard_normal(n_in).astype(np.float32)
+            y = np.full(n_out, np.nan, np.float32)
+            assert harness.gemv(be, wt, n_out, n_in, W, x, y, n_out) == 0, harness.errstr()
+            ref, l1 = oracle.gemv(wt, W, n_out, n_in, x)
+            assert np.all(np.abs(y.astype(np.float64) - ref) <= 1e-5 * l1 + 1e-6), sa.NAMES[wt]
+            # a second call reuses the uploaded copy
+            n_before, _ = harness.weights(be)
+            y2 = np.zeros(n_out, np.float32)
+            assert harness.gemv(be, wt, n_out, n_in, W, x, y2, n_out) == 0
+            assert harness.weights(be)[0] == n_before
+            assert np.array_equal(y, y2)
+            # prefill slot
+            X = rng.standard_normal((5, n_in)).astype(np.float32)
+            Y = np.zeros((5, n_out), np.float32)
+            assert harness.gemm(be, wt, n_out, n_in, W, X, Y) == 0, harness.errstr()
+            R, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+            assert np.all(np.abs(Y.astype(np.float64) - R) <= 1e-5 * L1 + 1e-6)
+            # embedding row lookup: the CPU dequantizer on the mmap'd row
+            out = np.zeros(n_in, np.float32)
+            assert harness.row_to_f32(be, wt, n_out, n_in, W, 3, out) == 0
+            assert np.array_equal(out.view(np.uint32),
+                                  oracle.dequant(wt, W[3], n_in).view(np.uint32))
+        n, nbytes = harness.weights(be)
+        assert n == 4 and nbytes > 0
+    finally:
+        harness.close(be)
+
+
+@pytest.mark.gpu
+def test_vtable_error_contract(harness):
+    """On failure gemv sets the message and leaves y untouched (reference
+    backend.c:90-98)."""
+    rc, be = harness.open(HIP_SO)
+    assert rc == 0, harness.errstr()
+    try:
+        rng = np.random.default_rng(5)
+        W = synth.make_weights(sa.Q4_K, 16, 256, rng)
+        x = rng.standard_normal(256).astype(np.float32)
+        y = np.full(17, 7.0, np.float32)
+        assert harness.gemv(be, sa.Q4_K, 16, 256, W, x, y, 17) == -1  # more rows than W has
+        assert "n_out" in harness.errstr()
+        assert np.all(y == 7.0)
+        bad = np.zeros(10, np.uint8)  # byte count does not match the shape
+        assert harness.gemv(be, sa.Q4_K, 16, 256, bad, x, y, 16) == -1
+        assert "upload" in harness.errstr()
+        assert np.all(y == 7.0)
+    finally:
+        harness.close(be)
