@@ -66,10 +66,7 @@ struct GemmX {
 };
 
 struct GemmArgs {
-    const uint8_t *wq;   // unit plane (nib16 records)
-    const uint8_t *wm;   // block plane (d | dmin | scales[12])
-    int R, G, logG;
-    int64_t S;           // matvec layout rounds per tile
+    const uint8_t *w;    // weights in GEMM order (gemm_layout_kernel)
     int64_t n_out, nb;   // weight rows, super-blocks per row
     int64_t M, Mp;
     GemmX X;
@@ -123,19 +120,67 @@ struct GemmW {
     U4 m;
 };
 
-// Records of (row, c) in the matvec layout (formats.h col_rec): unit k at
-// ((tile * S + s) * 8 + k) * 64 + r * G + g and the block at
-// (tile * S + s) * 64 + r * G + g, with s = c >> logG, g = c & (G - 1).
-// ub = tile * S * 512 + r * G and bb = tile * S * 64 + r * G are per row.
-__device__ inline void gemm_load_w(const GemmArgs &A, uint32_t ub, uint32_t bb, int64_t c, int h,
-                                   GemmW &w) {
-    const uint32_t s = (uint32_t)(c >> A.logG), g = (uint32_t)(c & (A.G - 1));
-    const uint32_t urec = ub + s * 512u + g;
-    const uint32_t brec = bb + s * 64u + g;
+// ---- GEMM weight order ---------------------------------------------------------
+//
+// The matvec layout interleaves the rows of a tile G columns apart, so the
+// 32 rows one GEMM wave needs for a super-block are spread over many cache
+// lines. Prefill uses a second copy in GEMM order, built on device from the
+// matvec planes on first use: for each block of 32 rows and super-block c,
+// 4608 contiguous bytes
+//   4 x 1024 B: for q = 0..3 and lane L = 32 h + r (r = row in the block),
+//               bytes 16 L .. 16 L + 7 = half h of unit 2q of row r,
+//               bytes 16 L + 8 .. 16 L + 15 = half h of unit 2q + 1 of row r
+//   512 B:      block records (d | dmin | scales) of rows 0..31
+// so a wave loads its operands for a super-block with 5 coalesced 16-byte
+// loads per lane, each half already where the MFMA B operand wants it.
+constexpr int kGemmChunk = 4608;
+
+__host__ __device__ inline int64_t gemm_layout_bytes(int64_t nblk32, int64_t nb) {
+    return nblk32 * nb * kGemmChunk;
+}
+
+// One thread per (32-row block, super-block, 16-byte slot); rows past n_out
+// are written as zeros.
+__global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_t *planes,
+                                                          uint8_t *out, int64_t nblk32) {
+    const int64_t nb = L.n_in / 256;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per = kGemmChunk / 16;  // 288 slots per chunk
+    if (i >= nblk32 * nb * per) return;
+    const int64_t chunk = i / per, slot = i % per;
+    const int64_t blk = chunk / nb, c = chunk % nb;
+    uint32_t v[4] = {0, 0, 0, 0};
+    if (slot < 256) {  // unit halves
+        const int q = (int)(slot >> 6), lane = (int)(slot & 63), h = lane >> 5, r = lane & 31;
+        const int64_t row = blk * 32 + r;
+        if (row < L.n_out) {
+            for (int k = 0; k < 2; k++) {
+                const uint8_t *src = planes + unit_off(L, 0, row, c * 8 + 2 * q + k) + 8 * h;
+                v[2 * k] = ldp<uint32_t>(src);
+                v[2 * k + 1] = ldp<uint32_t>(src + 4);
+            }
+        }
+    } else {  // block records
+        const int64_t row = blk * 32 + (slot - 256);
+        if (row < L.n_out) {
+            const uint8_t *src = planes + block_off(L, 1, row, c * 8);
+            for (int k = 0; k < 4; k++) v[k] = ldp<uint32_t>(src + 4 * k);
+        }
+    }
+    *reinterpret_cast<uint4 *>(out + i * 16) = make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// This lane's operands of super-block c from the GEMM-ordered copy (base of
+// the wave's 32-row block).
+__device__ inline void gemm_load_w(const uint8_t *blk_base, int64_t c, int lane, GemmW &w) {
+    const uint8_t *chunk = blk_base + c * kGemmChunk;
 #pragma unroll
-    for (int k = 0; k < 8; k++)
-        w.u[k] = *reinterpret_cast<const uint2 *>(A.wq + (urec + 64u * (uint32_t)k) * 16u + 8u * (uint32_t)h);
-    w.m = *reinterpret_cast<const U4 *>(A.wm + brec * 16u);
+    for (int q = 0; q < 4; q++) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(chunk + q * 1024 + 16 * lane);
+        w.u[2 * q] = make_uint2(v.x, v.y);
+        w.u[2 * q + 1] = make_uint2(v.z, v.w);
+    }
+    w.m = *reinterpret_cast<const U4 *>(chunk + 4096 + 16 * (lane & 31));
 }
 
 constexpr int kXPieces = kGemmBM * 16 / kGemmThreads;  // 16-byte quant pieces per thread
@@ -165,9 +210,7 @@ __attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel
     const int ln = lane & 31, h = lane >> 5;
     const int64_t m0 = (int64_t)mblk * kGemmBM;
     const int64_t n = (int64_t)nblk * kGemmBN + wave * 32 + ln;  // this lane's weight row
-    const int64_t nl = n < A.n_out ? n : A.n_out - 1;            // loads stay in the matrix
-    const uint32_t tS = (uint32_t)((nl / A.R) * A.S), rg = (uint32_t)((nl % A.R) * A.G);
-    const uint32_t ub = tS * 512u + rg, bb = tS * 64u + rg;
+    const uint8_t *wblk = A.w + (int64_t)(nblk * (kGemmBN / 32) + wave) * A.nb * kGemmChunk;
 
     v16f_t y[kGemmMT];
 #pragma unroll
@@ -187,8 +230,22 @@ __attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel
         for (int i = 0; i < kGemmMT; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc_h[i][r] = acc_l[i][r] = 0;
+        // activation operands are read one unit ahead of the MFMAs using them
+        v4i_t an[kGemmMT];
+#pragma unroll
+        for (int i = 0; i < kGemmMT; i++)
+            an[i] = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 16 * h);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
+            v4i_t ac[kGemmMT];
+#pragma unroll
+            for (int i = 0; i < kGemmMT; i++) {
+                ac[i] = an[i];
+                if (j < 7)
+                    an[i] = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 32 * (j + 1) + 16 * h);
+            }
+            // keep the reads of unit j + 1 ahead of the MFMAs of unit j
+            __builtin_amdgcn_sched_barrier(0);
             const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
             const uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
             const uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
@@ -199,9 +256,8 @@ __attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel
                               (int)bytes_times(q2, sl), (int)bytes_times(q3, sl)};
 #pragma unroll
             for (int i = 0; i < kGemmMT; i++) {
-                const v4i_t av = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 32 * j + 16 * h);
-                acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, acc_h[i], 0, 0, 0);
-                acc_l[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, acc_l[i], 0, 0, 0);
+                acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bh, acc_h[i], 0, 0, 0);
+                acc_l[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bl, acc_l[i], 0, 0, 0);
             }
         }
         // mins against the group sums: slot s of half h is group 8h + s
@@ -281,20 +337,20 @@ __attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel
     const int64_t last = A.nb - 1;
     GemmW wa, wb;
     load_x(0);
-    gemm_load_w(A, ub, bb, 0, h, wa);
+    gemm_load_w(wblk, 0, lane, wa);
     store_x(sx[0]);
     __syncthreads();
     for (int64_t c = 0;; c += 2) {
         const int64_t c1 = c + 1 < last ? c + 1 : last;
         load_x(c1);
-        gemm_load_w(A, ub, bb, c1, h, wb);
+        gemm_load_w(wblk, c1, lane, wb);
         compute(sx[0], wa);
         store_x(sx[1]);
         __syncthreads();
         if (c + 1 > last) break;
         const int64_t c2 = c + 2 < last ? c + 2 : last;
         load_x(c2);
-        gemm_load_w(A, ub, bb, c2, h, wa);
+        gemm_load_w(wblk, c2, lane, wa);
         compute(sx[1], wb);
         store_x(sx[0]);
         __syncthreads();

@@ -40,6 +40,8 @@ struct sihip_ctx {
 struct sihip_weight {
     Layout L;
     uint8_t *dev;
+    uint8_t *gemm = nullptr;  // GEMM-ordered copy, built on the first prefill call
+    int64_t gemm_bytes = 0;
 };
 
 static char g_init_err[512];
@@ -126,13 +128,14 @@ static int wgs_per_cu() {
 static int wave_target() {
     const char *e = getenv("SIHIP_WAVE_TARGET");
     const int v = e ? atoi(e) : 0;
-    return v > 0 ? v : 1024;
+    return v > 0 ? v : 800;
 }
 
 // Columns (super-blocks for K-quants, 32-element units otherwise) per wave
 // tile: the smallest power of two that keeps at least 80% of the lanes busy
-// and gives about wave_target() row tiles, so the whole chip is busy while
-// each lane keeps as many columns (and as few shuffle steps) as possible.
+// and gives at least wave_target() row tiles (about one per resident wave
+// of a decode launch, so no second wave of workgroups trails behind), while
+// each lane keeps as many rounds (and as few shuffle steps) as possible.
 static int choose_G(uint32_t type, int64_t n_out, int64_t n_in) {
     const int64_t ncols = is_kquant(type) ? n_in / 256 : n_in / 32;
     if (const char *f = getenv("SIHIP_TILE_COLS")) {
@@ -212,12 +215,13 @@ extern "C" int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w) {
     if (!w) return SIHIP_OK;
     if (ctx) HIP_OK(ctx, hipSetDevice(ctx->device));
     (void)hipFree(w->dev);
+    if (w->gemm) (void)hipFree(w->gemm);
     delete w;
     return SIHIP_OK;
 }
 
 extern "C" uint64_t sihip_weight_device_bytes(const sihip_weight *w) {
-    return w ? (uint64_t)w->L.total_bytes : 0;
+    return w ? (uint64_t)(w->L.total_bytes + w->gemm_bytes) : 0;
 }
 
 extern "C" int sihip_weight_tile_cols(const sihip_weight *w) { return w ? w->L.G : 0; }
@@ -376,10 +380,31 @@ static bool gemm_mfma_supported(uint32_t type) { return type == T_Q4_K; }
 
 // Y[m, :] = W x[m, :] for m < M on the matrix cores. The activation planes
 // live in the context's workspace, so calls on one context must not overlap.
-static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64_t ldx,
+static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X, int64_t ldx,
                          int64_t M, float *Y, int64_t ldy, hipStream_t st) {
+    sihip_weight *w = const_cast<sihip_weight *>(wc);  // the GEMM copy is a cache of w
     const Layout &L = w->L;
     const int64_t K = L.n_in, nb = K / 256;
+    const int NB = (int)((L.n_out + kGemmBN - 1) / kGemmBN);
+    if (!w->gemm) {
+        const int64_t nblk32 = (int64_t)NB * (kGemmBN / 32);
+        const int64_t bytes = gemm_layout_bytes(nblk32, nb);
+        uint8_t *g = nullptr;
+        hipError_t e = hipMalloc(&g, (size_t)bytes);
+        if (e != hipSuccess)
+            return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
+                           hipGetErrorString(e));
+        const int64_t threads = nblk32 * nb * (kGemmChunk / 16);
+        hipLaunchKernelGGL(gemm_layout_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           st, L, (const uint8_t *)w->dev, g, nblk32);
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+            (void)hipFree(g);
+            return set_err(ctx, SIHIP_EDEVICE, "gemm layout: %s", hipGetErrorString(e));
+        }
+        w->gemm = g;
+        w->gemm_bytes = bytes;
+    }
     const int64_t Mp = (M + kGemmBM - 1) / kGemmBM * kGemmBM;
     const int64_t ws = gemm_x_bytes(Mp, K);
     int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)ws);
@@ -394,12 +419,7 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const float *X, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm quantize: %s", hipGetErrorString(e));
     GemmArgs A;
-    A.wq = w->dev + L.plane_off[0];
-    A.wm = w->dev + L.plane_off[1];
-    A.R = L.R;
-    A.G = L.G;
-    A.logG = L.logG;
-    A.S = L.S;
+    A.w = w->gemm;
     A.n_out = L.n_out;
     A.nb = nb;
     A.M = M;
@@ -408,7 +428,7 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const float *X, 
     A.y = Y;
     A.ldy = ldy;
     A.MB = (int)(Mp / kGemmBM);
-    A.NB = (int)((L.n_out + kGemmBN - 1) / kGemmBN);
+    A.NB = NB;
     const int64_t grid = (int64_t)8 * ((A.NB + 7) / 8) * A.MB;
     hipLaunchKernelGGL(gemm_kq_kernel<T_Q4_K>, dim3((unsigned)grid), dim3(kGemmThreads), 0, st, A);
     e = hipGetLastError();
