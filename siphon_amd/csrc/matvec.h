@@ -81,24 +81,33 @@ struct MVArgs {
 //
 // Q8_K from f32 is split in two so the caller can issue its first weight
 // batch in between, from wave-uniform control flow: stage_q8k_first loads
-// the x values of the first pass (memory counters drain in order, so loads
-// issued before these would have to complete before the activations could be
-// used), stage_q8k_finish quantizes them and stages the remaining passes.
+// the x values of the first XP passes (16 blocks per pass; memory counters
+// drain in order, so x loaded after the weights could only be waited for
+// together with them), stage_activations quantizes them and stages the
+// remaining passes. XP > 1 is used for long rows (n_in > 4096) by kernels
+// whose register budget has room for the extra values.
 
+template <int XP>
 struct XFirst {
-    float4 t[4];
+    float4 t[XP][4];
 };
 
-// 16 lanes quantize one block: thread tid owns block (tid >> 4) of the pass,
-// elements 16 * (tid & 15) .. +15 of it.
-__device__ inline void stage_q8k_first(const MVArgs &a, XFirst &xf) {
+// 16 lanes quantize one block: thread tid owns block (tid >> 4) + 16 p of
+// pass p, elements 16 * (tid & 15) .. +15 of it.
+template <int XP>
+__device__ inline void stage_q8k_first(const MVArgs &a, XFirst<XP> &xf) {
     const int tid = threadIdx.x;
     const int64_t nb = a.n_in / 256;
-    const int64_t b = tid >> 4;
-    if (a.x && b < nb) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + b * 256 + (tid & 15) * 16);
+    if (!a.x) return;
 #pragma unroll
-        for (int i = 0; i < 4; i++) xf.t[i] = src[i];
+    for (int p = 0; p < XP; p++) {
+        if (16 * p < nb) {  // wave-uniform
+            int64_t b = (tid >> 4) + 16 * p;
+            b = b < nb ? b : nb - 1;  // clamped: the load stays in the row
+            const float4 *src = reinterpret_cast<const float4 *>(a.x + b * 256 + (tid & 15) * 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) xf.t[p][i] = src[i];
+        }
     }
 }
 
@@ -117,8 +126,8 @@ __device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int l
     if (lane16 == 0) reinterpret_cast<float *>(col + n)[b] = r.d;
 }
 
-template <uint32_t PAIR>
-__device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XFirst &xf) {
+template <uint32_t PAIR, int XP>
+__device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XFirst<XP> &xf) {
     const int tid = threadIdx.x;
     const int64_t n = a.n_in;
     for (int c = 0; c < a.nc; c++) {
@@ -130,11 +139,14 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             if (a.x) {
                 const float *xc = a.x + c * a.ldx;
                 const int lane16 = tid & 15;
-                for (int64_t b = tid >> 4; b < nb; b += kThreads / 16) {
-                    if (c == 0 && b == (tid >> 4)) {
-                        q8k_stage_block(col, n, b, lane16, xf.t);  // loaded up front
-                        continue;
-                    }
+                int64_t b0 = tid >> 4;
+                if (c == 0) {  // the passes loaded up front
+#pragma unroll
+                    for (int p = 0; p < XP; p++)
+                        if (b0 + 16 * p < nb) q8k_stage_block(col, n, b0 + 16 * p, lane16, xf.t[p]);
+                    b0 += 16 * XP;
+                }
+                for (int64_t b = b0; b < nb; b += kThreads / 16) {
                     const float4 *src = reinterpret_cast<const float4 *>(xc + b * 256 + lane16 * 16);
                     float4 t4[4];
 #pragma unroll
@@ -239,7 +251,7 @@ struct Buf {
 };
 
 // The matvec of one matrix (segment sg) by the workgroups of its range.
-template <uint32_t FMT, int NC>
+template <uint32_t FMT, int NC, int XP>
 __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *lds) {
     constexpr bool KQ = is_kquant(FMT);
     constexpr uint32_t PAIR = (FMT == T_F16) ? T_F16
@@ -327,10 +339,10 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     };
 
     Buf<FMT> bufA, bufB;
-    XFirst xf;
-    if constexpr (PAIR == T_Q8_K) stage_q8k_first(A, xf);
+    XFirst<XP> xf;
+    if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf);
     issue(bufA);
-    stage_activations<PAIR>(A, lds, xf);
+    stage_activations<PAIR, XP>(A, lds, xf);
     issue(bufB);
     __syncthreads();
     if (total == 0) return;  // a wave without rows only helped to stage
@@ -357,7 +369,7 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     if (left == 3) consume(bufA);
 }
 
-template <uint32_t F0, uint32_t F1, int NC>
+template <uint32_t F0, uint32_t F1, int NC, int XP>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     static_assert(pair_of(F0) == pair_of(F1), "one launch stages one activation format");
@@ -368,9 +380,9 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
         if (i < A.nseg && blockIdx.x >= A.seg[i].wg_begin) s = i;
     const MVSeg &sg = A.seg[s];
     if (F0 == F1 || sg.L.type == F0)
-        matvec_body<F0, NC>(A, sg, lds);
+        matvec_body<F0, NC, XP>(A, sg, lds);
     else
-        matvec_body<F1, NC>(A, sg, lds);
+        matvec_body<F1, NC, XP>(A, sg, lds);
 }
 
 // ---- standalone quantizers (global output in the reference block layouts) --

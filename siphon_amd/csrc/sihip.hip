@@ -228,9 +228,25 @@ extern "C" int sihip_weight_tile_cols(const sihip_weight *w) { return w ? w->L.G
 
 // ---- launches -----------------------------------------------------------------
 
+// Q8_K passes of the activation loaded before the weights: all four for
+// long rows of a single column where the kernel has register room (the
+// instances with Q6_K run at 2 waves per SIMD with registers to spare),
+// else the first.
+template <uint32_t F0, uint32_t F1>
+static int prologue_passes(const MVArgs &A) {
+    if (pair_of(F0) != T_Q8_K || A.nc != 1 || A.n_in <= 4096) return 1;
+    return (F0 == T_Q6_K || F1 == T_Q6_K) ? 4 : 1;
+}
+
 template <uint32_t F0, uint32_t F1, int NC>
 static hipError_t launch_nc(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((matvec_kernel<F0, F1, NC>), dim3(grid), dim3(kThreads), lds, st, A);
+    if constexpr (NC == 1 && pair_of(F0) == T_Q8_K) {
+        if (prologue_passes<F0, F1>(A) == 4) {
+            hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 4>), dim3(grid), dim3(kThreads), lds, st, A);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 1>), dim3(grid), dim3(kThreads), lds, st, A);
     return hipGetLastError();
 }
 

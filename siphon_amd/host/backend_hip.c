@@ -22,9 +22,12 @@ typedef struct {
     int (*gemm)(sihip_ctx *, const sihip_weight *, const float *, int64_t, float *);
 } hip_fns;
 
-/* one uploaded tensor, keyed by its mmap data pointer */
+/* one uploaded tensor, keyed by its mmap data pointer; type and shape are
+ * kept to detect a pointer that now belongs to a different tensor */
 typedef struct {
     const void *data;
+    uint32_t type;
+    uint64_t n_out, n_in, bytes;
     sihip_weight *w;
 } slot;
 
@@ -55,7 +58,7 @@ static slot *slot_find(hip_backend *hb, const void *data) {
     }
 }
 
-static int slot_insert(hip_backend *hb, const void *data, sihip_weight *w) {
+static int slot_insert(hip_backend *hb, const slot *ins) {
     if ((hb->n + 1) * 2 > hb->cap) {
         const size_t ncap = hb->cap ? hb->cap * 2 : 64;
         slot *ns = calloc(ncap, sizeof *ns);
@@ -70,10 +73,9 @@ static int slot_insert(hip_backend *hb, const void *data, sihip_weight *w) {
         hb->slots = ns;
         hb->cap = ncap;
     }
-    size_t j = slot_hash(data, hb->cap);
+    size_t j = slot_hash(ins->data, hb->cap);
     while (hb->slots[j].data) j = (j + 1) & (hb->cap - 1);
-    hb->slots[j].data = data;
-    hb->slots[j].w = w;
+    hb->slots[j] = *ins;
     hb->n++;
     return SI_OK;
 }
@@ -81,14 +83,34 @@ static int slot_insert(hip_backend *hb, const void *data, sihip_weight *w) {
 /* Map an SIHIP_* code (same values as SI_*; SIHIP_EDEVICE is extra) to SI_*. */
 static int si_code(int rc) { return rc == SIHIP_EDEVICE ? SI_EIO : rc; }
 
-/* The device copy of w, uploaded on first use. */
+/* The device copy of w, uploaded on first use. A cached copy whose key
+ * pointer now belongs to a tensor of another type or shape is stale (its
+ * memory was reused): it is replaced. */
 static int device_weight(hip_backend *hb, const si_tensor *w, sihip_weight **out) {
+    const uint64_t n_in = w->ne[0], n_out = w->ne[1] ? w->ne[1] : 1;
     slot *s = slot_find(hb, w->data);
     if (s) {
-        *out = s->w;
+        if (s->type == w->type && s->n_out == n_out && s->n_in == n_in && s->bytes == w->n_bytes) {
+            *out = s->w;
+            return SI_OK;
+        }
+        sihip_weight *dw = NULL;
+        const int rc = hb->f.weight_upload(hb->ctx, w->type, n_out, n_in, w->data, w->n_bytes, &dw);
+        if (rc) {
+            si_set_err("hip: upload of a %llu x %llu tensor (type %u): %s",
+                       (unsigned long long)n_out, (unsigned long long)n_in, (unsigned)w->type,
+                       hb->f.last_error(hb->ctx));
+            return si_code(rc);
+        }
+        hb->f.weight_free(hb->ctx, s->w);
+        s->type = w->type;
+        s->n_out = n_out;
+        s->n_in = n_in;
+        s->bytes = w->n_bytes;
+        s->w = dw;
+        *out = dw;
         return SI_OK;
     }
-    const uint64_t n_in = w->ne[0], n_out = w->ne[1] ? w->ne[1] : 1;
     sihip_weight *dw = NULL;
     const int rc = hb->f.weight_upload(hb->ctx, w->type, n_out, n_in, w->data, w->n_bytes, &dw);
     if (rc) {
@@ -97,7 +119,8 @@ static int device_weight(hip_backend *hb, const si_tensor *w, sihip_weight **out
                    hb->f.last_error(hb->ctx));
         return si_code(rc);
     }
-    const int irc = slot_insert(hb, w->data, dw);
+    const slot ins = {w->data, w->type, n_out, n_in, w->n_bytes, dw};
+    const int irc = slot_insert(hb, &ins);
     if (irc) {
         hb->f.weight_free(hb->ctx, dw);
         si_set_err("hip: out of host memory for the weight table");

@@ -44,11 +44,13 @@ def test_open_reports_no_device_or_opens(harness):
 def test_vtable_gemv_gemm_row_to_f32(harness, oracle):
     rc, be = harness.open(HIP_SO)
     assert rc == 0, harness.errstr()
+    keep = []  # weights stay alive like an mmap: the adapter keys uploads by address
     try:
         rng = np.random.default_rng(17)
         for wt, n_out, n_in in ((sa.Q4_K, 300, 2048), (sa.Q6_K, 129, 1024), (sa.Q8_0, 77, 896),
                                 (sa.F16, 64, 512)):
             W = synth.make_weights(wt, n_out, n_in, rng)
+            keep.append(W)
             x = rng.standard_normal(n_in).astype(np.float32)
             y = np.full(n_out, np.nan, np.float32)
             assert harness.gemv(be, wt, n_out, n_in, W, x, y, n_out) == 0, harness.errstr()
@@ -95,5 +97,33 @@ def test_vtable_error_contract(harness):
         assert harness.gemv(be, sa.Q4_K, 16, 256, bad, x, y, 16) == -1
         assert "upload" in harness.errstr()
         assert np.all(y == 7.0)
+    finally:
+        harness.close(be)
+
+
+@pytest.mark.gpu
+def test_reused_address_is_not_served_stale(harness, oracle):
+    """A host buffer that is freed and reused for a different tensor (a
+    different type or shape at the same address) gets a fresh upload."""
+    rc, be = harness.open(HIP_SO)
+    assert rc == 0, harness.errstr()
+    try:
+        rng = np.random.default_rng(23)
+        buf = np.zeros(64 * 512 * 2, np.uint8)  # one address, two tensors over time
+        W1 = synth.make_weights(sa.Q8_0, 32, 1024, rng)  # 32 x 32 blocks x 34 B
+        buf[:W1.nbytes] = W1.reshape(-1)
+        x1 = rng.standard_normal(1024).astype(np.float32)
+        y1 = np.zeros(32, np.float32)
+        assert harness.gemv(be, sa.Q8_0, 32, 1024, buf[:W1.nbytes], x1, y1, 32) == 0
+        ref1, l1 = oracle.gemv(sa.Q8_0, W1, 32, 1024, x1)
+        assert np.all(np.abs(y1.astype(np.float64) - ref1) <= 1e-5 * l1 + 1e-6)
+        W2 = synth.make_weights(sa.F16, 64, 512, rng)
+        buf[:W2.nbytes] = W2.reshape(-1)
+        x2 = rng.standard_normal(512).astype(np.float32)
+        y2 = np.zeros(64, np.float32)
+        assert harness.gemv(be, sa.F16, 64, 512, buf[:W2.nbytes], x2, y2, 64) == 0
+        ref2, l2 = oracle.gemv(sa.F16, W2, 64, 512, x2)
+        assert np.all(np.abs(y2.astype(np.float64) - ref2) <= 1e-5 * l2 + 1e-6)
+        assert harness.weights(be)[0] == 1  # the stale copy was replaced, not kept
     finally:
         harness.close(be)
