@@ -343,6 +343,11 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf);
     issue(bufA);
     stage_activations<PAIR, XP>(A, lds, xf);
+    if (total == 1) {  // one round: no second buffer (it would reload the same round)
+        __syncthreads();
+        consume(bufA);
+        return;
+    }
     issue(bufB);
     __syncthreads();
     if (total == 0) return;  // a wave without rows only helped to stage
