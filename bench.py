@@ -35,6 +35,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
+# HBM bytes per gate_up launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
+# in runs of their own (counters cannot be collected in a timed run),
+# scaled by the factors a 64 MiB copy gives (2.00 and 1.00); see
+# profiles/matvec_gate_up_traffic.md for the commands and raw values.
+GATE_UP_TRAFFIC_BYTES = 2.00 * 32454.0 * 1024 + 1.00 * 112.0 * 1024
 INT8_PEAK_TOPS = 5033.0         # MI355X dense int8 MFMA, TOPS (256 CU x 2.4 GHz x 8192)
 N_LAYERS = 32
 
@@ -195,7 +200,9 @@ def main():
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "avg_launch_us": round(us, 2),
         "algorithmic_bytes_per_launch": nbytes,
-        "traffic": None,
+        "traffic": round(GATE_UP_TRAFFIC_BYTES) if dom == "gate_up" else None,
+        "traffic_over_algorithmic": (round(GATE_UP_TRAFFIC_BYTES / nbytes, 4)
+                                     if dom == "gate_up" else None),
         "per_launch_us": {k: round(v[1], 2) for k, v in per.items()},
         "per_launch_GBs": {k: round(v[0] / (v[1] * 1e-6) / 1e9, 1) for k, v in per.items()},
     }
@@ -228,33 +235,45 @@ def main():
 
 
 def bench_gemm(dev, torch, stream, rng):
-    """Config 3: Q4_K W[14336 x 4096] x X[512 x 4096] -> Y[512 x 14336]."""
+    """Config 3: Q4_K W[14336 x 4096] x X[M x 4096] -> Y[M x 14336], M = 512
+    headline and the sweep {64, 128, 512, 2048}. Each call quantizes X to Q8_K
+    rows and runs the MFMA GEMM; ten weight copies rotate so the 256 MB
+    Infinity Cache cannot serve the weights. The first call per copy builds
+    its GEMM-ordered copy and is excluded (warm-up)."""
     import siphon_amd as sa
     from siphon_amd import synth
-    n_out, n_in, M = 14336, 4096, 512
+    n_out, n_in = 14336, 4096
     W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
-    w = dev.upload(sa.Q4_K, n_out, n_in, W)
-    X = torch.randn(M, n_in, device="cuda")
-    Y = torch.empty(M, n_out, device="cuda")
+    ws = [dev.upload(sa.Q4_K, n_out, n_in, W) for _ in range(10)]
     sp = stream.cuda_stream
-    with torch.cuda.stream(stream):
-        dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
+    sweep = {}
+    for M in (64, 128, 512, 2048):
+        X = torch.randn(M, n_in, device="cuda")
+        Y = torch.empty(M, n_out, device="cuda")
+        with torch.cuda.stream(stream):
+            for w in ws:
+                dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
         torch.cuda.synchronize()
+        reps = 20
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 5
         e0.record(stream)
-        for _ in range(reps):
-            dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
+        with torch.cuda.stream(stream):
+            for i in range(reps):
+                dev.gemm_dev(ws[i % len(ws)], X.data_ptr(), M, Y.data_ptr(), sp)
         e1.record(stream)
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / 1e3 / reps
-    ops = 2.0 * M * n_out * n_in
-    w.free()
-    tops = ops / t / 1e12
-    return {"value": round(tops, 2), "unit": "TOPS", "M": M, "shape": [n_out, n_in],
-            "us_per_call": round(t * 1e6, 1),
-            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
-                         "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 5)}}
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / 1e3 / reps
+        tops = 2.0 * M * n_out * n_in / t / 1e12
+        sweep[str(M)] = {"us_per_call": round(t * 1e6, 1), "TOPS": round(tops, 1),
+                         "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        del X, Y
+    for w in ws:
+        w.free()
+    head = sweep["512"]
+    return {"value": head["TOPS"], "unit": "TOPS", "M": 512, "shape": [n_out, n_in],
+            "us_per_call": head["us_per_call"], "sweep": sweep,
+            "roofline": {"bound": "mfma", "achieved": head["TOPS"], "peak": INT8_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": head["frac_int8_peak"]}}
 
 
 def cpu_baseline(host_layers, pass_bytes, budget_s=10.0):

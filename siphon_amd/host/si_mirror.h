@@ -8,9 +8,11 @@
  *   si_set_err, si_errstr           reference include/siphon/common.h:36-38
  *   si_tp (opaque lane pool)        reference include/siphon/threadpool.h:19
  *   si_backend_cpu                  reference include/siphon/tensor.h:58
- * SI_LOC_DEVICE is the location value the reference reserves for a device
- * backend (tensor.h:25-29); the adapter keeps weights SI_LOC_HOST (the
- * mmap stays the source) and tags its backend with it. */
+ * The reference has no device location yet (tensor.h:25-29 leaves
+ * SI_LOC_DEVICE for a later backend); the adapter needs none: weights stay
+ * SI_LOC_HOST (the mmap remains the source of every upload) and its
+ * backend is tagged SI_LOC_HOST because gemv takes and returns host
+ * arrays. */
 #ifndef SI_MIRROR_H
 #define SI_MIRROR_H
 
