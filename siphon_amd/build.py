@@ -78,8 +78,14 @@ def build_oracle(verbose: bool = False) -> None:
         _run(["make", "-s", "-C", odir, "ref"], verbose)
 
 
+def build_test_checkers(verbose: bool = False) -> None:
+    """The host emulation of the matvec kernel (tests/emu, test checker only)."""
+    _run(["make", "-s", "-C", os.path.join(ROOT, "tests", "emu")], verbose)
+
+
 def build_all(verbose: bool = False) -> None:
     build_oracle(verbose)
+    build_test_checkers(verbose)
     build_backend(verbose)
     build_hip(verbose)
 

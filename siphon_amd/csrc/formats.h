@@ -21,7 +21,7 @@
 //   two8  ( 8 B): u32 h[e / 16]; bits 8k + 2t .. +1 of h[i] = 2-bit value of
 //                 element 16i + 4t + k
 // The repacking is a bijection on the bits: device bytes equal GGUF bytes
-// (plus tile padding that no kernel reads).
+// (plus zero-filled tile padding).
 #pragma once
 
 #include <stdint.h>
@@ -97,8 +97,11 @@ SIHD inline PlaneSpec planes_of(uint32_t t) {
 // A row is a sequence of COLUMNS: super-blocks of 256 elements for the
 // K-quants, 32-element units for Q4_0/Q5_0/Q8_0/F16. A wave tile covers R
 // rows x G columns (R * G = 64, lane = r * G + g); round s of the tile gives
-// lane (r, g) column c = s * G + g of row tile * R + r. Rounds past the last
-// column (when G does not divide the column count) read zero-filled padding.
+// lane (r, g) column c = s * G + g of row tile * R + r. When G does not
+// divide the column count, the last round has padding slots past the row:
+// they are allocated (zero-filled) but the matvec kernel does not read them
+// (it re-reads a real column of the row and discards the result). Rows past
+// n_out in the last tile are zero-filled and read.
 //   column-level plane record = (tile * S + s) * 64 + lane
 //   unit-level plane record (K-quants, unit k = 0..7 of the super-block)
 //                            = ((tile * S + s) * 8 + k) * 64 + lane

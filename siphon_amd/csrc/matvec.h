@@ -219,9 +219,9 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
 // wave0 + nwaves, ... and S rounds per tile. One round is one super-block per
 // lane for the K-quants and kBatch units per lane otherwise. All control
 // flow in the loop is wave-uniform (scalar); loads are never predicated per
-// lane: rows past n_out in the last tile and columns past the end of a row
-// read the zero-filled padding that the upload allocates, and their LDS
-// activation reads are clamped into the row, so they contribute exactly 0.
+// lane: rows past n_out in the last tile read the zero-filled padding that
+// the upload allocates (their results are not stored), and padding slots
+// past the end of a row re-read a real column and are discarded.
 
 struct Item {
     uint32_t tile, s, rec;  // rec = (tile * S + s) * 64
@@ -269,6 +269,13 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     const uint32_t S = (uint32_t)L.S;
     const uint32_t n_in = (uint32_t)L.n_in;
     const uint32_t last_col = (uint32_t)L.ncols - 1;
+    // When G does not divide the columns, the last round of a tile has
+    // padding slots (column s * G + g past the row). Their lanes load the
+    // row's last real column of that round instead, which the same load
+    // instruction fetches anyway, so padding costs no memory traffic; their
+    // contribution is discarded.
+    const uint32_t glast = last_col - (S - 1) * (uint32_t)G;
+    const uint32_t lane_last = (uint32_t)(r * G) + ((uint32_t)g < glast ? (uint32_t)g : glast);
     const uint32_t col_bytes = (uint32_t)A.col_bytes;
     const uint32_t ntiles = (uint32_t)((sg.n_out + L.R - 1) / L.R);
     const uint32_t nwaves = sg.nwg * kWaves;
@@ -298,10 +305,11 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     auto issue = [&](Buf<FMT> &b) {
 #pragma unroll
         for (int i = 0; i < ITEMS; i++) {
+            const uint32_t ln = in_it.s == S - 1 ? lane_last : (uint32_t)lane;
             if constexpr (KQ)
-                load_kblock<FMT>(P, in_it.rec * 8u + (uint32_t)lane, in_it.rec + (uint32_t)lane, b.k);
+                load_kblock<FMT>(P, in_it.rec * 8u + ln, in_it.rec + ln, b.k);
             else
-                load_unit<FMT>(P, in_it.rec + (uint32_t)lane, b.u[i]);
+                load_unit<FMT>(P, in_it.rec + ln, b.u[i]);
             if (issued < total) {
                 issued++;
                 if (issued < total) step(in_it);
@@ -318,11 +326,17 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
         for (int i = 0; i < ITEMS; i++) {
             if (c_k < total) {
                 uint32_t col = c_it.s * (uint32_t)G + (uint32_t)g;
-                col = col < last_col ? col : last_col;  // padding columns read a valid LDS slot
+                const bool pad = col > last_col;
+                col = pad ? last_col : col;  // padding slots read a valid LDS column
+                float keep[NC];
+#pragma unroll
+                for (int c = 0; c < NC; c++) keep[c] = acc[c];
                 if constexpr (KQ)
                     compute_kblock<FMT, NC>(lds, col_bytes, n_in, col, b.k, acc);
                 else
                     compute_unit<FMT, NC>(lds, col_bytes, n_in, col, b.u[i], acc);
+#pragma unroll
+                for (int c = 0; c < NC; c++) acc[c] = pad ? keep[c] : acc[c];
                 if (c_it.s == S - 1) {
                     const int64_t row = (int64_t)c_it.tile * L.R + r;
 #pragma unroll

@@ -58,23 +58,31 @@ static void run(const Layout &L, const uint8_t *W, const uint8_t *lds, int64_t c
             for (int g = 0; g < L.G; g++) {
                 const uint32_t lane = (uint32_t)(r * L.G + g);
                 float acc[1] = {0.0f};
-                // every round of the tile, padding columns included (they
-                // hold zero weights and read the last column's activations)
+                // every round of the tile; a padding slot (column past the
+                // row, last round only) re-reads the row's last real column
+                // of that round and its contribution is discarded
+                const int64_t glast = L.ncols - 1 - (L.S - 1) * L.G;
+                const uint32_t lane_last =
+                    (uint32_t)(r * L.G + (g < glast ? g : glast));
                 for (int64_t s = 0; s < L.S; s++) {
                     int64_t col = s * L.G + g;
-                    if (col > L.ncols - 1) col = L.ncols - 1;
+                    const bool pad = col > L.ncols - 1;
+                    if (pad) col = L.ncols - 1;
+                    const uint32_t ln = s == L.S - 1 ? lane_last : lane;
                     const uint32_t rec = (uint32_t)((tile * L.S + s) * 64);
+                    const float keep = acc[0];
                     if constexpr (is_kquant(FMT)) {
                         KRaw raw;
-                        load_kblock<FMT>(P, rec * 8u + lane, rec + lane, raw);
+                        load_kblock<FMT>(P, rec * 8u + ln, rec + ln, raw);
                         compute_kblock<FMT, 1>(lds, (uint32_t)cb, (uint32_t)L.n_in, (uint32_t)col,
                                                raw, acc);
                     } else {
                         Raw raw;
-                        load_unit<FMT>(P, rec + lane, raw);
+                        load_unit<FMT>(P, rec + ln, raw);
                         compute_unit<FMT, 1>(lds, (uint32_t)cb, (uint32_t)L.n_in, (uint32_t)col,
                                              raw, acc);
                     }
+                    if (pad) acc[0] = keep;
                 }
                 v[g] = acc[0];
             }

@@ -11,8 +11,8 @@ SO = os.path.join(HERE, "libsiphon_emu.so")
 
 class Emulator:
     def __init__(self):
-        if not os.path.exists(SO):
-            subprocess.run(["make", "-s", "-C", HERE], check=True)
+        # make rebuilds only when emu.cpp or the kernel headers it compiles changed
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
         L = ctypes.CDLL(SO)
         vp = ctypes.c_void_p
         L.emu_gemv_pair.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
