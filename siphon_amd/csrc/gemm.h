@@ -230,21 +230,28 @@ __attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel
         for (int i = 0; i < kGemmMT; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc_h[i][r] = acc_l[i][r] = 0;
-        // activation operands are read one unit ahead of the MFMAs using them
-        v4i_t an[kGemmMT];
+        // The MFMA section runs at a raised wave priority: of the two waves
+        // on a SIMD, the one issuing MFMAs wins the issue slot, and the
+        // other one's scalar-core work fills the gaps (measured ~6% faster
+        // than equal priorities).
+        __builtin_amdgcn_s_setprio(1);
+        // activation operands are read two units ahead of the MFMAs using them
+        v4i_t aa[8][kGemmMT];
 #pragma unroll
-        for (int i = 0; i < kGemmMT; i++)
-            an[i] = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 16 * h);
+        for (int i = 0; i < kGemmMT; i++) {
+            aa[0][i] = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 16 * h);
+            aa[1][i] = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 32 + 16 * h);
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             v4i_t ac[kGemmMT];
 #pragma unroll
             for (int i = 0; i < kGemmMT; i++) {
-                ac[i] = an[i];
-                if (j < 7)
-                    an[i] = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 32 * (j + 1) + 16 * h);
+                ac[i] = aa[j][i];
+                if (j < 6)
+                    aa[j + 2][i] = *reinterpret_cast<const v4i_t *>(buf + (32 * i + ln) * kXRow + 32 * (j + 2) + 16 * h);
             }
-            // keep the reads of unit j + 1 ahead of the MFMAs of unit j
+            // keep the reads of unit j + 2 ahead of the MFMAs of unit j
             __builtin_amdgcn_sched_barrier(0);
             const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
             const uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
@@ -260,6 +267,7 @@ __attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel
                 acc_l[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bl, acc_l[i], 0, 0, 0);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         // mins against the group sums: slot s of half h is group 8h + s
         v8h_t bm;
 #pragma unroll
