@@ -15,11 +15,13 @@ blocks (random fields, f16 scales in the configured ranges), activations
 N(0,1); both are resident in HBM before timing starts.
 
 Extra fields: the dominant kernel's roofline (Q4_K matvec, per-launch HIP
-events), the M=512 prefill GEMM (config 3) in TOPS, and the reference's own
+events), the M=512 prefill GEMM (config 3) in TOPS, the other formats'
+matvec rates at configs 0, 1 and 4 (batch 1 and 8), and the reference's own
 AVX2 gemv (oracle/_ref, through its lane pool) on a bounded sample of the
 same weights on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-gemm]
+                    [--no-configs] [--profile gemm|traffic|configs]
 """
 from __future__ import annotations
 
@@ -58,6 +60,12 @@ def parse():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--unfused", action="store_true",
                     help="one launch per matrix instead of fused q/k/v and gate/up launches")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-format matvec measurements (configs 0, 1, 4)")
+    ap.add_argument("--profile", choices=("gemm", "traffic", "configs"),
+                    help="run one workload for a profiler and exit: the GEMM M sweep, "
+                         "a 64 MiB copy plus 12 gate/up launches (HBM counter runs), "
+                         "or the per-format matvec measurements")
     return ap.parse_args()
 
 
@@ -95,6 +103,17 @@ def main():
     torch.cuda.init()
     dev = sa.Device(0)
     rng = np.random.default_rng(args.seed)
+    if args.profile:
+        stream = torch.cuda.Stream()
+        if args.profile == "gemm":
+            out = bench_gemm(dev, torch, stream, rng)
+        elif args.profile == "configs":
+            out = bench_configs(dev, torch, stream, rng)
+        else:
+            out = profile_traffic(dev, torch, stream, rng)
+        dev.close()
+        print(json.dumps(out), flush=True)
+        return
     t0 = time.time()
     cpu_layers = 0 if args.no_cpu else 2
     layers, host_layers = build_layers(dev, rng, cpu_layers)
@@ -222,6 +241,12 @@ def main():
 
     if not args.no_gemm:
         result["gemm_m512"] = bench_gemm(dev, torch, stream, rng)
+    if not args.no_configs:
+        for l in layers:  # the per-format runs upload their own matrices
+            for w in l.values():
+                w.free()
+        layers = []
+        result["configs"] = bench_configs(dev, torch, stream, rng)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(host_layers, pass_bytes)
@@ -274,6 +299,103 @@ def bench_gemm(dev, torch, stream, rng):
             "us_per_call": head["us_per_call"], "sweep": sweep,
             "roofline": {"bound": "mfma", "achieved": head["TOPS"], "peak": INT8_PEAK_TOPS,
                          "unit": "TOP/s", "frac": head["frac_int8_peak"]}}
+
+
+def _config_shapes():
+    """Configs 0, 1 and 4 of the benchmark plan: (label, type, n_out, n_in,
+    batches). Config 1's Q6_K head uses n_in 1024 (Q6_K needs a multiple of
+    256; the 896-wide head of that model cannot be Q6_K)."""
+    import siphon_amd as sa
+    shapes = [("cfg0 Q4_K 5632x2048", sa.Q4_K, 5632, 2048, (1,)),
+              ("cfg1 Q8_0 4864x896", sa.Q8_0, 4864, 896, (1,)),
+              ("cfg1 Q6_K head 151936x1024", sa.Q6_K, 151936, 1024, (1,)),
+              ("cfg1 Q8_0 head 151936x896", sa.Q8_0, 151936, 896, (1,))]
+    for wt in (sa.Q2_K, sa.Q3_K, sa.Q5_K, sa.Q5_0, sa.F16):
+        nm = sa.NAMES[wt]
+        shapes += [(f"cfg4 {nm} attn 5120x5120", wt, 5120, 5120, (1, 8)),
+                   (f"cfg4 {nm} kv 1024x5120", wt, 1024, 5120, (1, 8)),
+                   (f"cfg4 {nm} ffn_up 27648x5120", wt, 27648, 5120, (1, 8)),
+                   (f"cfg4 {nm} ffn_down 5120x27648", wt, 5120, 27648, (1, 8))]
+    return shapes
+
+
+def bench_configs(dev, torch, stream, rng, rotate_bytes=512 << 20):
+    """Per-format matvec rates at the other configs' shapes, batch 1 (and 8
+    for config 4). Enough copies of each matrix rotate that more than
+    `rotate_bytes` stream between two reads of one copy, so the 256 MB
+    Infinity Cache cannot serve them; the launches over all copies are one
+    HIP graph, replayed; rate = weight bytes / average launch time."""
+    from siphon_amd import synth
+    sp = stream.cuda_stream
+    out = {}
+    for label, wt, n_out, n_in, batches in _config_shapes():
+        W = synth.make_weights(wt, n_out, n_in, rng)
+        copies = max(2, -(-rotate_bytes // W.nbytes) + 1)
+        ws = [dev.upload(wt, n_out, n_in, W) for _ in range(copies)]
+        del W
+        entry = {"bytes": ws[0].gguf_bytes, "copies": copies}
+        for M in batches:
+            X = torch.randn(M, n_in, device="cuda")
+            Y = torch.empty(M, n_out, device="cuda")
+
+            def run():
+                for w in ws:
+                    if M == 1:
+                        dev.gemv_dev(w, X.data_ptr(), Y.data_ptr(), n_out, sp)
+                    else:
+                        dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
+            with torch.cuda.stream(stream):
+                run()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                run()
+            g.replay()
+            torch.cuda.synchronize()
+            reps = max(3, int(2e9 // (copies * ws[0].gguf_bytes)))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                with torch.cuda.stream(stream):
+                    g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+            gbs = ws[0].gguf_bytes / (us * 1e-6) / 1e9
+            entry[f"batch{M}"] = {"us_per_call": round(us, 2), "GB/s": round(gbs, 1),
+                                  "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+            del g, X, Y
+        for w in ws:
+            w.free()
+        out[label] = entry
+    return out
+
+
+def profile_traffic(dev, torch, stream, rng):
+    """For the HBM counter runs (FETCH_SIZE, WRITE_SIZE): three 64 MiB
+    device copies (calibration: the counters' bytes per dispatch against a
+    known size), then 12 fused gate/up launches over 6 distinct weight
+    pairs (793 MB, more than the Infinity Cache)."""
+    import siphon_amd as sa
+    from siphon_amd import synth
+    a = torch.ones(16 << 20, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    W = synth.make_weights(sa.Q4_K, 14336, 4096, rng)
+    pairs = [[dev.upload(sa.Q4_K, 14336, 4096, W) for _ in range(2)] for _ in range(6)]
+    x = torch.randn(4096, device="cuda")
+    ys = [torch.empty(14336, device="cuda") for _ in range(2)]
+    for r in range(2):
+        for ws in pairs:
+            dev.gemv_multi_dev(ws, x.data_ptr(), [y.data_ptr() for y in ys], stream.cuda_stream)
+    torch.cuda.synchronize()
+    for ws in pairs:
+        for w in ws:
+            w.free()
+    return {"copy_bytes": 2 * (64 << 20), "gate_up_launches": 12,
+            "gate_up_weight_bytes": 2 * 33030144}
 
 
 def cpu_baseline(host_layers, pass_bytes, budget_s=10.0):

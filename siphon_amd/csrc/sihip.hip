@@ -11,6 +11,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <utility>
 #include <vector>
 
 #include "../../include/sihip.h"
@@ -136,6 +137,10 @@ static int wave_target() {
 // and gives at least wave_target() row tiles (about one per resident wave
 // of a decode launch, so no second wave of workgroups trails behind), while
 // each lane keeps as many rounds (and as few shuffle steps) as possible.
+// A matrix that this leaves with fewer than 256 row tiles (few rows and
+// long rows, e.g. a 1024-row kv projection) takes wider tiles at down to 50%
+// busy lanes: padding slots cost lanes but no memory traffic (they re-read a
+// real column), and more waves in flight matter more there.
 static int choose_G(uint32_t type, int64_t n_out, int64_t n_in) {
     const int64_t ncols = is_kquant(type) ? n_in / 256 : n_in / 32;
     if (const char *f = getenv("SIHIP_TILE_COLS")) {
@@ -143,16 +148,21 @@ static int choose_G(uint32_t type, int64_t n_out, int64_t n_in) {
         if (G >= 1 && G <= 64 && !(G & (G - 1))) return G;
     }
     const int64_t target = wave_target();
-    int best = 1;
-    int64_t best_tiles = 0;
-    for (int G = 1; G <= 64; G *= 2) {
-        const int64_t S = (ncols + G - 1) / G;
-        if (ncols * 10 < S * G * 8) continue;  // fewer than 80% of the lanes busy
-        const int64_t tiles = (n_out + 64 / G - 1) / (64 / G);
-        if (tiles > best_tiles) { best = G; best_tiles = tiles; }
-        if (tiles >= target) break;
-    }
-    return best;
+    auto pick = [&](int pct) {
+        int best = 1;
+        int64_t best_tiles = 0;
+        for (int G = 1; G <= 64; G *= 2) {
+            const int64_t S = (ncols + G - 1) / G;
+            if (ncols * 100 < S * G * pct) continue;  // too few lanes busy
+            const int64_t tiles = (n_out + 64 / G - 1) / (64 / G);
+            if (tiles > best_tiles) { best = G; best_tiles = tiles; }
+            if (tiles >= target) break;
+        }
+        return std::make_pair(best, best_tiles);
+    };
+    auto [G, tiles] = pick(80);
+    if (tiles < 256) G = pick(50).first;
+    return G;
 }
 
 extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out,
