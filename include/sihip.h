@@ -82,6 +82,13 @@ uint64_t sihip_weight_device_bytes(const sihip_weight *w);
  * wavefront, 1..64 (a power of two). Chosen at upload from the shape; the
  * environment variable SIHIP_TILE_COLS forces it (tests, tuning). */
 int sihip_weight_tile_cols(const sihip_weight *w);
+/* Layout introspection: rounds of a wave tile (tile_cols columns each) per
+ * column slice of the matvec. Rows of 8192 elements or more are cut into
+ * slices of about 4096 elements computed by separate workgroups and added
+ * in slice order; equal to the tile's round count when the rows are not
+ * sliced. The environment variable SIHIP_SPLIT_ELEMS sets the slice length
+ * in elements at upload (0: no slices). */
+int sihip_weight_slice_rounds(const sihip_weight *w);
 
 /* ---- matvec / matmul: host pointers, synchronous ---------------------
  * Same semantics as the reference cpu_gemv (backend.c:85-120):

@@ -67,6 +67,7 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_weight_device_bytes.argtypes = [_vp]
     L.sihip_weight_device_bytes.restype = _u64
     L.sihip_weight_tile_cols.argtypes = [_vp]
+    L.sihip_weight_slice_rounds.argtypes = [_vp]
     L.sihip_gemv.argtypes = [_vp, _vp, _vp, _vp, _i64]
     L.sihip_gemm.argtypes = [_vp, _vp, _vp, _i64, _vp]
     L.sihip_gemv_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
@@ -114,6 +115,10 @@ class Weight:
     @property
     def tile_cols(self) -> int:
         return int(self.dev.L.sihip_weight_tile_cols(self.handle))
+
+    @property
+    def slice_rounds(self) -> int:
+        return int(self.dev.L.sihip_weight_slice_rounds(self.handle))
 
     @property
     def gguf_bytes(self) -> int:

@@ -161,6 +161,26 @@ inline bool make_layout(uint32_t type, int64_t n_out, int64_t n_in, int G, Layou
     return true;
 }
 
+// Column slices of long rows. A matvec workgroup that computes whole rows
+// first converts the whole activation row into LDS; for long rows that
+// prologue outweighs the workgroup's share of the streaming. Rows of at
+// least 2 * kSliceElems elements are cut into slices of about kSliceElems
+// activation elements (whole rounds of the tile), each computed by its own
+// workgroups; the partial sums of a row are added in slice order.
+// slice_rounds() gives the rounds per slice, L.S (one slice) for shorter
+// rows or elems <= 0.
+constexpr int64_t kSliceElems = 4096;
+
+SIHD inline bool sliced_rows(int64_t n_in, int64_t elems) { return elems > 0 && n_in >= 2 * elems; }
+
+SIHD inline int64_t slice_rounds(const Layout &L, int64_t elems) {
+    const int64_t col_elems = is_kquant(L.type) ? 256 : 32;
+    if (!sliced_rows(L.n_in, elems)) return L.S;
+    int64_t r = elems / (L.G * col_elems);
+    if (r < 1) r = 1;
+    return r < L.S ? r : L.S;
+}
+
 // Record index of column c of row `row` (column-level planes).
 SIHD inline int64_t col_rec(const Layout &L, int64_t row, int64_t c) {
     const int64_t tile = row / L.R, r = row % L.R;

@@ -51,19 +51,37 @@ __host__ __device__ inline int64_t lds_col_bytes(uint32_t pair, int64_t n_in) {
     return n_in * 2;  // F16
 }
 
-// One weight matrix of a launch. Several matrices that share the activation
-// (QKV, gate+up) run in one launch: each gets a contiguous range of
-// workgroups, and all of them stage the same activation into LDS.
+// One weight matrix of a launch, described by what the kernel reads (the
+// layout's plane bases and tile geometry, with the host computing whatever
+// it can). Several matrices that share the activation (QKV, gate+up) run in
+// one launch: matrix i takes the workgroups of grid row blockIdx.y == i
+// (the surplus of a row wider than its nwg exits at once), and all of them
+// stage the same activation into LDS. A launch of one matrix reads seg[0]
+// at a fixed offset, so the first kernel-argument loads of its waves go out
+// together; selecting the matrix by a loaded value first would add a round
+// trip (measured: about 0.4 us per launch).
 constexpr int kMaxSegs = 4;
 
 struct MVSeg {
-    const uint8_t *w;     // plane base
-    Layout L;
-    float *y;             // outputs, column c at y + c * ldy
+    const uint8_t *plane[4];  // plane bases
+    float *y;                 // outputs, column c at y + c * ldy
     int64_t ldy;
-    int64_t n_out;        // rows to compute (<= L.n_out)
-    uint32_t wg_begin;    // first workgroup of this matrix
-    uint32_t nwg;         // workgroups of this matrix
+    // Column slices. split == 1: a workgroup computes whole rows (spr == S).
+    // split > 1: workgroup i computes rounds [spr * (i % split), +spr) of
+    // the kWaves tiles of group i / split, one tile per wave, and stores its
+    // partial sums in part[(slice * NC + c) * ntiles * R + row]; the last
+    // workgroup of a group to arrive (counted in cnt[group], which is zero
+    // between launches) adds the slices in slice order and writes y.
+    float *part;
+    uint32_t *cnt;
+    uint32_t split, spr;
+    uint32_t type;
+    uint32_t n_out;           // rows to compute (<= the layout's rows)
+    uint32_t ntiles;          // ceil(n_out / R)
+    uint32_t nwg;             // workgroups of this matrix
+    uint32_t G, logG, R;      // wave tile: G columns x R rows
+    uint32_t S;               // rounds per tile
+    uint32_t ncols;           // columns per row
 };
 
 struct MVArgs {
@@ -95,15 +113,14 @@ struct XFirst {
 // 16 lanes quantize one block: thread tid owns block (tid >> 4) + 16 p of
 // pass p, elements 16 * (tid & 15) .. +15 of it.
 template <int XP>
-__device__ inline void stage_q8k_first(const MVArgs &a, XFirst<XP> &xf) {
+__device__ inline void stage_q8k_first(const MVArgs &a, XFirst<XP> &xf, int64_t b0, int64_t b1) {
     const int tid = threadIdx.x;
-    const int64_t nb = a.n_in / 256;
     if (!a.x) return;
 #pragma unroll
     for (int p = 0; p < XP; p++) {
-        if (16 * p < nb) {  // wave-uniform
-            int64_t b = (tid >> 4) + 16 * p;
-            b = b < nb ? b : nb - 1;  // clamped: the load stays in the row
+        if (b0 + 16 * p < b1) {  // wave-uniform
+            int64_t b = b0 + (tid >> 4) + 16 * p;
+            b = b < b1 ? b : b1 - 1;  // clamped: the load stays in the range
             const float4 *src = reinterpret_cast<const float4 *>(a.x + b * 256 + (tid & 15) * 16);
 #pragma unroll
             for (int i = 0; i < 4; i++) xf.t[p][i] = src[i];
@@ -126,8 +143,11 @@ __device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int l
     if (lane16 == 0) reinterpret_cast<float *>(col + n)[b] = r.d;
 }
 
+// Stages pair blocks [b0, b1) of each column (32-element units for F16) at
+// their places in the full-row LDS image.
 template <uint32_t PAIR, int XP>
-__device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XFirst<XP> &xf) {
+__device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XFirst<XP> &xf,
+                                         int64_t b0, int64_t b1) {
     const int tid = threadIdx.x;
     const int64_t n = a.n_in;
     for (int c = 0; c < a.nc; c++) {
@@ -139,14 +159,14 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             if (a.x) {
                 const float *xc = a.x + c * a.ldx;
                 const int lane16 = tid & 15;
-                int64_t b0 = tid >> 4;
+                int64_t bt = b0 + (tid >> 4);
                 if (c == 0) {  // the passes loaded up front
 #pragma unroll
                     for (int p = 0; p < XP; p++)
-                        if (b0 + 16 * p < nb) q8k_stage_block(col, n, b0 + 16 * p, lane16, xf.t[p]);
-                    b0 += 16 * XP;
+                        if (bt + 16 * p < b1) q8k_stage_block(col, n, bt + 16 * p, lane16, xf.t[p]);
+                    bt += 16 * XP;
                 }
-                for (int64_t b = b0; b < nb; b += kThreads / 16) {
+                for (int64_t b = bt; b < b1; b += kThreads / 16) {
                     const float4 *src = reinterpret_cast<const float4 *>(xc + b * 256 + lane16 * 16);
                     float4 t4[4];
 #pragma unroll
@@ -155,8 +175,8 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
                 }
             } else {
                 const uint8_t *src = a.xq + c * a.ldxq;
-                for (int64_t i = tid; i < nb * 73; i += kThreads) {
-                    const int64_t b = i / 73, w = i % 73;  // 73 dwords per 292-byte block
+                for (int64_t i = tid; i < (b1 - b0) * 73; i += kThreads) {
+                    const int64_t b = b0 + i / 73, w = i % 73;  // 73 dwords per 292-byte block
                     const uint32_t v = reinterpret_cast<const uint32_t *>(src + b * 292)[w];
                     if (w == 0) dcol[b] = __uint_as_float(v);
                     else if (w < 65)
@@ -170,7 +190,7 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             const int64_t nb = n / 32;
             float *dcol = reinterpret_cast<float *>(col + n);
             int *scol = reinterpret_cast<int *>(col + n + nb * 4);
-            for (int64_t b = tid; b < nb; b += kThreads) {
+            for (int64_t b = b0 + tid; b < b1; b += kThreads) {
                 uint32_t q[8];
                 float d;
                 int sum;
@@ -203,11 +223,11 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             uint16_t *h = reinterpret_cast<uint16_t *>(col);
             if (a.x) {
                 const float *xc = a.x + c * a.ldx;
-                for (int64_t i = tid; i < n; i += kThreads)
+                for (int64_t i = b0 * 32 + tid; i < b1 * 32; i += kThreads)
                     h[i] = __builtin_bit_cast(uint16_t, (_Float16)xc[i]);
             } else {
                 const uint16_t *src = reinterpret_cast<const uint16_t *>(a.xq + c * a.ldxq);
-                for (int64_t i = tid; i < n; i += kThreads) h[i] = src[i];
+                for (int64_t i = b0 * 32 + tid; i < b1 * 32; i += kThreads) h[i] = src[i];
             }
         }
     }
@@ -250,25 +270,67 @@ struct Buf {
     Raw u[kBatch];
 };
 
+// End of a column-sliced workgroup: count its arrival in its tile group and,
+// if it is the group's last, add the partial sums of the group's rows over
+// the slices in slice order (the same order whichever workgroup is last)
+// and reset the counter for the next launch. Nothing waits on another
+// workgroup.
+//
+// Partial sums travel through agent-scope atomic stores and loads, which
+// write through / read past the per-XCD L2 caches, so no L2 write-back or
+// invalidation (what an agent-scope release / acquire fence costs on gfx950:
+// a 7x slower launch) is needed: each wave waits until its partial stores
+// have completed before the workgroup counts its arrival, and the last
+// workgroup reads the partials only after its arrival has returned.
+//
+// `last` is a word of LDS past the staged activations (the launch of a sliced
+// matrix allocates it; a static LDS variable would add to every launch's LDS
+// and cost occupancy where the activations fill it exactly).
+template <int NC>
+__device__ inline void split_reduce(const MVSeg &sg, uint32_t grp, uint32_t ldp, uint32_t *last) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *last = __hip_atomic_fetch_add(sg.cnt + grp, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == sg.split - 1;
+    __syncthreads();
+    if (!*last) return;
+    const uint32_t rows = kWaves * sg.R;
+    for (uint32_t i = threadIdx.x; i < rows * NC; i += kThreads) {
+        const uint32_t c = i / rows;
+        const int64_t row = (int64_t)grp * rows + (i - c * rows);
+        if (row < (int64_t)sg.n_out) {
+            float v = 0.0f;
+            for (uint32_t p = 0; p < sg.split; p++)
+                v += __hip_atomic_load(sg.part + (int64_t)(p * NC + c) * ldp + row, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            sg.y[c * sg.ldy + row] = v;
+        }
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(sg.cnt + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The matvec of one matrix (segment sg) by the workgroups of its range.
-template <uint32_t FMT, int NC, int XP>
+// SPLIT: compiled with the column-slice paths (a launch with a sliced
+// matrix); without them a launch of whole rows keeps the shorter code.
+template <uint32_t FMT, int NC, int XP, bool SPLIT>
 __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *lds) {
     constexpr bool KQ = is_kquant(FMT);
     constexpr uint32_t PAIR = (FMT == T_F16) ? T_F16
                               : (FMT == T_Q4_0 || FMT == T_Q5_0 || FMT == T_Q8_0) ? T_Q8_0
                                                                                    : T_Q8_K;
     constexpr int ITEMS = Buf<FMT>::items;
-    const Layout &L = sg.L;
     const int lane = threadIdx.x & 63;
-    const int G = L.G;
+    const int G = (int)sg.G;
     const int g = lane & (G - 1);
-    const int r = lane >> L.logG;
+    const int r = lane >> sg.logG;
     Planes P;
 #pragma unroll
-    for (int p = 0; p < 4; p++) P.p[p] = sg.w + L.plane_off[p];
-    const uint32_t S = (uint32_t)L.S;
-    const uint32_t n_in = (uint32_t)L.n_in;
-    const uint32_t last_col = (uint32_t)L.ncols - 1;
+    for (int p = 0; p < 4; p++) P.p[p] = sg.plane[p];
+    const uint32_t S = sg.S;
+    const uint32_t n_in = (uint32_t)A.n_in;
+    const uint32_t last_col = sg.ncols - 1;
     // When G does not divide the columns, the last round of a tile has
     // padding slots (column s * G + g past the row). Their lanes load the
     // row's last real column of that round instead, which the same load
@@ -277,20 +339,34 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     const uint32_t glast = last_col - (S - 1) * (uint32_t)G;
     const uint32_t lane_last = (uint32_t)(r * G) + ((uint32_t)g < glast ? (uint32_t)g : glast);
     const uint32_t col_bytes = (uint32_t)A.col_bytes;
-    const uint32_t ntiles = (uint32_t)((sg.n_out + L.R - 1) / L.R);
-    const uint32_t nwaves = sg.nwg * kWaves;
+    const uint32_t ntiles = sg.ntiles;
+    const uint32_t R = sg.R;
     // wave-uniform: keep the whole walk in scalar registers
-    const uint32_t wave0 =
-        (blockIdx.x - sg.wg_begin) * kWaves +
-        (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t wgi = blockIdx.x;
+    const bool split = SPLIT && sg.split > 1;
+    const uint32_t grp = split ? wgi / sg.split : 0u;
+    const uint32_t slice = split ? wgi - grp * sg.split : 0u;
+    // rounds [s_begin, s_end) of each tile
+    const uint32_t s_begin = SPLIT ? slice * sg.spr : 0u;
+    const uint32_t s_end = !SPLIT ? S : s_begin + sg.spr < S ? s_begin + sg.spr : S;
+    const uint32_t wave0 = (split ? grp : wgi) * kWaves + wv;
+    const uint32_t nwaves = split ? ntiles : sg.nwg * kWaves;  // split: one tile per wave
     const uint32_t my_tiles = wave0 < ntiles ? (ntiles - 1 - wave0) / nwaves + 1 : 0;
-    const uint32_t total = my_tiles * S;  // rounds of this wave
+    const uint32_t total = my_tiles * (s_end - s_begin);  // rounds of this wave
+
+    // finished rows go to y, or (sliced) to this slice's partial sums, rows
+    // of the last tile included; agent-scope stores, which partial sums need
+    // (split_reduce) and which cost y nothing
+    float *const out = split ? sg.part + (int64_t)slice * NC * ntiles * R : sg.y;
+    const int64_t out_ld = split ? (int64_t)ntiles * R : sg.ldy;
+    const int64_t out_rows = split ? (int64_t)ntiles * R : (int64_t)sg.n_out;
 
     auto step = [&](Item &it) {
-        if (++it.s == S) {
-            it.s = 0;
+        if (++it.s == s_end) {
+            it.s = s_begin;
             it.tile += nwaves;
-            it.rec = it.tile * S * 64u;
+            it.rec = (it.tile * S + s_begin) * 64u;
         } else {
             it.rec += 64u;
         }
@@ -300,7 +376,7 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     // a wave without rows (only in the last workgroup) still loads, from
     // tile 0, so that the loads before the barrier are unconditional
     const uint32_t t0 = total ? wave0 : 0u;
-    Item in_it{t0, 0, t0 * S * 64u};
+    Item in_it{t0, s_begin, (t0 * S + s_begin) * 64u};
     uint32_t issued = 0;
     auto issue = [&](Buf<FMT> &b) {
 #pragma unroll
@@ -316,7 +392,7 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
             }
         }
     };
-    Item c_it{wave0, 0, wave0 * S * 64u};
+    Item c_it{wave0, s_begin, (wave0 * S + s_begin) * 64u};
     uint32_t c_k = 0;
     float acc[NC];
 #pragma unroll
@@ -337,12 +413,14 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
                     compute_unit<FMT, NC>(lds, col_bytes, n_in, col, b.u[i], acc);
 #pragma unroll
                 for (int c = 0; c < NC; c++) acc[c] = pad ? keep[c] : acc[c];
-                if (c_it.s == S - 1) {
-                    const int64_t row = (int64_t)c_it.tile * L.R + r;
+                if (c_it.s == s_end - 1) {
+                    const int64_t row = (int64_t)c_it.tile * R + r;
 #pragma unroll
                     for (int c = 0; c < NC; c++) {
                         const float v = group_sum(acc[c], G);
-                        if (g == 0 && row < sg.n_out) sg.y[c * sg.ldy + row] = v;
+                        if (g == 0 && row < out_rows)
+                            __hip_atomic_store(out + c * out_ld + row, v, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
                         acc[c] = 0.0f;
                     }
                 }
@@ -352,56 +430,67 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
         }
     };
 
+    // activation blocks of the columns this workgroup's rounds read
+    const int64_t b0 = (int64_t)s_begin * G;
+    const int64_t b1 = (int64_t)s_end * G < sg.ncols ? (int64_t)s_end * G : (int64_t)sg.ncols;
     Buf<FMT> bufA, bufB;
     XFirst<XP> xf;
-    if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf);
+    if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf, b0, b1);
     issue(bufA);
-    stage_activations<PAIR, XP>(A, lds, xf);
+    stage_activations<PAIR, XP>(A, lds, xf, b0, b1);
     if (total == 1) {  // one round: no second buffer (it would reload the same round)
         __syncthreads();
         consume(bufA);
-        return;
-    }
-    issue(bufB);
-    __syncthreads();
-    if (total == 0) return;  // a wave without rows only helped to stage
-
-    // Two buffers in flight: each buffer is refilled right after it has been
-    // decoded, so a refill never overwrites registers with a load pending and
-    // every wait covers one buffer only. The steady-state loop has one exit
-    // at the top and unconditional refills, so the memory counters always
-    // hold the two buffers in the same order and each wait is for the older
-    // one alone. The last 1-3 buffers drain without redundant refills.
-    const uint32_t nbuf = (total + ITEMS - 1) / ITEMS;
-    uint32_t i = 0;  // next buffer to decode; A holds it, B the one after
-    while (i + 4 <= nbuf) {
-        consume(bufA);
-        issue(bufA);
-        consume(bufB);
+    } else {
         issue(bufB);
-        i += 2;
+        __syncthreads();
+        // a wave without rows (total == 0) only helped to stage
+        if (total != 0) {
+            // Two buffers in flight: each buffer is refilled right after it
+            // has been decoded, so a refill never overwrites registers with a
+            // load pending and every wait covers one buffer only. The
+            // steady-state loop has one exit at the top and unconditional
+            // refills, so the memory counters always hold the two buffers in
+            // the same order and each wait is for the older one alone. The
+            // last 1-3 buffers drain without redundant refills.
+            const uint32_t nbuf = (total + ITEMS - 1) / ITEMS;
+            uint32_t i = 0;  // next buffer to decode; A holds it, B the one after
+            while (i + 4 <= nbuf) {
+                consume(bufA);
+                issue(bufA);
+                consume(bufB);
+                issue(bufB);
+                i += 2;
+            }
+            const uint32_t left = nbuf - i;  // 1..3
+            consume(bufA);
+            if (left == 3) issue(bufA);
+            if (left >= 2) consume(bufB);
+            if (left == 3) consume(bufA);
+        }
     }
-    const uint32_t left = nbuf - i;  // 1..3
-    consume(bufA);
-    if (left == 3) issue(bufA);
-    if (left >= 2) consume(bufB);
-    if (left == 3) consume(bufA);
+    if constexpr (SPLIT)
+        if (split) split_reduce<NC>(sg, grp, ntiles * R,
+                         reinterpret_cast<uint32_t *>(lds + (int64_t)A.nc * A.col_bytes));
 }
 
-template <uint32_t F0, uint32_t F1, int NC, int XP>
+// MULTI: the matrices of grid row blockIdx.y (a launch of several);
+// otherwise the one matrix seg[0], with a grid of exactly its workgroups.
+template <uint32_t F0, uint32_t F1, int NC, int XP, bool SPLIT, bool MULTI>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     static_assert(pair_of(F0) == pair_of(F1), "one launch stages one activation format");
-    // segment of this workgroup (wave-uniform)
-    int s = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxSegs; i++)
-        if (i < A.nseg && blockIdx.x >= A.seg[i].wg_begin) s = i;
-    const MVSeg &sg = A.seg[s];
-    if (F0 == F1 || sg.L.type == F0)
-        matvec_body<F0, NC, XP>(A, sg, lds);
-    else
-        matvec_body<F1, NC, XP>(A, sg, lds);
+    static_assert(MULTI || F0 == F1, "formats mix only in launches of several matrices");
+    if constexpr (MULTI) {
+        const MVSeg &sg = A.seg[blockIdx.y];
+        if (blockIdx.x >= sg.nwg) return;  // the whole workgroup, before any barrier
+        if (F0 == F1 || sg.type == F0)
+            matvec_body<F0, NC, XP, SPLIT>(A, sg, lds);
+        else
+            matvec_body<F1, NC, XP, SPLIT>(A, sg, lds);
+    } else {
+        matvec_body<F0, NC, XP, SPLIT>(A, A.seg[0], lds);
+    }
 }
 
 // ---- standalone quantizers (global output in the reference block layouts) --

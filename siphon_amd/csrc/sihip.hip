@@ -43,6 +43,12 @@ struct sihip_weight {
     uint8_t *dev;
     uint8_t *gemm = nullptr;  // GEMM-ordered copy, built on the first prefill call
     int64_t gemm_bytes = 0;
+    // column slices of the matvec (split == 1: whole rows per workgroup);
+    // part and cnt live in the same allocation as the planes
+    uint32_t split = 1, spr = 0;
+    float *part = nullptr;
+    uint32_t *cnt = nullptr;
+    int64_t split_bytes = 0;
 };
 
 static char g_init_err[512];
@@ -132,6 +138,13 @@ static int wave_target() {
     return v > 0 ? v : 800;
 }
 
+// Activation elements per column slice (slice_rounds in formats.h);
+// SIHIP_SPLIT_ELEMS overrides kSliceElems (0: no slices).
+static int64_t split_elems() {
+    const char *e = getenv("SIHIP_SPLIT_ELEMS");
+    return e ? atol(e) : kSliceElems;
+}
+
 // Columns (super-blocks for K-quants, 32-element units otherwise) per wave
 // tile: the smallest power of two that keeps at least 80% of the lanes busy
 // and gives at least wave_target() row tiles (about one per resident wave
@@ -141,11 +154,29 @@ static int wave_target() {
 // long rows, e.g. a 1024-row kv projection) takes wider tiles at down to 50%
 // busy lanes: padding slots cost lanes but no memory traffic (they re-read a
 // real column), and more waves in flight matter more there.
+//
+// Rows of at least two slice lengths are cut into column slices; their tiles
+// are narrow, 4 super-blocks (K-quants) or 8 blocks wide, so that a wave
+// keeps several rounds per slice (measured on rows of 14336 and 27648: 4-29%
+// faster than the widest tiles without slices), and wider only while the
+// launch would have fewer than 256 workgroups.
 static int choose_G(uint32_t type, int64_t n_out, int64_t n_in) {
     const int64_t ncols = is_kquant(type) ? n_in / 256 : n_in / 32;
     if (const char *f = getenv("SIHIP_TILE_COLS")) {
         const int G = atoi(f);
         if (G >= 1 && G <= 64 && !(G & (G - 1))) return G;
+    }
+    const int64_t elems = split_elems();
+    if (sliced_rows(n_in, elems)) {
+        int G = is_kquant(type) ? 4 : 8;
+        for (; G < 64; G *= 2) {
+            Layout L;
+            if (!make_layout(type, n_out, n_in, G, &L)) break;
+            const int64_t spr = slice_rounds(L, elems);
+            const int64_t wgs = (L.ntiles + kWaves - 1) / kWaves * ((L.S + spr - 1) / spr);
+            if (wgs >= 256) break;
+        }
+        return G;
     }
     const int64_t target = wave_target();
     auto pick = [&](int pct) {
@@ -187,9 +218,16 @@ extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out
     Layout L;
     if (!make_layout(type, (int64_t)n_out, (int64_t)n_in, choose_G(type, n_out, n_in), &L))
         return set_err(ctx, SIHIP_EINVAL, "weight_upload: no layout for this shape");
+    const uint32_t spr = (uint32_t)slice_rounds(L, split_elems());
+    const uint32_t split = (uint32_t)((L.S + spr - 1) / spr);
+    // slices: partial sums for up to kMaxCols columns, then one counter per
+    // group of kWaves row tiles
+    const int64_t part_bytes = split > 1 ? (int64_t)split * kMaxCols * L.ntiles * L.R * 4 : 0;
+    const int64_t cnt_bytes = split > 1 ? ((L.ntiles + kWaves - 1) / kWaves) * 4 : 0;
+    const int64_t alloc = L.total_bytes + part_bytes + cnt_bytes;
     uint8_t *dev = nullptr;
-    if (hipMalloc((void **)&dev, (size_t)L.total_bytes) != hipSuccess)
-        return set_err(ctx, SIHIP_ENOMEM, "weight_upload: %lld device bytes", (long long)L.total_bytes);
+    if (hipMalloc((void **)&dev, (size_t)alloc) != hipSuccess)
+        return set_err(ctx, SIHIP_ENOMEM, "weight_upload: %lld device bytes", (long long)alloc);
     uint8_t *raw = nullptr;
     if (hipMalloc((void **)&raw, (size_t)bytes) != hipSuccess) {
         (void)hipFree(dev);
@@ -200,7 +238,7 @@ extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out
     const int64_t recs = (type == T_F16) ? nunits : (int64_t)(n_in / be);
     const int64_t rec_bytes = (type == T_F16) ? 64 : bb;
     const int64_t total = (int64_t)n_out * recs;
-    hipError_t e = hipMemsetAsync(dev, 0, (size_t)L.total_bytes, ctx->stream);
+    hipError_t e = hipMemsetAsync(dev, 0, (size_t)alloc, ctx->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(raw, host_blocks, (size_t)bytes, hipMemcpyHostToDevice, ctx->stream);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(repack_kernel, dim3((unsigned)((total + kThreads - 1) / kThreads)),
@@ -217,6 +255,13 @@ extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out
     sihip_weight *w = new sihip_weight();
     w->L = L;
     w->dev = dev;
+    w->split = split;
+    w->spr = spr;
+    if (split > 1) {
+        w->part = reinterpret_cast<float *>(dev + L.total_bytes);
+        w->cnt = reinterpret_cast<uint32_t *>(dev + L.total_bytes + part_bytes);
+        w->split_bytes = part_bytes + cnt_bytes;
+    }
     *out = w;
     return rc;
 }
@@ -231,43 +276,69 @@ extern "C" int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w) {
 }
 
 extern "C" uint64_t sihip_weight_device_bytes(const sihip_weight *w) {
-    return w ? (uint64_t)(w->L.total_bytes + w->gemm_bytes) : 0;
+    return w ? (uint64_t)(w->L.total_bytes + w->split_bytes + w->gemm_bytes) : 0;
 }
 
 extern "C" int sihip_weight_tile_cols(const sihip_weight *w) { return w ? w->L.G : 0; }
 
+extern "C" int sihip_weight_slice_rounds(const sihip_weight *w) { return w ? (int)w->spr : 0; }
+
 // ---- launches -----------------------------------------------------------------
 
 // Q8_K passes of the activation loaded before the weights: all four for
-// long rows of a single column where the kernel has register room (the
-// instances with Q6_K run at 2 waves per SIMD with registers to spare),
-// else the first.
+// long unsliced rows of a single column where the kernel has register room
+// (the instances with Q6_K run at 2 waves per SIMD with registers to
+// spare), else the first. Launches with sliced matrices take one pass (a
+// slice of about 4096 elements is one).
 template <uint32_t F0, uint32_t F1>
 static int prologue_passes(const MVArgs &A) {
     if (pair_of(F0) != T_Q8_K || A.nc != 1 || A.n_in <= 4096) return 1;
     return (F0 == T_Q6_K || F1 == T_Q6_K) ? 4 : 1;
 }
 
-template <uint32_t F0, uint32_t F1, int NC>
-static hipError_t launch_nc(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
-    if constexpr (NC == 1 && pair_of(F0) == T_Q8_K) {
+static bool any_sliced(const MVArgs &A) {
+    for (int i = 0; i < A.nseg; i++)
+        if (A.seg[i].split > 1) return true;
+    return false;
+}
+
+template <uint32_t F0, uint32_t F1, int NC, bool MULTI>
+static hipError_t launch_nc(const MVArgs &A, dim3 grid, size_t lds, hipStream_t st) {
+    if (any_sliced(A)) {
+        hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 1, true, MULTI>), grid, dim3(kThreads), lds,
+                           st, A);
+        return hipGetLastError();
+    }
+    if constexpr (NC == 1 && (F0 == T_Q6_K || F1 == T_Q6_K)) {
         if (prologue_passes<F0, F1>(A) == 4) {
-            hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 4>), dim3(grid), dim3(kThreads), lds, st, A);
+            hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 4, false, MULTI>), grid, dim3(kThreads),
+                               lds, st, A);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 1>), dim3(grid), dim3(kThreads), lds, st, A);
+    hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 1, false, MULTI>), grid, dim3(kThreads), lds, st,
+                       A);
     return hipGetLastError();
 }
 
+// Launches of several matrices are single-column (gemv_multi); a launch of
+// one matrix takes 1, 2, 4 or 8 columns (at most 4 for the K-quants).
 template <uint32_t F0, uint32_t F1>
-static hipError_t launch_fmt(const MVArgs &A, int grid, size_t lds, hipStream_t st) {
-    switch (A.nc) {
-        case 1: return launch_nc<F0, F1, 1>(A, grid, lds, st);
-        case 2: return launch_nc<F0, F1, 2>(A, grid, lds, st);
-        case 4: return launch_nc<F0, F1, 4>(A, grid, lds, st);
-        case 8: return launch_nc<F0, F1, 8>(A, grid, lds, st);
-        default: return hipErrorInvalidValue;
+static hipError_t launch_fmt(const MVArgs &A, dim3 grid, size_t lds, hipStream_t st) {
+    if (A.nseg > 1)
+        return A.nc == 1 ? launch_nc<F0, F1, 1, true>(A, grid, lds, st) : hipErrorInvalidValue;
+    if constexpr (F0 != F1) {
+        return hipErrorInvalidValue;
+    } else {
+        switch (A.nc) {
+            case 1: return launch_nc<F0, F0, 1, false>(A, grid, lds, st);
+            case 2: return launch_nc<F0, F0, 2, false>(A, grid, lds, st);
+            case 4: return launch_nc<F0, F0, 4, false>(A, grid, lds, st);
+            case 8:
+                if constexpr (!is_kquant(F0)) return launch_nc<F0, F0, 8, false>(A, grid, lds, st);
+                return hipErrorInvalidValue;
+            default: return hipErrorInvalidValue;
+        }
     }
 }
 
@@ -277,7 +348,7 @@ static bool mix_supported(uint32_t f0, uint32_t f1) {
     return f0 == f1 || (f0 == T_Q4_K && f1 == T_Q6_K) || (f0 == T_Q5_K && f1 == T_Q6_K);
 }
 
-static hipError_t launch_any(const MVArgs &A, uint32_t f0, uint32_t f1, int grid, size_t lds,
+static hipError_t launch_any(const MVArgs &A, uint32_t f0, uint32_t f1, dim3 grid, size_t lds,
                              hipStream_t st) {
     if (f0 == T_Q4_K && f1 == T_Q6_K) return launch_fmt<T_Q4_K, T_Q6_K>(A, grid, lds, st);
     if (f0 == T_Q5_K && f1 == T_Q6_K) return launch_fmt<T_Q5_K, T_Q6_K>(A, grid, lds, st);
@@ -300,11 +371,15 @@ static int64_t col_bytes_aligned(uint32_t pair, int64_t n_in) {
     return (lds_col_bytes(pair, n_in) + 15) & ~(int64_t)15;
 }
 
+// LDS bytes past the activation columns of a launch with a sliced matrix
+// (the arrival flag of split_reduce).
+constexpr int64_t kSliceLds = 16;
+
 // Largest supported column count (1, 2, 4 or 8) whose LDS fits.
 static int max_cols(const sihip_ctx *ctx, uint32_t pair, int64_t n_in) {
     const int64_t cb = col_bytes_aligned(pair, n_in);
     for (int nc = kMaxCols; nc >= 1; nc >>= 1)
-        if ((size_t)(cb * nc) <= ctx->lds_limit) return nc;
+        if ((size_t)(cb * nc + kSliceLds) <= ctx->lds_limit) return nc;
     return 0;
 }
 
@@ -330,20 +405,26 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         return set_err(ctx, SIHIP_ERANGE, "activation row of %lld does not fit in LDS",
                        (long long)n_in);
     if (is_kquant(f1) && ncmax > 4) ncmax = 4;  // 8 K-quant columns exceed the VGPR file
+    if (count > 1) {
+        if (M != 1) return set_err(ctx, SIHIP_EINVAL, "a launch of several matrices takes one column");
+        ncmax = 1;
+    }
     const int64_t cb = col_bytes_aligned(pair, n_in);
     // workgroups: one row tile per wave when the chip has room; otherwise
     // each matrix gets a share of the cap proportional to its bytes
     const int64_t wg_cap = (int64_t)ctx->n_cu * wgs_per_cu();
+    // (a sliced matrix always takes one workgroup per tile group and slice)
     int64_t want[kMaxSegs], nwg[kMaxSegs], want_sum = 0, bytes_sum = 0;
     for (int i = 0; i < count; i++) {
         const int64_t ntiles = (n_out[i] + w[i]->L.R - 1) / w[i]->L.R;
         want[i] = (ntiles + kWaves - 1) / kWaves;
+        if (w[i]->split > 1) want[i] *= w[i]->split;
         want_sum += want[i];
         bytes_sum += w[i]->L.total_bytes;
     }
     for (int i = 0; i < count; i++) {
         nwg[i] = want[i];
-        if (want_sum > wg_cap) {
+        if (want_sum > wg_cap && w[i]->split == 1) {
             const int64_t share = (int64_t)((double)wg_cap * (double)w[i]->L.total_bytes /
                                             (double)bytes_sum);
             nwg[i] = share < 1 ? 1 : (share < want[i] ? share : want[i]);
@@ -357,15 +438,25 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         memset(&A, 0, sizeof(A));
         uint32_t wg = 0;
         for (int i = 0; i < count; i++) {
+            const Layout &L = w[i]->L;
             MVSeg &sg = A.seg[i];
-            sg.w = w[i]->dev;
-            sg.L = w[i]->L;
+            for (int p = 0; p < 4; p++) sg.plane[p] = w[i]->dev + L.plane_off[p];
             sg.y = y[i] + m * ldy[i];
             sg.ldy = ldy[i];
-            sg.n_out = n_out[i];
-            sg.wg_begin = wg;
+            sg.part = w[i]->part;
+            sg.cnt = w[i]->cnt;
+            sg.split = w[i]->split;
+            sg.spr = w[i]->spr;
+            sg.type = L.type;
+            sg.n_out = (uint32_t)n_out[i];
+            sg.ntiles = (uint32_t)((n_out[i] + L.R - 1) / L.R);
             sg.nwg = (uint32_t)nwg[i];
-            wg += (uint32_t)nwg[i];
+            sg.G = (uint32_t)L.G;
+            sg.logG = (uint32_t)L.logG;
+            sg.R = (uint32_t)L.R;
+            sg.S = (uint32_t)L.S;
+            sg.ncols = (uint32_t)L.ncols;
+            wg = (uint32_t)nwg[i] > wg ? (uint32_t)nwg[i] : wg;
         }
         A.nseg = count;
         A.n_in = n_in;
@@ -375,7 +466,9 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         A.ldxq = ldxq;
         A.nc = nc;
         A.col_bytes = cb;
-        const hipError_t e = launch_any(A, f0, f1, (int)wg, (size_t)(cb * nc), st);
+        const hipError_t e =
+            launch_any(A, f0, f1, dim3(wg, (unsigned)count),
+                       (size_t)(cb * nc + (any_sliced(A) ? kSliceLds : 0)), st);
         if (e != hipSuccess)
             return set_err(ctx, SIHIP_EDEVICE, "matvec launch: %s", hipGetErrorString(e));
         m += nc;

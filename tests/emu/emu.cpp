@@ -47,24 +47,31 @@ static void stage(uint32_t pair, int64_t n, const uint8_t *xq, uint8_t *col) {
     }
 }
 
+// spr: rounds per column slice (slice_rounds); the partial sums of the
+// slices are added in slice order, starting from 0.0f, as the kernel's
+// reduction does; one slice (spr == L.S) is the row's value itself.
 template <uint32_t FMT>
-static void run(const Layout &L, const uint8_t *W, const uint8_t *lds, int64_t cb, float *y) {
+static void run(const Layout &L, const uint8_t *W, const uint8_t *lds, int64_t cb, int64_t spr,
+                float *y) {
     Planes P;
     for (int p = 0; p < 4; p++) P.p[p] = W + L.plane_off[p];
     for (int64_t tile = 0; tile < L.ntiles; tile++) {
         for (int r = 0; r < L.R; r++) {
             const int64_t row = tile * L.R + r;
+            float yrow = 0.0f;
+            for (int64_t s0 = 0; s0 < L.S; s0 += spr) {
+            const int64_t s1 = s0 + spr < L.S ? s0 + spr : L.S;
             std::vector<float> v(L.G, 0.0f);
             for (int g = 0; g < L.G; g++) {
                 const uint32_t lane = (uint32_t)(r * L.G + g);
                 float acc[1] = {0.0f};
-                // every round of the tile; a padding slot (column past the
+                // the rounds of the slice; a padding slot (column past the
                 // row, last round only) re-reads the row's last real column
                 // of that round and its contribution is discarded
                 const int64_t glast = L.ncols - 1 - (L.S - 1) * L.G;
                 const uint32_t lane_last =
                     (uint32_t)(r * L.G + (g < glast ? g : glast));
-                for (int64_t s = 0; s < L.S; s++) {
+                for (int64_t s = s0; s < s1; s++) {
                     int64_t col = s * L.G + g;
                     const bool pad = col > L.ncols - 1;
                     if (pad) col = L.ncols - 1;
@@ -92,7 +99,9 @@ static void run(const Layout &L, const uint8_t *W, const uint8_t *lds, int64_t c
                 for (int g = 0; g < L.G; g++) nv[g] = v[g] + v[reduce_partner(g, k)];
                 v = nv;
             }
-            if (row < L.n_out) y[row] = v[0];
+            yrow = spr >= L.S ? v[0] : yrow + v[0];
+            }
+            if (row < L.n_out) y[row] = yrow;
         }
     }
 }
@@ -122,11 +131,14 @@ int emu_repack(uint32_t type, int64_t n_out, int64_t n_in, int G, const uint8_t 
     return 0;
 }
 
-// Full emulated matvec: rows (GGUF bytes) x pair-format activation -> y.
-int emu_gemv_pair(uint32_t type, int64_t n_out, int64_t n_in, int G, const uint8_t *rows,
-                  const uint8_t *xq, float *y) {
+// Full emulated matvec: rows (GGUF bytes) x pair-format activation -> y,
+// with column slices of about slice_elems elements (< 0: the library's
+// default kSliceElems, 0: none).
+int emu_gemv_pair(uint32_t type, int64_t n_out, int64_t n_in, int G, int64_t slice_elems,
+                  const uint8_t *rows, const uint8_t *xq, float *y) {
     Layout L;
     if (!make_layout(type, n_out, n_in, G, &L)) return -1;
+    const int64_t spr = slice_rounds(L, slice_elems < 0 ? kSliceElems : slice_elems);
     std::vector<uint8_t> dev((size_t)L.total_bytes);
     if (emu_repack(type, n_out, n_in, G, rows, dev.data())) return -1;
     const uint32_t pair = pair_of(type);
@@ -134,15 +146,15 @@ int emu_gemv_pair(uint32_t type, int64_t n_out, int64_t n_in, int G, const uint8
     std::vector<uint8_t> lds((size_t)cb, 0);
     stage(pair, n_in, xq, lds.data());
     switch (type) {
-        case T_F16:  run<T_F16>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q4_0: run<T_Q4_0>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q5_0: run<T_Q5_0>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q8_0: run<T_Q8_0>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q2_K: run<T_Q2_K>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q3_K: run<T_Q3_K>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q4_K: run<T_Q4_K>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q5_K: run<T_Q5_K>(L, dev.data(), lds.data(), cb, y); break;
-        case T_Q6_K: run<T_Q6_K>(L, dev.data(), lds.data(), cb, y); break;
+        case T_F16:  run<T_F16>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q4_0: run<T_Q4_0>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q5_0: run<T_Q5_0>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q8_0: run<T_Q8_0>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q2_K: run<T_Q2_K>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q3_K: run<T_Q3_K>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q4_K: run<T_Q4_K>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q5_K: run<T_Q5_K>(L, dev.data(), lds.data(), cb, spr, y); break;
+        case T_Q6_K: run<T_Q6_K>(L, dev.data(), lds.data(), cb, spr, y); break;
         default: return -1;
     }
     return 0;

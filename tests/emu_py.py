@@ -16,18 +16,22 @@ class Emulator:
         L = ctypes.CDLL(SO)
         vp = ctypes.c_void_p
         L.emu_gemv_pair.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
-                                    vp, vp, vp]
+                                    ctypes.c_int64, vp, vp, vp]
         L.emu_layout_bytes.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
         L.emu_layout_bytes.restype = ctypes.c_int64
         L.emu_repack.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, vp, vp]
         self.L = L
 
-    def gemv_pair(self, wtype, n_out, n_in, G, rows, xq):
+    def gemv_pair(self, wtype, n_out, n_in, G, rows, xq, slice_elems=None):
+        """slice_elems: column slice length as the library reads it from
+        SIHIP_SPLIT_ELEMS at upload (None: that variable, else the default)."""
+        if slice_elems is None:
+            slice_elems = int(os.environ.get("SIHIP_SPLIT_ELEMS", "-1"))
         rows = np.ascontiguousarray(rows, dtype=np.uint8)
         xq = np.ascontiguousarray(xq, dtype=np.uint8)
         y = np.zeros(n_out, dtype=np.float32)
-        rc = self.L.emu_gemv_pair(wtype, n_out, n_in, G, rows.ctypes.data, xq.ctypes.data,
-                                  y.ctypes.data)
+        rc = self.L.emu_gemv_pair(wtype, n_out, n_in, G, slice_elems, rows.ctypes.data,
+                                  xq.ctypes.data, y.ctypes.data)
         assert rc == 0
         return y
 

@@ -30,6 +30,31 @@ def test_emulated_matvec_vs_oracle(oracle, emu, wt):
             assert np.all(err <= 1e-5 * l1 + 1e-6), (siq.NAMES[wt], n_out, n_in, G)
 
 
+@pytest.mark.parametrize("wt", siq.WEIGHT_TYPES, ids=lambda t: siq.NAMES[t])
+def test_emulated_column_slices_vs_oracle(oracle, emu, wt):
+    """Rows cut into column slices (one round per slice up to the whole
+    row), the partial sums added in slice order, stay within tolerance of
+    the oracle; a slice length of at least the row is the unsliced kernel
+    bit for bit."""
+    rng = np.random.default_rng(700 + wt)
+    n_out, n_in = (21, 2304) if wt in KQ else (21, 1120)
+    W = synth.make_weights(wt, n_out, n_in, rng)
+    x = rng.standard_normal(n_in).astype(np.float32)
+    xq = oracle.quantize(siq.PAIR[wt], x)
+    ref = np.zeros(n_out)
+    l1 = np.zeros(n_out)
+    for r in range(n_out):
+        ref[r], l1[r] = oracle.vec_dot(wt, n_in, W[r], xq)
+    for G in [1, 2, 8, 64]:
+        whole = emu.gemv_pair(wt, n_out, n_in, G, W, xq, slice_elems=0)
+        same = emu.gemv_pair(wt, n_out, n_in, G, W, xq, slice_elems=n_in)
+        assert np.array_equal(whole.view(np.uint32), same.view(np.uint32))
+        for elems in [1, 256, 1024]:
+            y = emu.gemv_pair(wt, n_out, n_in, G, W, xq, slice_elems=elems)
+            err = np.abs(y - ref)
+            assert np.all(err <= 1e-5 * l1 + 1e-6), (siq.NAMES[wt], G, elems)
+
+
 def test_repack_is_a_permutation(emu):
     """Device bytes hold every GGUF byte's information: repacking a matrix
     whose every bit is set gives exactly as many set bits as the GGUF bytes
