@@ -474,6 +474,17 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
                          reinterpret_cast<uint32_t *>(lds + (int64_t)A.nc * A.col_bytes));
 }
 
+// Requests every kernel argument a wave uses before its first branch, so
+// that they arrive in one round trip of scalar loads (the compiler would
+// otherwise load some after the first test and pay a second one).
+__device__ inline void request_args(const MVArgs &A, const MVSeg &sg) {
+    asm volatile("" ::"s"(sg.plane[0]), "s"(sg.plane[1]), "s"(sg.plane[2]), "s"(sg.plane[3]),
+                 "s"(sg.y), "s"(sg.ldy), "s"(sg.part), "s"(sg.cnt), "s"(sg.split), "s"(sg.spr),
+                 "s"(sg.type), "s"(sg.n_out), "s"(sg.ntiles), "s"(sg.nwg), "s"(sg.G),
+                 "s"(sg.logG), "s"(sg.R), "s"(sg.S), "s"(sg.ncols), "s"(A.x), "s"(A.xq),
+                 "s"(A.ldx), "s"(A.ldxq), "s"(A.n_in), "s"(A.nc), "s"(A.col_bytes));
+}
+
 // MULTI: the matrices of grid row blockIdx.y (a launch of several);
 // otherwise the one matrix seg[0], with a grid of exactly its workgroups.
 template <uint32_t F0, uint32_t F1, int NC, int XP, bool SPLIT, bool MULTI>
@@ -481,15 +492,16 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MVArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     static_assert(pair_of(F0) == pair_of(F1), "one launch stages one activation format");
     static_assert(MULTI || F0 == F1, "formats mix only in launches of several matrices");
+    const MVSeg sg = A.seg[MULTI ? blockIdx.y : 0];
+    request_args(A, sg);
     if constexpr (MULTI) {
-        const MVSeg &sg = A.seg[blockIdx.y];
         if (blockIdx.x >= sg.nwg) return;  // the whole workgroup, before any barrier
         if (F0 == F1 || sg.type == F0)
             matvec_body<F0, NC, XP, SPLIT>(A, sg, lds);
         else
             matvec_body<F1, NC, XP, SPLIT>(A, sg, lds);
     } else {
-        matvec_body<F0, NC, XP, SPLIT>(A, A.seg[0], lds);
+        matvec_body<F0, NC, XP, SPLIT>(A, sg, lds);
     }
 }
 
