@@ -31,6 +31,7 @@
 // so a lane's 16 bytes are contiguous.
 #pragma once
 
+#include "agent.h"
 #include "formats.h"
 #include "quant.h"
 #include "unit.h"
@@ -44,18 +45,22 @@ typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kGemmThreads = 256;
-#ifndef SIHIP_GEMM_MT
-#define SIHIP_GEMM_MT 2
-#endif
-constexpr int kGemmBM = 32 * SIHIP_GEMM_MT;    // activation rows per workgroup
 constexpr int kGemmBN = 128;                   // weight rows per workgroup (32 per wave)
-constexpr int kGemmMT = kGemmBM / 32;          // 32-row MFMA tiles per wave along m
-constexpr int kGemmWaves = kGemmMT <= 2 ? 2 : 1;  // waves per SIMD the registers allow
 constexpr int kXRow = 256 + 16;                // LDS bytes per activation row (padded)
-constexpr int kXQBytes = kGemmBM * kXRow;      // quant tile
-constexpr int kXDOff = kXQBytes;               // f32 dx[BM]
-constexpr int kXBOff = kXDOff + kGemmBM * 4;   // f16 bsums[BM][16]
-constexpr int kXTile = kXBOff + kGemmBM * 32;  // one LDS buffer
+
+// Tile geometry for MT 32-row MFMA tiles per wave along m (BM activation
+// rows per workgroup) and the LDS activation buffer of one super-block.
+template <int MT>
+struct GemmGeo {
+    static constexpr int BM = 32 * MT;
+    static constexpr int XQBytes = BM * kXRow;       // quant tile
+    static constexpr int XDOff = XQBytes;            // f32 dx[BM]
+    static constexpr int XBOff = XDOff + BM * 4;     // f16 bsums[BM][16]
+    static constexpr int XTile = XBOff + BM * 32;    // one LDS buffer
+    static constexpr int XPieces = BM * 16 / kGemmThreads;  // 16-byte quant pieces per thread
+    static constexpr int XE = BM * 2 + BM / 4;       // 16-byte pieces of group sums + scales
+    static constexpr int XEPieces = (XE + kGemmThreads - 1) / kGemmThreads;
+};
 
 // Activation planes written by gemm_quantize_x (Mp = M rounded up to BM;
 // rows M..Mp-1 are zero).
@@ -73,6 +78,14 @@ struct GemmArgs {
     float *y;
     int64_t ldy;
     int MB, NB;          // workgroup tiles along m and n
+    // K slices (S == 1: one workgroup per output tile). S > 1: slice s of
+    // a tile covers super-blocks [s * SBK, (s + 1) * SBK); its partial sums
+    // go to part[(s * Mp + m) * NB * BN + n] and the last slice of the tile
+    // to arrive (counted in cnt[mblk * NB + nblk], zero between launches)
+    // adds them in slice order into y and resets the counter.
+    int S, SBK;
+    float *part;
+    uint32_t *cnt;
 };
 
 __host__ __device__ inline int64_t gemm_x_bytes(int64_t Mp, int64_t K) {
@@ -183,10 +196,6 @@ __device__ inline void gemm_load_w(const uint8_t *blk_base, int64_t c, int lane,
     w.m = *reinterpret_cast<const U4 *>(chunk + 4096 + 16 * (lane & 31));
 }
 
-constexpr int kXPieces = kGemmBM * 16 / kGemmThreads;  // 16-byte quant pieces per thread
-constexpr int kXE = kGemmBM * 2 + kGemmBM / 4;  // 16-byte pieces of group sums + scales
-constexpr int kXEPieces = (kXE + kGemmThreads - 1) / kGemmThreads;
-
 __device__ inline uint32_t bytes_times(uint32_t q, uint32_t f) {
     // bytewise q * f for bytes and products below 256 (no carries between bytes)
     const u16x2_t a = __builtin_bit_cast(u16x2_t, q);
@@ -194,17 +203,30 @@ __device__ inline uint32_t bytes_times(uint32_t q, uint32_t f) {
     return __builtin_bit_cast(uint32_t, (u16x2_t)(a * b));
 }
 
-template <uint32_t FMT>
+// MT: 32-row MFMA tiles per wave along m (2 for large M; 1 for small M,
+// which doubles the workgroups). NBUF: super-blocks of weights in flight
+// per wave (registers for 4 fit at MT = 1), so a small-M launch, whose few
+// workgroups each stream a long run of weights, keeps more bytes in flight.
+template <uint32_t FMT, int MT, int NBUF>
 __global__ __launch_bounds__(kGemmThreads)
-__attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel(GemmArgs A) {
+__attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
     static_assert(FMT == T_Q4_K, "MFMA prefill: Q4_K");
-    __shared__ __attribute__((aligned(16))) uint8_t sx[2][kXTile];
+    static_assert(NBUF % 2 == 0, "LDS buffers alternate with the super-block parity");
+    using Geo = GemmGeo<MT>;
+    constexpr int kGemmMT = MT;
+    constexpr int kGemmBM = Geo::BM;
+    constexpr int kXDOff = Geo::XDOff, kXBOff = Geo::XBOff;
+    constexpr int kXPieces = Geo::XPieces, kXE = Geo::XE, kXEPieces = Geo::XEPieces;
+    __shared__ __attribute__((aligned(16))) uint8_t sx[2][Geo::XTile];
     // XCD-aware tile order: workgroups are dispatched round-robin over the 8
     // XCDs, so the m-tiles of one n-tile (which read the same weights) are
     // given to consecutive workgroups of the same XCD and share its L2.
+    // (the m-tiles of one n-tile and K slice are consecutive)
     const int b = blockIdx.x;
     const int xcd = b & 7, t = b >> 3;
-    const int nblk = (t / A.MB) * 8 + xcd, mblk = t % A.MB;
+    const int per = A.MB * A.S;
+    const int nblk = (t / per) * 8 + xcd, rest = t % per;
+    const int slice = rest / A.MB, mblk = rest % A.MB;
     if (nblk >= A.NB) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ln = lane & 31, h = lane >> 5;
@@ -338,41 +360,102 @@ __attribute__((amdgpu_waves_per_eu(kGemmWaves, kGemmWaves))) void gemm_kq_kernel
         }
     };
 
-    // Two weight buffers and two LDS activation buffers in ping-pong: the
-    // loads of super-block c + 1 are issued before super-block c is
-    // computed. Loads are unconditional (past the end they repeat the last
-    // super-block), so the memory counters always hold them in issue order.
-    const int64_t last = A.nb - 1;
-    GemmW wa, wb;
-    load_x(0);
-    gemm_load_w(wblk, 0, lane, wa);
+    // A ring of NBUF weight buffers and two LDS activation buffers in
+    // ping-pong: the weights of super-block c + NBUF - 1 and the activation
+    // tile of c + 1 are requested before c is computed. Loads are
+    // unconditional (past the end they repeat the last super-block), so the
+    // memory counters always hold them in issue order.
+    const int64_t c0 = (int64_t)slice * A.SBK;
+    const int64_t last = (c0 + A.SBK < A.nb ? c0 + A.SBK : A.nb) - 1;  // this slice's super-blocks
+    auto clamp = [&](int64_t c) { return c < last ? c : last; };
+    GemmW wb[NBUF];
+    load_x(c0);
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; k++) gemm_load_w(wblk, clamp(c0 + k), lane, wb[k]);
     store_x(sx[0]);
     __syncthreads();
-    for (int64_t c = 0;; c += 2) {
-        const int64_t c1 = c + 1 < last ? c + 1 : last;
-        load_x(c1);
-        gemm_load_w(wblk, c1, lane, wb);
-        compute(sx[0], wa);
-        store_x(sx[1]);
-        __syncthreads();
-        if (c + 1 > last) break;
-        const int64_t c2 = c + 2 < last ? c + 2 : last;
-        load_x(c2);
-        gemm_load_w(wblk, c2, lane, wa);
-        compute(sx[1], wb);
-        store_x(sx[0]);
-        __syncthreads();
-        if (c + 2 > last) break;
+    for (int64_t c = c0;; c += NBUF) {
+        bool done = false;
+#pragma unroll
+        for (int k = 0; k < NBUF; k++) {
+            const int64_t cc = c + k;
+            gemm_load_w(wblk, clamp(cc + NBUF - 1), lane, wb[(k + NBUF - 1) % NBUF]);
+            load_x(clamp(cc + 1));
+            compute(sx[k & 1], wb[k]);
+            store_x(sx[(k + 1) & 1]);
+            __syncthreads();
+            if (cc >= last) {
+                done = true;
+                break;
+            }
+        }
+        if (done) break;
     }
+    if (A.S == 1) {
+        if (n < A.n_out) {
+#pragma unroll
+            for (int i = 0; i < kGemmMT; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int64_t m = m0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
+                    if (m < A.M) A.y[m * A.ldy + n] = y[i][r];
+                }
+        }
+        return;
+    }
+    // K slices: partial sums through agent-scope stores and loads (they
+    // write through and read past the per-XCD L2s; no cache write-back or
+    // invalidation is needed), each wave waiting for its stores before the
+    // workgroup counts its arrival; nothing waits on another workgroup.
+    const int64_t ldp = (int64_t)A.NB * kGemmBN;
     if (n < A.n_out) {
 #pragma unroll
         for (int i = 0; i < kGemmMT; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int64_t m = m0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-                if (m < A.M) A.y[m * A.ldy + n] = y[i][r];
+                if (m < A.M)
+                    __hip_atomic_store(A.part + ((int64_t)slice * A.Mp + m) * ldp + n, y[i][r],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
     }
+    __shared__ uint32_t last_flag;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    uint32_t *cnt = A.cnt + (int64_t)mblk * A.NB + nblk;
+    if (threadIdx.x == 0)
+        last_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)A.S - 1;
+    __syncthreads();
+    if (!last_flag) return;
+    // this thread's outputs: rows m0 + idx / BN, columns nblk * BN + idx % BN
+    // for idx = tid + 256 q; all loads of one slice are issued together
+    constexpr int kOut = kGemmBM * kGemmBN / kGemmThreads;
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        A.part, (short)0, (int)((int64_t)A.S * A.Mp * ldp * 4), 0x00020000);
+    const int64_t nn = (int64_t)nblk * kGemmBN + threadIdx.x % kGemmBN;
+    float v[kOut];
+#pragma unroll
+    for (int q = 0; q < kOut; q++) v[q] = 0.0f;
+    for (int sl = 0; sl < A.S; sl++) {
+        float pv[kOut];
+#pragma unroll
+        for (int q = 0; q < kOut; q++) {
+            const int64_t m = m0 + (threadIdx.x + kGemmThreads * q) / kGemmBN;
+            // rows past M were not written: read row 0's value, unused
+            pv[q] = load_agent_f32(pr, (uint32_t)((((int64_t)sl * A.Mp + (m < A.M ? m : 0)) * ldp + nn) * 4));
+        }
+#pragma unroll
+        for (int q = 0; q < kOut; q++) v[q] += pv[q];
+    }
+    if (nn < A.n_out) {
+#pragma unroll
+        for (int q = 0; q < kOut; q++) {
+            const int64_t m = m0 + (threadIdx.x + kGemmThreads * q) / kGemmBN;
+            if (m < A.M) A.y[m * A.ldy + nn] = v[q];
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace sihip

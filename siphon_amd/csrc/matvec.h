@@ -30,6 +30,7 @@
 //   F16:            sum f16(w)*f16(x) with f32 accumulation (v_dot2)
 #pragma once
 
+#include "agent.h"
 #include "formats.h"
 #include "quant.h"
 #include "unit.h"
@@ -296,14 +297,26 @@ __device__ inline void split_reduce(const MVSeg &sg, uint32_t grp, uint32_t ldp,
     __syncthreads();
     if (!*last) return;
     const uint32_t rows = kWaves * sg.R;
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        sg.part, (short)0, (int)(sg.split * NC * ldp * 4), 0x00020000);
     for (uint32_t i = threadIdx.x; i < rows * NC; i += kThreads) {
         const uint32_t c = i / rows;
         const int64_t row = (int64_t)grp * rows + (i - c * rows);
         if (row < (int64_t)sg.n_out) {
+            // slices in groups of 8 whose loads are issued together, added in
+            // slice order
             float v = 0.0f;
-            for (uint32_t p = 0; p < sg.split; p++)
-                v += __hip_atomic_load(sg.part + (int64_t)(p * NC + c) * ldp + row, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t p0 = 0; p0 < sg.split; p0 += 8) {
+                float pv[8];
+#pragma unroll
+                for (uint32_t k = 0; k < 8; k++) {
+                    const uint32_t p = p0 + k < sg.split ? p0 + k : sg.split - 1;
+                    pv[k] = load_agent_f32(pr, (uint32_t)(((int64_t)(p * NC + c) * ldp + row) * 4));
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < 8; k++)
+                    if (p0 + k < sg.split) v += pv[k];
+            }
             sg.y[c * sg.ldy + row] = v;
         }
     }

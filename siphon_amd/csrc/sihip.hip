@@ -36,7 +36,14 @@ struct sihip_ctx {
     size_t d_aux_cap = 0;
     void *d_ws = nullptr;  // prefill GEMM: quantized activation planes
     size_t d_ws_cap = 0;
+    void *d_gpart = nullptr;  // prefill GEMM K slices: partial sums
+    size_t d_gpart_cap = 0;
+    uint32_t *d_gcnt = nullptr;  // prefill GEMM K slices: arrival counters (zero between calls)
 };
+
+// Arrival counters of K-sliced GEMM tiles, allocated (and zeroed) on the
+// first sliced call; launches with more tiles than this are not sliced.
+constexpr int64_t kGemmCounters = 65536;
 
 struct sihip_weight {
     Layout L;
@@ -116,6 +123,8 @@ extern "C" void sihip_shutdown(sihip_ctx *ctx) {
     if (ctx->d_out) (void)hipFree(ctx->d_out);
     if (ctx->d_aux) (void)hipFree(ctx->d_aux);
     if (ctx->d_ws) (void)hipFree(ctx->d_ws);
+    if (ctx->d_gpart) (void)hipFree(ctx->d_gpart);
+    if (ctx->d_gcnt) (void)hipFree(ctx->d_gcnt);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -524,7 +533,12 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
         w->gemm = g;
         w->gemm_bytes = bytes;
     }
-    const int64_t Mp = (M + kGemmBM - 1) / kGemmBM * kGemmBM;
+    // small M: 32-row m tiles (twice the workgroups) with four super-blocks
+    // of weights in flight per wave; SIHIP_GEMM_MT (1 or 2) overrides
+    int mt = M <= 128 ? 1 : 2;
+    if (const char *e = getenv("SIHIP_GEMM_MT")) mt = atoi(e) == 1 ? 1 : 2;
+    const int64_t BM = 32 * mt;
+    const int64_t Mp = (M + BM - 1) / BM * BM;
     const int64_t ws = gemm_x_bytes(Mp, K);
     int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)ws);
     if (rc) return rc;
@@ -546,10 +560,54 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
     A.X = XP;
     A.y = Y;
     A.ldy = ldy;
-    A.MB = (int)(Mp / kGemmBM);
+    A.MB = (int)(Mp / BM);
     A.NB = NB;
-    const int64_t grid = (int64_t)8 * ((A.NB + 7) / 8) * A.MB;
-    hipLaunchKernelGGL(gemm_kq_kernel<T_Q4_K>, dim3((unsigned)grid), dim3(kGemmThreads), 0, st, A);
+    // K slices of SBK super-blocks when the output tiles alone would leave
+    // CUs idle (M <= 32 at the benchmark shapes: 112 tiles on 256 CUs):
+    // about one workgroup per CU, at least 4 super-blocks per slice. The
+    // partial sums cost a write and a read of S x M x N floats, which
+    // outweighs the extra parallelism once the tiles fill the chip
+    // (measured M = 64: 26.2 us unsliced, 32.3 us in 4 slices).
+    // SIHIP_GEMM_SBK overrides (0: no slices).
+    const int64_t tiles = (int64_t)A.MB * NB;
+    int64_t sbk = 0;
+    if (tiles < ctx->n_cu) {
+        int64_t S = (ctx->n_cu + tiles - 1) / tiles;
+        if (S > nb / 4) S = nb / 4;
+        if (S > 1) sbk = (nb + S - 1) / S;
+    }
+    if (const char *e = getenv("SIHIP_GEMM_SBK")) sbk = atol(e);
+    A.S = 1;
+    A.SBK = (int)nb;
+    A.part = nullptr;
+    A.cnt = nullptr;
+    if (sbk > 0 && sbk < nb && (int64_t)A.MB * NB <= kGemmCounters) {
+        const int S = (int)((nb + sbk - 1) / sbk);
+        rc = ensure(ctx, &ctx->d_gpart, &ctx->d_gpart_cap,
+                    (size_t)S * Mp * NB * kGemmBN * sizeof(float));
+        if (rc) return rc;
+        if (!ctx->d_gcnt) {
+            void *p = nullptr;
+            if (hipMalloc(&p, kGemmCounters * 4) != hipSuccess)
+                return set_err(ctx, SIHIP_ENOMEM, "gemm slice counters");
+            if (hipMemset(p, 0, kGemmCounters * 4) != hipSuccess) {
+                (void)hipFree(p);
+                return set_err(ctx, SIHIP_EDEVICE, "gemm slice counters: memset failed");
+            }
+            ctx->d_gcnt = (uint32_t *)p;
+        }
+        A.S = S;
+        A.SBK = (int)sbk;
+        A.part = (float *)ctx->d_gpart;
+        A.cnt = ctx->d_gcnt;
+    }
+    const int64_t grid = (int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S;
+    if (mt == 1)
+        hipLaunchKernelGGL((gemm_kq_kernel<T_Q4_K, 1, 4>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                           st, A);
+    else
+        hipLaunchKernelGGL((gemm_kq_kernel<T_Q4_K, 2, 2>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                           st, A);
     e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
     return SIHIP_OK;

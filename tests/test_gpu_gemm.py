@@ -77,3 +77,31 @@ def test_gemm_config3_sampled_rows(dev, oracle):
     ref, L1 = oracle.gemm(sa.Q4_K, W[rows], len(rows), n_in, X)
     assert_close(Y[:, rows].reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
                  "config 3 sampled rows")
+
+
+@pytest.mark.parametrize("mt,sbk", [(1, 1), (1, 3), (1, 4), (1, 0), (2, 3), (2, 0)])
+def test_gemm_k_slices(dev, oracle, monkeypatch, mt, sbk):
+    """K slices of the small-M GEMM (11 super-blocks: ragged last slice,
+    several m tiles, a ragged last n tile): every slicing and tile height
+    within tolerance of the oracle, and a repeated call gives the same bits
+    (the last slice of each tile resets its arrival counter)."""
+    monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1")
+    monkeypatch.setenv("SIHIP_GEMM_MT", str(mt))
+    monkeypatch.setenv("SIHIP_GEMM_SBK", str(sbk))
+    rng = np.random.default_rng(1100 + 10 * mt + sbk)
+    n_out, n_in, M = 333, 2816, 70
+    W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(sa.Q4_K, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+        Y2 = dev.gemm(w, X)
+        Y3 = dev.gemm(w, X[:5])
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
+    what = f"gemm MT={mt} SBK={sbk}"
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
+    assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
+    assert_close(Y3.reshape(-1), ref[:5].reshape(-1).astype(np.float64), L1[:5].reshape(-1),
+                 what + " M=5")
