@@ -112,17 +112,18 @@ struct XFirst {
 };
 
 // 16 lanes quantize one block: thread tid owns block (tid >> 4) + 16 p of
-// pass p, elements 16 * (tid & 15) .. +15 of it.
+// pass p (counted from block b0 of the row, nbl blocks staged), elements
+// 16 * (tid & 15) .. +15 of it.
 template <int XP>
-__device__ inline void stage_q8k_first(const MVArgs &a, XFirst<XP> &xf, int64_t b0, int64_t b1) {
+__device__ inline void stage_q8k_first(const MVArgs &a, XFirst<XP> &xf, int64_t b0, int64_t nbl) {
     const int tid = threadIdx.x;
     if (!a.x) return;
 #pragma unroll
     for (int p = 0; p < XP; p++) {
-        if (b0 + 16 * p < b1) {  // wave-uniform
-            int64_t b = b0 + (tid >> 4) + 16 * p;
-            b = b < b1 ? b : b1 - 1;  // clamped: the load stays in the range
-            const float4 *src = reinterpret_cast<const float4 *>(a.x + b * 256 + (tid & 15) * 16);
+        if (16 * p < nbl) {  // wave-uniform
+            int64_t b = (tid >> 4) + 16 * p;
+            b = b < nbl ? b : nbl - 1;  // clamped: the load stays in the range
+            const float4 *src = reinterpret_cast<const float4 *>(a.x + (b0 + b) * 256 + (tid & 15) * 16);
 #pragma unroll
             for (int i = 0; i < 4; i++) xf.t[p][i] = src[i];
         }
@@ -144,13 +145,14 @@ __device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int l
     if (lane16 == 0) reinterpret_cast<float *>(col + n)[b] = r.d;
 }
 
-// Stages pair blocks [b0, b1) of each column (32-element units for F16) at
-// their places in the full-row LDS image.
+// Stages pair blocks [b0, b0 + nbl) of each column (32-element units for
+// F16) as the LDS image of a row of n = nbl blocks' elements: a launch of
+// whole rows stages its row (b0 = 0), a column slice only its slice, so its
+// LDS holds a slice rather than a row.
 template <uint32_t PAIR, int XP>
 __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XFirst<XP> &xf,
-                                         int64_t b0, int64_t b1) {
+                                         int64_t b0, int64_t nbl, int64_t n) {
     const int tid = threadIdx.x;
-    const int64_t n = a.n_in;
     for (int c = 0; c < a.nc; c++) {
         uint8_t *col = lds + c * a.col_bytes;
         if constexpr (PAIR == T_Q8_K) {
@@ -158,16 +160,16 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             float *dcol = reinterpret_cast<float *>(col + n);
             int16_t *bcol = reinterpret_cast<int16_t *>(col + n + nb * 4);
             if (a.x) {
-                const float *xc = a.x + c * a.ldx;
+                const float *xc = a.x + c * a.ldx + b0 * 256;
                 const int lane16 = tid & 15;
-                int64_t bt = b0 + (tid >> 4);
+                int64_t bt = tid >> 4;
                 if (c == 0) {  // the passes loaded up front
 #pragma unroll
                     for (int p = 0; p < XP; p++)
-                        if (bt + 16 * p < b1) q8k_stage_block(col, n, bt + 16 * p, lane16, xf.t[p]);
+                        if (bt + 16 * p < nbl) q8k_stage_block(col, n, bt + 16 * p, lane16, xf.t[p]);
                     bt += 16 * XP;
                 }
-                for (int64_t b = bt; b < b1; b += kThreads / 16) {
+                for (int64_t b = bt; b < nbl; b += kThreads / 16) {
                     const float4 *src = reinterpret_cast<const float4 *>(xc + b * 256 + lane16 * 16);
                     float4 t4[4];
 #pragma unroll
@@ -175,9 +177,9 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
                     q8k_stage_block(col, n, b, lane16, t4);
                 }
             } else {
-                const uint8_t *src = a.xq + c * a.ldxq;
-                for (int64_t i = tid; i < (b1 - b0) * 73; i += kThreads) {
-                    const int64_t b = b0 + i / 73, w = i % 73;  // 73 dwords per 292-byte block
+                const uint8_t *src = a.xq + c * a.ldxq + b0 * 292;
+                for (int64_t i = tid; i < nbl * 73; i += kThreads) {
+                    const int64_t b = i / 73, w = i % 73;  // 73 dwords per 292-byte block
                     const uint32_t v = reinterpret_cast<const uint32_t *>(src + b * 292)[w];
                     if (w == 0) dcol[b] = __uint_as_float(v);
                     else if (w < 65)
@@ -191,17 +193,17 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             const int64_t nb = n / 32;
             float *dcol = reinterpret_cast<float *>(col + n);
             int *scol = reinterpret_cast<int *>(col + n + nb * 4);
-            for (int64_t b = b0 + tid; b < b1; b += kThreads) {
+            for (int64_t b = tid; b < nbl; b += kThreads) {
                 uint32_t q[8];
                 float d;
                 int sum;
                 if (a.x) {
-                    const Q80Block r = q80_block(a.x + c * a.ldx + b * 32);
+                    const Q80Block r = q80_block(a.x + c * a.ldx + (b0 + b) * 32);
                     for (int t = 0; t < 8; t++) q[t] = r.q[t];
                     d = r.d;
                     sum = r.sum;
                 } else {
-                    const uint8_t *src = a.xq + c * a.ldxq + b * 34;
+                    const uint8_t *src = a.xq + c * a.ldxq + (b0 + b) * 34;
                     d = f16_bits_to_f32((uint32_t)src[0] | ((uint32_t)src[1] << 8));
                     sum = 0;
                     for (int t = 0; t < 8; t++) {
@@ -223,12 +225,12 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
         } else {  // F16
             uint16_t *h = reinterpret_cast<uint16_t *>(col);
             if (a.x) {
-                const float *xc = a.x + c * a.ldx;
-                for (int64_t i = b0 * 32 + tid; i < b1 * 32; i += kThreads)
+                const float *xc = a.x + c * a.ldx + b0 * 32;
+                for (int64_t i = tid; i < nbl * 32; i += kThreads)
                     h[i] = __builtin_bit_cast(uint16_t, (_Float16)xc[i]);
             } else {
-                const uint16_t *src = reinterpret_cast<const uint16_t *>(a.xq + c * a.ldxq);
-                for (int64_t i = b0 * 32 + tid; i < b1 * 32; i += kThreads) h[i] = src[i];
+                const uint16_t *src = reinterpret_cast<const uint16_t *>(a.xq + c * a.ldxq) + b0 * 32;
+                for (int64_t i = tid; i < nbl * 32; i += kThreads) h[i] = src[i];
             }
         }
     }
@@ -367,6 +369,14 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     const uint32_t nwaves = split ? ntiles : sg.nwg * kWaves;  // split: one tile per wave
     const uint32_t my_tiles = wave0 < ntiles ? (ntiles - 1 - wave0) / nwaves + 1 : 0;
     const uint32_t total = my_tiles * (s_end - s_begin);  // rounds of this wave
+    // activation blocks of the columns this workgroup's rounds read; a
+    // slice's LDS image is a row of its own (n_loc elements, columns from
+    // cbase)
+    const int64_t b0 = (int64_t)s_begin * G;
+    const int64_t b1 = (int64_t)s_end * G < sg.ncols ? (int64_t)s_end * G : (int64_t)sg.ncols;
+    constexpr uint32_t kColElems = KQ ? 256u : 32u;
+    const uint32_t n_loc = SPLIT ? (uint32_t)(b1 - b0) * kColElems : n_in;
+    const uint32_t cbase = SPLIT ? (uint32_t)b0 : 0u;
 
     // finished rows go to y, or (sliced) to this slice's partial sums, rows
     // of the last tile included; agent-scope stores, which partial sums need
@@ -421,9 +431,9 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
 #pragma unroll
                 for (int c = 0; c < NC; c++) keep[c] = acc[c];
                 if constexpr (KQ)
-                    compute_kblock<FMT, NC>(lds, col_bytes, n_in, col, b.k, acc);
+                    compute_kblock<FMT, NC>(lds, col_bytes, n_loc, col - cbase, b.k, acc);
                 else
-                    compute_unit<FMT, NC>(lds, col_bytes, n_in, col, b.u[i], acc);
+                    compute_unit<FMT, NC>(lds, col_bytes, n_loc, col - cbase, b.u[i], acc);
 #pragma unroll
                 for (int c = 0; c < NC; c++) acc[c] = pad ? keep[c] : acc[c];
                 if (c_it.s == s_end - 1) {
@@ -443,14 +453,11 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
         }
     };
 
-    // activation blocks of the columns this workgroup's rounds read
-    const int64_t b0 = (int64_t)s_begin * G;
-    const int64_t b1 = (int64_t)s_end * G < sg.ncols ? (int64_t)s_end * G : (int64_t)sg.ncols;
     Buf<FMT> bufA, bufB;
     XFirst<XP> xf;
-    if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf, b0, b1);
+    if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf, b0, b1 - b0);
     issue(bufA);
-    stage_activations<PAIR, XP>(A, lds, xf, b0, b1);
+    stage_activations<PAIR, XP>(A, lds, xf, b0, b1 - b0, n_loc);
     if (total == 1) {  // one round: no second buffer (it would reload the same round)
         __syncthreads();
         consume(bufA);

@@ -409,7 +409,17 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         if (t < f0) f0 = t;
         if (t > f1) f1 = t;
     }
-    int ncmax = max_cols(ctx, pair, n_in);
+    // LDS per activation column: a whole row, or for a sliced matrix one
+    // slice (its workgroups stage only their slice)
+    int64_t n_lds = 0;
+    for (int i = 0; i < count; i++) {
+        const Layout &L = w[i]->L;
+        const int64_t need = w[i]->split > 1
+                                 ? (int64_t)w[i]->spr * L.G * (is_kquant(L.type) ? 256 : 32)
+                                 : n_in;
+        n_lds = need > n_lds ? need : n_lds;
+    }
+    int ncmax = max_cols(ctx, pair, n_lds);
     if (ncmax == 0)
         return set_err(ctx, SIHIP_ERANGE, "activation row of %lld does not fit in LDS",
                        (long long)n_in);
@@ -418,7 +428,7 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         if (M != 1) return set_err(ctx, SIHIP_EINVAL, "a launch of several matrices takes one column");
         ncmax = 1;
     }
-    const int64_t cb = col_bytes_aligned(pair, n_in);
+    const int64_t cb = col_bytes_aligned(pair, n_lds);
     // workgroups: one row tile per wave when the chip has room; otherwise
     // each matrix gets a share of the cap proportional to its bytes
     const int64_t wg_cap = (int64_t)ctx->n_cu * wgs_per_cu();
