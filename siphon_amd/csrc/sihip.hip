@@ -135,10 +135,16 @@ extern "C" const char *sihip_last_error(const sihip_ctx *ctx) {
 
 // ---- weights ------------------------------------------------------------------
 
+// Workgroup cap per CU for matvec launches with more row tiles than waves:
+// two, the number resident at once for the heavier kernels, so the whole
+// grid is one generation of long-lived workgroups (each walks several
+// tiles) instead of several generations that each repeat the prologue
+// (measured 2-4% faster than 4 or 8 on heads and 27648-row matrices).
+// SIHIP_WG_PER_CU overrides.
 static int wgs_per_cu() {
     const char *e = getenv("SIHIP_WG_PER_CU");
     const int v = e ? atoi(e) : 0;
-    return v > 0 ? v : 8;
+    return v > 0 ? v : 2;
 }
 
 static int wave_target() {
