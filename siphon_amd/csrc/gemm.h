@@ -130,7 +130,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_quantize_x(const float *x, 
 // the block record.
 struct GemmW {
     uint2 u[8];
-    U4 m;
+    uint4 scb;   // sh_0..sh_7 (x, y), sl_0..sl_7 (z, w): one byte per unit
+    float2 dd;   // d, dmin
+    v8h_t bm;    // mins of units 4h..4h+3 (this lane's half), each twice
 };
 
 // ---- GEMM weight order ---------------------------------------------------------
@@ -139,14 +141,22 @@ struct GemmW {
 // 32 rows one GEMM wave needs for a super-block are spread over many cache
 // lines. Prefill uses a second copy in GEMM order, built on device from the
 // matvec planes on first use: for each block of 32 rows and super-block c,
-// 4608 contiguous bytes
+// 5888 contiguous bytes
 //   4 x 1024 B: for q = 0..3 and lane L = 32 h + r (r = row in the block),
 //               bytes 16 L .. 16 L + 7 = half h of unit 2q of row r,
 //               bytes 16 L + 8 .. 16 L + 15 = half h of unit 2q + 1 of row r
-//   512 B:      block records (d | dmin | scales) of rows 0..31
-// so a wave loads its operands for a super-block with 5 coalesced 16-byte
-// loads per lane, each half already where the MFMA B operand wants it.
-constexpr int kGemmChunk = 4608;
+//   512 B:      per row, the unit scales sc_j = 8 sh_j + sl_j split in
+//               bytes: sh_0..sh_7, then sl_0..sl_7
+//   256 B:      per row, f32 d and dmin
+//   1024 B:     per lane L, f16 mins of units 4h..4h+3 of row r, each twice
+//               (the B operand of the min MFMA)
+// so a wave loads a super-block with 8 coalesced loads per lane, each unit
+// half already where the MFMA B operand wants it and no scale decoding left
+// in the loop.
+constexpr int kGemmScOff = 4096;
+constexpr int kGemmDOff = kGemmScOff + 512;
+constexpr int kGemmMinOff = kGemmDOff + 256;
+constexpr int kGemmChunk = kGemmMinOff + 1024;
 
 __host__ __device__ inline int64_t gemm_layout_bytes(int64_t nblk32, int64_t nb) {
     return nblk32 * nb * kGemmChunk;
@@ -158,13 +168,14 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
                                                           uint8_t *out, int64_t nblk32) {
     const int64_t nb = L.n_in / 256;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t per = kGemmChunk / 16;  // 288 slots per chunk
+    const int64_t per = kGemmChunk / 16;  // 368 slots per chunk
     if (i >= nblk32 * nb * per) return;
-    const int64_t chunk = i / per, slot = i % per;
+    const int64_t chunk = i / per;
+    const int slot = (int)(i % per);
     const int64_t blk = chunk / nb, c = chunk % nb;
     uint32_t v[4] = {0, 0, 0, 0};
-    if (slot < 256) {  // unit halves
-        const int q = (int)(slot >> 6), lane = (int)(slot & 63), h = lane >> 5, r = lane & 31;
+    if (slot < kGemmScOff / 16) {  // unit halves
+        const int q = slot >> 6, lane = slot & 63, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out) {
             for (int k = 0; k < 2; k++) {
@@ -173,11 +184,38 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
                 v[2 * k + 1] = ldp<uint32_t>(src + 4);
             }
         }
-    } else {  // block records
-        const int64_t row = blk * 32 + (slot - 256);
+    } else if (slot < kGemmDOff / 16) {  // scale bytes of one row
+        const int64_t row = blk * 32 + (slot - kGemmScOff / 16);
         if (row < L.n_out) {
-            const uint8_t *src = planes + block_off(L, 1, row, c * 8);
-            for (int k = 0; k < 4; k++) v[k] = ldp<uint32_t>(src + 4 * k);
+            const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
+            for (int j = 0; j < 8; j++) {
+                int sc, mn;
+                k4_scale_min(m, j, sc, mn);
+                v[j >> 2] |= (uint32_t)(sc >> 3) << (8 * (j & 3));
+                v[2 + (j >> 2)] |= (uint32_t)(sc & 7) << (8 * (j & 3));
+            }
+        }
+    } else if (slot < kGemmMinOff / 16) {  // d, dmin of rows 2k, 2k + 1
+        const int k = slot - kGemmDOff / 16;
+        for (int t = 0; t < 2; t++) {
+            const int64_t row = blk * 32 + 2 * k + t;
+            if (row < L.n_out) {
+                const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
+                v[2 * t] = __float_as_uint(half_to_float(m.x & 0xffffu));
+                v[2 * t + 1] = __float_as_uint(half_to_float(m.x >> 16));
+            }
+        }
+    } else {  // mins of lane L
+        const int lane = slot - kGemmMinOff / 16, h = lane >> 5, r = lane & 31;
+        const int64_t row = blk * 32 + r;
+        if (row < L.n_out) {
+            const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
+            for (int t = 0; t < 4; t++) {
+                int sc, mn;
+                k4_scale_min(m, 4 * h + t, sc, mn);
+                const uint32_t hb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mn);
+                v[t] = hb | (hb << 16);
+            }
         }
     }
     *reinterpret_cast<uint4 *>(out + i * 16) = make_uint4(v[0], v[1], v[2], v[3]);
@@ -193,14 +231,24 @@ __device__ inline void gemm_load_w(const uint8_t *blk_base, int64_t c, int lane,
         w.u[2 * q] = make_uint2(v.x, v.y);
         w.u[2 * q + 1] = make_uint2(v.z, v.w);
     }
-    w.m = *reinterpret_cast<const U4 *>(chunk + 4096 + 16 * (lane & 31));
+    w.scb = *reinterpret_cast<const uint4 *>(chunk + kGemmScOff + 16 * (lane & 31));
+    w.dd = *reinterpret_cast<const float2 *>(chunk + kGemmDOff + 8 * (lane & 31));
+    w.bm = *reinterpret_cast<const v8h_t *>(chunk + kGemmMinOff + 16 * lane);
 }
 
-__device__ inline uint32_t bytes_times(uint32_t q, uint32_t f) {
-    // bytewise q * f for bytes and products below 256 (no carries between bytes)
+// Bytewise q * f for bytes and products below 256 (no carries between
+// bytes); f2 holds the factor in both 16-bit halves.
+__device__ inline uint32_t bytes_times(uint32_t q, uint32_t f2) {
     const u16x2_t a = __builtin_bit_cast(u16x2_t, q);
-    const u16x2_t b = {(unsigned short)f, (unsigned short)f};
+    const u16x2_t b = __builtin_bit_cast(u16x2_t, f2);
     return __builtin_bit_cast(uint32_t, (u16x2_t)(a * b));
+}
+
+// Byte j (0..7) of the 8 bytes lo:hi in both 16-bit halves (v_perm_b32;
+// selector 0x0c gives a zero byte).
+__device__ inline uint32_t byte_pair(uint32_t lo, uint32_t hi, int j) {
+    const uint32_t sel = (uint32_t)j | (0x0cu << 8) | ((uint32_t)j << 16) | (0x0cu << 24);
+    return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
 // MT: 32-row MFMA tiles per wave along m (2 for large M; 1 for small M,
@@ -242,11 +290,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
 
     // one super-block: weights w (this lane's row), activation tile in buf
     auto compute = [&](const uint8_t *buf, const GemmW &w) {
-        int sc[8], mn[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) k4_scale_min(w.m, j, sc[j], mn[j]);
-        const float d = half_to_float(w.m.x & 0xffffu);
-        const float dmin = half_to_float(w.m.x >> 16);
+        const float d = w.dd.x, dmin = w.dd.y;
         v16i_t acc_h[kGemmMT], acc_l[kGemmMT];
 #pragma unroll
         for (int i = 0; i < kGemmMT; i++)
@@ -278,7 +322,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
             const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
             const uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
             const uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
-            const uint32_t sh = (uint32_t)sc[j] >> 3, sl = (uint32_t)sc[j] & 7u;
+            const uint32_t sh = byte_pair(w.scb.x, w.scb.y, j), sl = byte_pair(w.scb.z, w.scb.w, j);
             const v4i_t bh = {(int)bytes_times(q0, sh), (int)bytes_times(q1, sh),
                               (int)bytes_times(q2, sh), (int)bytes_times(q3, sh)};
             const v4i_t bl = {(int)bytes_times(q0, sl), (int)bytes_times(q1, sl),
@@ -291,17 +335,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
         }
         __builtin_amdgcn_s_setprio(0);
         // mins against the group sums: slot s of half h is group 8h + s
-        v8h_t bm;
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            // min of unit 4h + s (reference kernels.c:648-656), selected
-            // arithmetically so no private array is indexed by the lane half
-            const int lo = (int)((w.m.z >> (8 * s)) & 63u);
-            const int hi = (int)(((w.m.w >> (8 * s + 4)) & 15u) | (((w.m.z >> (8 * s + 6)) & 3u) << 4));
-            const _Float16 v = (_Float16)(float)(h ? hi : lo);
-            bm[2 * s] = v;
-            bm[2 * s + 1] = v;
-        }
+        const v8h_t bm = w.bm;
         const float *dx = reinterpret_cast<const float *>(buf + kXDOff);
 #pragma unroll
         for (int i = 0; i < kGemmMT; i++) {
