@@ -104,6 +104,12 @@ int sihip_gemv(sihip_ctx *ctx, const sihip_weight *w, const float *x,
  * batched equivalent, with X quantized per row. */
 int sihip_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X,
                int64_t M, float *Y);
+/* Weight values of one row, out[0..n_in): the si_backend row_to_f32 slot
+ * (reference backend.c:122-131, which calls si_dequant_row_* of
+ * kernels.c:599-817), from the device copy, bit-identical to the reference
+ * dequantizer. */
+int sihip_dequant_row(sihip_ctx *ctx, const sihip_weight *w, uint64_t row,
+                      float *out);
 
 /* ---- device pointers, stream-ordered (no host synchronisation) -------
  * x, y, X, Y point to device memory; stream is a hipStream_t (NULL for
@@ -112,6 +118,12 @@ int sihip_gemv_dev(sihip_ctx *ctx, const sihip_weight *w, const float *x,
                    float *y, int64_t n_out, void *stream);
 int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float *X,
                    int64_t M, float *Y, void *stream);
+/* Rows [row0, row0 + nrows) dequantized as sihip_dequant_row, row r at
+ * out + (r - row0) * ldo (out 16-byte aligned, ldo >= n_in, a multiple of
+ * 4): an embedding lookup for a host that keeps activations on the device. */
+int sihip_dequant_rows_dev(sihip_ctx *ctx, const sihip_weight *w,
+                           uint64_t row0, uint64_t nrows, float *out,
+                           int64_t ldo, void *stream);
 /* Several matrices that share one input x (q/k/v at reference
  * engine.c:317-319, gate/up at 375-376) in one launch: y[i] receives
  * gemv(w[i], x). All w[i] must have the same n_in; at most 4. */

@@ -71,6 +71,8 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_gemv.argtypes = [_vp, _vp, _vp, _vp, _i64]
     L.sihip_gemm.argtypes = [_vp, _vp, _vp, _i64, _vp]
     L.sihip_gemv_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
+    L.sihip_dequant_row.argtypes = [_vp, _vp, _u64, _vp]
+    L.sihip_dequant_rows_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _i64, _vp]
     L.sihip_gemm_dev.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
     L.sihip_gemv_multi_dev.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(_vp), _vp,
                                        ctypes.POINTER(_vp), _vp]
@@ -173,6 +175,16 @@ class Device:
     # device-pointer variants (pointers as ints, stream as int or None)
     def gemv_dev(self, w: Weight, x_ptr: int, y_ptr: int, n_out: int, stream: int | None = None):
         self._check(self.L.sihip_gemv_dev(self.ctx, w.handle, x_ptr, y_ptr, n_out, stream))
+
+    def dequant_row(self, w: Weight, row: int) -> np.ndarray:
+        out = np.zeros(w.n_in, dtype=np.float32)
+        self._check(self.L.sihip_dequant_row(self.ctx, w.handle, row, _ptr(out)))
+        return out
+
+    def dequant_rows_dev(self, w: Weight, row0: int, nrows: int, out_ptr: int, ldo: int,
+                         stream: int | None = None):
+        self._check(self.L.sihip_dequant_rows_dev(self.ctx, w.handle, row0, nrows, out_ptr, ldo,
+                                                  stream))
 
     def gemm_dev(self, w: Weight, X_ptr: int, M: int, Y_ptr: int, stream: int | None = None):
         self._check(self.L.sihip_gemm_dev(self.ctx, w.handle, X_ptr, M, Y_ptr, stream))

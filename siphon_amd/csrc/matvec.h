@@ -566,6 +566,44 @@ __global__ __launch_bounds__(kThreads) void convert_f16_kernel(const float *x, u
     if (i < n) out[i] = __builtin_bit_cast(uint16_t, (_Float16)x[i]);
 }
 
+// ---- dequantized rows (reference row_to_f32, backend.c:122-131) -------------
+
+// Rows [row0, row0 + nrows) of the matrix into out (row r - row0 at
+// out + (r - row0) * ldo): one thread per (row, column), the column's units
+// decoded as the dot products decode them (unit.h dequant_*).
+template <uint32_t FMT>
+__global__ __launch_bounds__(kThreads) void dequant_rows_kernel(Layout L, const uint8_t *w,
+                                                                int64_t row0, int64_t nrows,
+                                                                float *out, int64_t ldo) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nrows * L.ncols) return;
+    const int64_t rr = i / L.ncols, c = i % L.ncols;
+    Planes P;
+#pragma unroll
+    for (int p = 0; p < 4; p++) P.p[p] = w + L.plane_off[p];
+    const uint32_t cr = (uint32_t)col_rec(L, row0 + rr, c);
+    float *o = out + rr * ldo;
+    float v[32];
+    if constexpr (is_kquant(FMT)) {
+        KRaw raw;
+        load_kblock<FMT>(P, (cr >> 6) * 512u + (cr & 63u), cr, raw);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            dequant_kunit<FMT>(raw, k, v);
+            float4 *dst = reinterpret_cast<float4 *>(o + c * 256 + 32 * k);
+#pragma unroll
+            for (int q = 0; q < 8; q++) dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        }
+    } else {
+        Raw raw;
+        load_unit<FMT>(P, cr, raw);
+        dequant_unit<FMT>(raw, v);
+        float4 *dst = reinterpret_cast<float4 *>(o + c * 32);
+#pragma unroll
+        for (int q = 0; q < 8; q++) dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+}
+
 // ---- repack: GGUF blocks -> planes ------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void repack_kernel(Layout L, const uint8_t *src,

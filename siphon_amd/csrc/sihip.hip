@@ -639,6 +639,61 @@ static int run_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64
     return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out, st);
 }
 
+// ---- dequantized rows --------------------------------------------------------------
+
+static hipError_t launch_dequant(const Layout &L, const uint8_t *w, int64_t row0, int64_t nrows,
+                                 float *out, int64_t ldo, hipStream_t st) {
+    const dim3 grid((unsigned)((nrows * L.ncols + kThreads - 1) / kThreads)), block(kThreads);
+    switch (L.type) {
+        case T_F16: hipLaunchKernelGGL(dequant_rows_kernel<T_F16>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q4_0: hipLaunchKernelGGL(dequant_rows_kernel<T_Q4_0>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q5_0: hipLaunchKernelGGL(dequant_rows_kernel<T_Q5_0>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q8_0: hipLaunchKernelGGL(dequant_rows_kernel<T_Q8_0>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q2_K: hipLaunchKernelGGL(dequant_rows_kernel<T_Q2_K>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q3_K: hipLaunchKernelGGL(dequant_rows_kernel<T_Q3_K>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q4_K: hipLaunchKernelGGL(dequant_rows_kernel<T_Q4_K>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q5_K: hipLaunchKernelGGL(dequant_rows_kernel<T_Q5_K>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        case T_Q6_K: hipLaunchKernelGGL(dequant_rows_kernel<T_Q6_K>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+extern "C" int sihip_dequant_rows_dev(sihip_ctx *ctx, const sihip_weight *w, uint64_t row0,
+                                      uint64_t nrows, float *out, int64_t ldo, void *stream) {
+    if (!ctx || !w || !out) return set_err(ctx, SIHIP_EINVAL, "dequant_rows_dev: NULL argument");
+    if (nrows == 0 || row0 >= (uint64_t)w->L.n_out || nrows > (uint64_t)w->L.n_out - row0)
+        return set_err(ctx, SIHIP_EINVAL, "dequant_rows_dev: rows %llu..%llu outside 0..%lld",
+                       (unsigned long long)row0, (unsigned long long)(row0 + nrows),
+                       (long long)w->L.n_out);
+    if (ldo < w->L.n_in || ldo % 4 != 0 || !aligned16(out))
+        return set_err(ctx, SIHIP_EINVAL,
+                       "dequant_rows_dev: out must be 16-byte aligned with a row stride of at "
+                       "least n_in, a multiple of 4");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const hipError_t e =
+        launch_dequant(w->L, w->dev, (int64_t)row0, (int64_t)nrows, out, ldo, (hipStream_t)stream);
+    if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "dequant launch: %s", hipGetErrorString(e));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_dequant_row(sihip_ctx *ctx, const sihip_weight *w, uint64_t row, float *out) {
+    if (!ctx || !w || !out) return set_err(ctx, SIHIP_EINVAL, "dequant_row: NULL argument");
+    if (row >= (uint64_t)w->L.n_out)
+        return set_err(ctx, SIHIP_EINVAL, "dequant_row: row %llu outside 0..%lld",
+                       (unsigned long long)row, (long long)w->L.n_out - 1);
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const size_t ob = (size_t)w->L.n_in * 4;
+    const int rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, ob);
+    if (rc) return rc;
+    const hipError_t e = launch_dequant(w->L, w->dev, (int64_t)row, 1, (float *)ctx->d_out,
+                                        w->L.n_in, ctx->stream);
+    if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "dequant launch: %s", hipGetErrorString(e));
+    HIP_OK(ctx, hipMemcpyAsync(out, ctx->d_out, ob, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
 extern "C" int sihip_gemv_dev(sihip_ctx *ctx, const sihip_weight *w, const float *x, float *y,
                               int64_t n_out, void *stream) {
     if (!ctx || !w || !x || !y) return set_err(ctx, SIHIP_EINVAL, "gemv_dev: NULL argument");

@@ -422,4 +422,92 @@ SIHD inline int reduce_partner(int lane, int k) {
     }
 }
 
+// ---- dequantization (reference kernels.c:599-817, float semantics) ----------
+//
+// Weight values of one unit, as the reference dequantizer computes them:
+//   Q4_0/Q5_0/Q8_0: (float)q * d                      (q signed: u - 8, u - 16)
+//   Q2_K/Q4_K/Q5_K: (d * (float)s) * (float)q - dmin * (float)m
+//   Q3_K/Q6_K:      (d * (float)s) * (float)q         (q signed: u - 4, u - 32)
+// with s, m the scale and min of the element's 16-group (Q4_K/Q5_K: of the
+// unit), each product rounded to f32 (no contraction). The quants come from
+// the same decode as the dot products.
+
+// Unit k of the super-block w into out[0..31].
+template <uint32_t FMT>
+SIHD inline void dequant_kunit(const KRaw &w, int k, float out[32]) {
+    uint32_t q[8];
+    int s0, s1, m0 = 0, m1 = 0, bias = 0;
+    float d, dmin = 0.0f;
+    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+        nib_split(w.a[k], q);
+        if constexpr (FMT == T_Q5_K) add_bit4(q, w.c[k], 4);
+        k4_scale_min(w.m, k, s0, m0);
+        s1 = s0;
+        m1 = m0;
+        d = half_to_float(w.m.x & 0xffffu);
+        dmin = half_to_float(w.m.x >> 16);
+    } else if constexpr (FMT == T_Q6_K) {
+        nib_split(w.a[k], q);
+        two8_split(w.b[k].x, w.b[k].y, q, 4, true);
+        const uint32_t sw = u4_word(w.m, k >> 1);
+        s0 = sbfe8(sw, 16 * (k & 1));
+        s1 = sbfe8(sw, 16 * (k & 1) + 8);
+        d = half_to_float(w.e & 0xffffu);
+        bias = 32;
+    } else if constexpr (FMT == T_Q3_K) {
+        two8_split(w.b[k].x, w.b[k].y, q, 0, false);
+        add_bit4(q, w.c[k], 2);
+        s0 = k3_scale(w.m, 2 * k);
+        s1 = k3_scale(w.m, 2 * k + 1);
+        d = half_to_float(w.e & 0xffffu);
+        bias = 4;
+    } else {  // Q2_K
+        two8_split(w.b[k].x, w.b[k].y, q, 0, false);
+        const uint32_t sw = u4_word(w.m, k >> 1) >> (16 * (k & 1));
+        s0 = (int)(sw & 15u);
+        m0 = (int)((sw >> 4) & 15u);
+        s1 = (int)((sw >> 8) & 15u);
+        m1 = (int)((sw >> 12) & 15u);
+        d = half_to_float(w.e & 0xffffu);
+        dmin = half_to_float(w.e >> 16);
+    }
+    for (int e = 0; e < 32; e++) {
+        const int u = (int)((q[e >> 2] >> (8 * (e & 3))) & 0xffu) - bias;
+        const float dl = d * (float)(e < 16 ? s0 : s1);
+        if constexpr (FMT == T_Q3_K || FMT == T_Q6_K) {
+            out[e] = dl * (float)u;
+        } else {
+            const float ml = dmin * (float)(e < 16 ? m0 : m1);
+            out[e] = dl * (float)u - ml;
+        }
+    }
+}
+
+// The 32-element unit w into out[0..31].
+template <uint32_t FMT>
+SIHD inline void dequant_unit(const Raw &w, float out[32]) {
+    if constexpr (FMT == T_F16) {
+        const uint32_t v[16] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w,
+                                w.c.x, w.c.y, w.c.z, w.c.w, w.d.x, w.d.y, w.d.z, w.d.w};
+        for (int e = 0; e < 32; e++) out[e] = half_to_float((v[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+    } else {
+        uint32_t q[8];
+        int bias = 0;
+        if constexpr (FMT == T_Q8_0) {
+            q[0] = w.a.x; q[1] = w.a.y; q[2] = w.a.z; q[3] = w.a.w;
+            q[4] = w.b.x; q[5] = w.b.y; q[6] = w.b.z; q[7] = w.b.w;
+        } else {
+            nib_split(w.a, q);
+            if constexpr (FMT == T_Q5_0) add_bit4(q, w.f, 4);
+            bias = FMT == T_Q4_0 ? 8 : 16;
+        }
+        const float d = half_to_float(w.e & 0xffffu);
+        for (int e = 0; e < 32; e++) {
+            const uint32_t byte = (q[e >> 2] >> (8 * (e & 3))) & 0xffu;
+            const int v = FMT == T_Q8_0 ? (int)(int8_t)byte : (int)byte - bias;
+            out[e] = (float)v * d;
+        }
+    }
+}
+
 }  // namespace sihip

@@ -160,4 +160,52 @@ int emu_gemv_pair(uint32_t type, int64_t n_out, int64_t n_in, int G, int64_t sli
     return 0;
 }
 
+// Dequantize every row of a repacked matrix through the planar layout (the
+// device kernel's indexing): out[row * n_in + i].
+int emu_dequant(uint32_t type, int64_t n_out, int64_t n_in, int G, const uint8_t *rows, float *out) {
+    Layout L;
+    if (!make_layout(type, n_out, n_in, G, &L)) return -1;
+    std::vector<uint8_t> dev((size_t)L.total_bytes);
+    if (emu_repack(type, n_out, n_in, G, rows, dev.data())) return -1;
+    Planes P;
+    for (int p = 0; p < 4; p++) P.p[p] = dev.data() + L.plane_off[p];
+    for (int64_t row = 0; row < n_out; row++) {
+        for (int64_t c = 0; c < L.ncols; c++) {
+            const uint32_t cr = (uint32_t)col_rec(L, row, c);
+            float *o = out + row * n_in;
+            if (is_kquant(type)) {
+                KRaw w;
+                const uint32_t urec = (cr >> 6) * 512u + (cr & 63u);
+                switch (type) {
+                    case T_Q2_K: load_kblock<T_Q2_K>(P, urec, cr, w); break;
+                    case T_Q3_K: load_kblock<T_Q3_K>(P, urec, cr, w); break;
+                    case T_Q4_K: load_kblock<T_Q4_K>(P, urec, cr, w); break;
+                    case T_Q5_K: load_kblock<T_Q5_K>(P, urec, cr, w); break;
+                    default: load_kblock<T_Q6_K>(P, urec, cr, w); break;
+                }
+                for (int k = 0; k < 8; k++) {
+                    float *u = o + c * 256 + 32 * k;
+                    switch (type) {
+                        case T_Q2_K: dequant_kunit<T_Q2_K>(w, k, u); break;
+                        case T_Q3_K: dequant_kunit<T_Q3_K>(w, k, u); break;
+                        case T_Q4_K: dequant_kunit<T_Q4_K>(w, k, u); break;
+                        case T_Q5_K: dequant_kunit<T_Q5_K>(w, k, u); break;
+                        default: dequant_kunit<T_Q6_K>(w, k, u); break;
+                    }
+                }
+            } else {
+                Raw w;
+                float *u = o + c * 32;
+                switch (type) {
+                    case T_Q4_0: load_unit<T_Q4_0>(P, cr, w); dequant_unit<T_Q4_0>(w, u); break;
+                    case T_Q5_0: load_unit<T_Q5_0>(P, cr, w); dequant_unit<T_Q5_0>(w, u); break;
+                    case T_Q8_0: load_unit<T_Q8_0>(P, cr, w); dequant_unit<T_Q8_0>(w, u); break;
+                    default: load_unit<T_F16>(P, cr, w); dequant_unit<T_F16>(w, u); break;
+                }
+            }
+        }
+    }
+    return 0;
+}
+
 }  // extern "C"

@@ -20,6 +20,8 @@ class Emulator:
         L.emu_layout_bytes.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
         L.emu_layout_bytes.restype = ctypes.c_int64
         L.emu_repack.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, vp, vp]
+        L.emu_dequant.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                  vp, vp]
         self.L = L
 
     def gemv_pair(self, wtype, n_out, n_in, G, rows, xq, slice_elems=None):
@@ -41,4 +43,11 @@ class Emulator:
         out = np.zeros(nb, dtype=np.uint8)
         rows = np.ascontiguousarray(rows, dtype=np.uint8)
         assert self.L.emu_repack(wtype, n_out, n_in, G, rows.ctypes.data, out.ctypes.data) == 0
+        return out
+
+    def dequant(self, wtype, n_out, n_in, G, rows):
+        """Every row's weight values through the planar layout."""
+        rows = np.ascontiguousarray(rows, dtype=np.uint8)
+        out = np.zeros((n_out, n_in), dtype=np.float32)
+        assert self.L.emu_dequant(wtype, n_out, n_in, G, rows.ctypes.data, out.ctypes.data) == 0
         return out

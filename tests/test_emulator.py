@@ -65,3 +65,17 @@ def test_repack_is_a_permutation(emu):
         W = np.full((n_out, n_in // be * bb), 0xFF, np.uint8)
         dev = emu.repack(wt, n_out, n_in, 4, W)
         assert int(np.unpackbits(dev).sum()) == int(np.unpackbits(W).sum()), siq.NAMES[wt]
+
+
+@pytest.mark.parametrize("wt", siq.WEIGHT_TYPES, ids=lambda t: siq.NAMES[t])
+def test_emulated_dequant_bitexact(oracle, emu, wt):
+    """The device dequantizer's decode (unit.h) through the planar layout
+    reproduces the reference dequantization bit for bit, for every tile
+    width (padding rows and columns included)."""
+    rng = np.random.default_rng(800 + wt)
+    n_out, n_in = (37, 1792) if wt in KQ else (37, 1120)
+    W = synth.make_weights(wt, n_out, n_in, rng)
+    ref = np.stack([oracle.dequant(wt, W[r], n_in) for r in range(n_out)])
+    for G in [1, 4, 64]:
+        got = emu.dequant(wt, n_out, n_in, G, W)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (siq.NAMES[wt], G)

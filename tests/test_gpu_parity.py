@@ -208,3 +208,31 @@ def test_gemv_multi_matches_single_and_oracle(dev, oracle, combo):
             b.free()
         for w in ws:
             w.free()
+
+
+@pytest.mark.parametrize("wt", sa.WEIGHT_TYPES, ids=lambda t: sa.NAMES[t])
+def test_dequant_rows_bitexact(dev, oracle, monkeypatch, wt):
+    """row_to_f32 from the device copy: bit-identical to the reference
+    dequantizer, for one row at a time (host pointer) and for a range of rows
+    into device memory, at a narrow and a wide tile (padding included)."""
+    rng = np.random.default_rng(3000 + wt)
+    n_out, n_in = (37, 1792) if wt in KQ else (37, 1120)
+    W = synth.make_weights(wt, n_out, n_in, rng)
+    ref = np.stack([oracle.dequant(wt, W[r], n_in) for r in range(n_out)])
+    for G in (1, 16):
+        monkeypatch.setenv("SIHIP_TILE_COLS", str(G))
+        w = dev.upload(wt, n_out, n_in, W)
+        buf = dev.alloc(n_out * n_in * 4)
+        try:
+            for r in (0, 17, n_out - 1):
+                got = dev.dequant_row(w, r)
+                assert np.array_equal(got.view(np.uint32), ref[r].view(np.uint32)), (sa.NAMES[wt], G, r)
+            dev.dequant_rows_dev(w, 3, n_out - 3, buf.ptr, n_in)
+            dev.synchronize()
+            got = buf.to_host(np.float32, (n_out - 3) * n_in).reshape(n_out - 3, n_in)
+            assert np.array_equal(got.view(np.uint32), ref[3:].view(np.uint32)), (sa.NAMES[wt], G)
+            with pytest.raises(sa.SihipError):
+                dev.dequant_row(w, n_out)  # past the last row
+        finally:
+            buf.free()
+            w.free()
