@@ -163,6 +163,15 @@ int si_backend_hip_gemm(si_backend *be, const si_tensor *w, const float *X, int6
     return SI_OK;
 }
 
+int si_backend_hip_upload(si_backend *be, const si_tensor *w) {
+    if (!be || !w || !w->data) {
+        si_set_err("hip upload: bad arguments");
+        return SI_EINVAL;
+    }
+    sihip_weight *dw;
+    return device_weight(as_hip(be), w, &dw);
+}
+
 int si_backend_hip_weights(const si_backend *be, uint64_t *device_bytes) {
     const hip_backend *hb = (const hip_backend *)be;
     uint64_t total = 0;

@@ -87,3 +87,10 @@ int th_row_to_f32(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, 
 }
 
 int th_weights(si_backend *be, uint64_t *bytes) { return si_backend_hip_weights(be, bytes); }
+
+int th_upload(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, const void *data,
+              uint64_t bytes) {
+    g_err[0] = 0;
+    const si_tensor t = make_tensor(be, type, n_out, n_in, data, bytes);
+    return si_backend_hip_upload(be, &t);
+}

@@ -24,6 +24,7 @@ class Harness:
         L.th_gemm.argtypes = [vp, u32, u64, u64, vp, u64, vp, i64, vp]
         L.th_row_to_f32.argtypes = [vp, u32, u64, u64, vp, u64, u64, vp]
         L.th_weights.argtypes = [vp, ctypes.POINTER(u64)]
+        L.th_upload.argtypes = [vp, u32, u64, u64, vp, u64]
         self.L = L
 
     def errstr(self) -> str:
@@ -51,6 +52,9 @@ class Harness:
     def row_to_f32(self, be, wt, n_out, n_in, W, row, out):
         return self.L.th_row_to_f32(be, wt, n_out, n_in, W.ctypes.data, W.nbytes, row,
                                     out.ctypes.data)
+
+    def upload(self, be, wt, n_out, n_in, W):
+        return self.L.th_upload(be, wt, n_out, n_in, W.ctypes.data, W.nbytes)
 
     def weights(self, be):
         b = ctypes.c_uint64()

@@ -4,8 +4,8 @@ include/siphon/tensor.h:43-55), driven through its test harness.
 
 CPU tests: loading and failure behaviour (missing library, no device).
 GPU tests: gemv / gemm / row_to_f32 through the vtable against the oracle,
-upload-once caching, and the reference's error contract (message set,
-output untouched)."""
+upload-once caching, the load-time upload hook, and the reference's error
+contract (message set, output untouched)."""
 import numpy as np
 import pytest
 
@@ -125,5 +125,42 @@ def test_reused_address_is_not_served_stale(harness, oracle):
         ref2, l2 = oracle.gemv(sa.F16, W2, 64, 512, x2)
         assert np.all(np.abs(y2.astype(np.float64) - ref2) <= 1e-5 * l2 + 1e-6)
         assert harness.weights(be)[0] == 1  # the stale copy was replaced, not kept
+    finally:
+        harness.close(be)
+
+
+@pytest.mark.gpu
+def test_load_time_upload(harness, oracle):
+    """si_backend_hip_upload puts every tensor of a model on the device at
+    load time: later gemv / gemm calls on them upload nothing, a second
+    upload of the same tensor is a no-op, and a bad tensor is refused with a
+    message."""
+    rc, be = harness.open(HIP_SO)
+    assert rc == 0, harness.errstr()
+    try:
+        rng = np.random.default_rng(31)
+        shapes = ((sa.Q4_K, 256, 4096), (sa.Q6_K, 96, 9216), (sa.Q5_0, 33, 640))
+        Ws = [synth.make_weights(wt, n_out, n_in, rng) for wt, n_out, n_in in shapes]
+        for (wt, n_out, n_in), W in zip(shapes, Ws):
+            assert harness.upload(be, wt, n_out, n_in, W) == 0, harness.errstr()
+        n, nbytes = harness.weights(be)
+        assert n == len(shapes) and nbytes >= sum(W.nbytes for W in Ws)
+        for (wt, n_out, n_in), W in zip(shapes, Ws):
+            assert harness.upload(be, wt, n_out, n_in, W) == 0
+            x = rng.standard_normal(n_in).astype(np.float32)
+            y = np.full(n_out, np.nan, np.float32)
+            assert harness.gemv(be, wt, n_out, n_in, W, x, y, n_out) == 0, harness.errstr()
+            ref, l1 = oracle.gemv(wt, W, n_out, n_in, x)
+            assert np.all(np.abs(y.astype(np.float64) - ref) <= 1e-5 * l1 + 1e-6), sa.NAMES[wt]
+            X = rng.standard_normal((8, n_in)).astype(np.float32)
+            Y = np.zeros((8, n_out), np.float32)
+            assert harness.gemm(be, wt, n_out, n_in, W, X, Y) == 0, harness.errstr()
+            R, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+            assert np.all(np.abs(Y.astype(np.float64) - R) <= 1e-5 * L1 + 1e-6), sa.NAMES[wt]
+        assert harness.weights(be) == (n, nbytes)
+        bad = np.zeros(10, np.uint8)  # byte count does not match the shape
+        assert harness.upload(be, sa.Q4_K, 16, 256, bad) == -1
+        assert "upload" in harness.errstr()
+        assert harness.weights(be) == (n, nbytes)
     finally:
         harness.close(be)
