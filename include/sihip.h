@@ -75,7 +75,15 @@ int sihip_weight_upload(sihip_ctx *ctx, uint32_t ggml_type, uint64_t n_out,
                         uint64_t n_in, const void *host_blocks,
                         uint64_t bytes, sihip_weight **out);
 int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w);
-/* Device bytes the repacked weight occupies (>= the GGUF bytes). */
+/* Build now the weight's second device copy in the order of the
+ * matrix-core GEMM (Q4_K only; other types: no-op), which sihip_gemm
+ * otherwise builds on its first call with M >= 5. No reference
+ * counterpart: it belongs to the batched prefill slot, which the reference
+ * lacks (its prompt runs token by token, cmd_run.c:275-283). For loaders
+ * that put everything on the device before the first token. Idempotent. */
+int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w);
+/* Device bytes the weight occupies: the repacked copy (>= the GGUF bytes),
+ * the column-slice partial sums, and the GEMM copy once built. */
 uint64_t sihip_weight_device_bytes(const sihip_weight *w);
 /* Layout introspection: row columns (256-element super-blocks for the
  * K-quants, 32-element blocks otherwise) handled side by side by one

@@ -68,6 +68,7 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_weight_device_bytes.restype = _u64
     L.sihip_weight_tile_cols.argtypes = [_vp]
     L.sihip_weight_slice_rounds.argtypes = [_vp]
+    L.sihip_weight_prepare_gemm.argtypes = [_vp, _vp]
     L.sihip_gemv.argtypes = [_vp, _vp, _vp, _vp, _i64]
     L.sihip_gemm.argtypes = [_vp, _vp, _vp, _i64, _vp]
     L.sihip_gemv_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
@@ -125,6 +126,10 @@ class Weight:
     @property
     def gguf_bytes(self) -> int:
         return self.n_out * row_bytes(self.type, self.n_in)
+
+    def prepare_gemm(self):
+        """Build the matrix-core GEMM copy now (Q4_K; no-op otherwise)."""
+        self.dev._check(self.dev.L.sihip_weight_prepare_gemm(self.dev.ctx, self.handle))
 
     def free(self):
         if self.handle:

@@ -523,6 +523,41 @@ static int64_t gemm_min_m() {
 
 static bool gemm_mfma_supported(uint32_t type) { return type == T_Q4_K; }
 
+// The weight's copy in the GEMM's order (gemm_layout_kernel), built from
+// its matvec copy on stream st.
+static int build_gemm_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
+    const Layout &L = w->L;
+    const int64_t nb = L.n_in / 256;
+    const int64_t nblk32 = (L.n_out + kGemmBN - 1) / kGemmBN * (kGemmBN / 32);
+    const int64_t bytes = gemm_layout_bytes(nblk32, nb);
+    uint8_t *g = nullptr;
+    hipError_t e = hipMalloc(&g, (size_t)bytes);
+    if (e != hipSuccess)
+        return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
+                       hipGetErrorString(e));
+    const int64_t threads = nblk32 * nb * (kGemmChunk / 16);
+    hipLaunchKernelGGL(gemm_layout_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       st, L, (const uint8_t *)w->dev, g, nblk32);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        (void)hipFree(g);
+        return set_err(ctx, SIHIP_EDEVICE, "gemm layout: %s", hipGetErrorString(e));
+    }
+    w->gemm = g;
+    w->gemm_bytes = bytes;
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
+    if (!ctx || !w) return set_err(ctx, SIHIP_EINVAL, "weight_prepare_gemm: NULL argument");
+    if (!gemm_mfma_supported(w->L.type) || w->gemm) return SIHIP_OK;
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const int rc = build_gemm_copy(ctx, w, ctx->stream);
+    if (rc) return rc;
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
 // Y[m, :] = W x[m, :] for m < M on the matrix cores. The activation planes
 // live in the context's workspace, so calls on one context must not overlap.
 static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X, int64_t ldx,
@@ -532,23 +567,8 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
     const int64_t K = L.n_in, nb = K / 256;
     const int NB = (int)((L.n_out + kGemmBN - 1) / kGemmBN);
     if (!w->gemm) {
-        const int64_t nblk32 = (int64_t)NB * (kGemmBN / 32);
-        const int64_t bytes = gemm_layout_bytes(nblk32, nb);
-        uint8_t *g = nullptr;
-        hipError_t e = hipMalloc(&g, (size_t)bytes);
-        if (e != hipSuccess)
-            return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
-                           hipGetErrorString(e));
-        const int64_t threads = nblk32 * nb * (kGemmChunk / 16);
-        hipLaunchKernelGGL(gemm_layout_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                           st, L, (const uint8_t *)w->dev, g, nblk32);
-        e = hipGetLastError();
-        if (e != hipSuccess) {
-            (void)hipFree(g);
-            return set_err(ctx, SIHIP_EDEVICE, "gemm layout: %s", hipGetErrorString(e));
-        }
-        w->gemm = g;
-        w->gemm_bytes = bytes;
+        const int rc = build_gemm_copy(ctx, w, st);
+        if (rc) return rc;
     }
     // small M: 32-row m tiles (twice the workgroups) with four super-blocks
     // of weights in flight per wave; SIHIP_GEMM_MT (1 or 2) overrides

@@ -17,6 +17,7 @@ typedef struct {
     int (*weight_upload)(sihip_ctx *, uint32_t, uint64_t, uint64_t, const void *, uint64_t,
                          sihip_weight **);
     int (*weight_free)(sihip_ctx *, sihip_weight *);
+    int (*weight_prepare_gemm)(sihip_ctx *, sihip_weight *);
     uint64_t (*weight_device_bytes)(const sihip_weight *);
     int (*gemv)(sihip_ctx *, const sihip_weight *, const float *, float *, int64_t);
     int (*gemm)(sihip_ctx *, const sihip_weight *, const float *, int64_t, float *);
@@ -168,8 +169,18 @@ int si_backend_hip_upload(si_backend *be, const si_tensor *w) {
         si_set_err("hip upload: bad arguments");
         return SI_EINVAL;
     }
+    hip_backend *hb = as_hip(be);
     sihip_weight *dw;
-    return device_weight(as_hip(be), w, &dw);
+    const int rc = device_weight(hb, w, &dw);
+    if (rc) return rc;
+    const int grc = hb->f.weight_prepare_gemm(hb->ctx, dw);
+    if (grc) {
+        si_set_err("hip: gemm copy of a %llu x %llu tensor: %s",
+                   (unsigned long long)w->ne[1], (unsigned long long)w->ne[0],
+                   hb->f.last_error(hb->ctx));
+        return si_code(grc);
+    }
+    return SI_OK;
 }
 
 int si_backend_hip_weights(const si_backend *be, uint64_t *device_bytes) {
@@ -216,6 +227,7 @@ int si_backend_hip_open(const char *lib_path, int device, si_backend **out) {
     RESOLVE(last_error, "sihip_last_error");
     RESOLVE(weight_upload, "sihip_weight_upload");
     RESOLVE(weight_free, "sihip_weight_free");
+    RESOLVE(weight_prepare_gemm, "sihip_weight_prepare_gemm");
     RESOLVE(weight_device_bytes, "sihip_weight_device_bytes");
     RESOLVE(gemv, "sihip_gemv");
     RESOLVE(gemm, "sihip_gemm");

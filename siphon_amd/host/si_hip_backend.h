@@ -53,12 +53,13 @@ void si_backend_hip_close(si_backend *be);
 int si_backend_hip_gemm(si_backend *be, const si_tensor *w, const float *X, int64_t M,
                         float *Y);
 
-/* Upload w now rather than on its first gemv: the model loader's hook for
- * device-resident weights (after si_tensor_from_gguf, reference
- * backend.c:144-176, model.c:171 assigning layer backends), so the first
- * token pays no upload. Idempotent: a tensor already on the device (same
- * data pointer, type and shape) is not uploaded again. SI_OK or a negative
- * SI_* code with si_errstr() set. */
+/* Upload w now rather than on its first gemv or gemm: the model loader's
+ * hook for device-resident weights (after si_tensor_from_gguf, reference
+ * backend.c:144-176, model.c:13), so neither the first token nor the first
+ * prompt pays an upload. Builds the matrix-core GEMM copy too where the type
+ * has one. Idempotent: a tensor already on the device (same data pointer,
+ * type and shape) is not uploaded again. SI_OK or a negative SI_* code with
+ * si_errstr() set. */
 int si_backend_hip_upload(si_backend *be, const si_tensor *w);
 
 /* Number of weight tensors uploaded so far and their device bytes. */

@@ -105,3 +105,35 @@ def test_gemm_k_slices(dev, oracle, monkeypatch, mt, sbk):
     assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
     assert_close(Y3.reshape(-1), ref[:5].reshape(-1).astype(np.float64), L1[:5].reshape(-1),
                  what + " M=5")
+
+
+def test_prepare_gemm_matches_lazy_copy(dev, oracle):
+    """sihip_weight_prepare_gemm builds the GEMM copy at once (device bytes
+    grow by it, a second call adds nothing); a later gemm gives the bits of a
+    weight whose copy its first gemm built. Other types: a no-op."""
+    rng = np.random.default_rng(4242)
+    n_out, n_in, M = 700, 2048, 40
+    W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
+    X = _rows(rng, M, n_in)
+    eager, lazy = dev.upload(sa.Q4_K, n_out, n_in, W), dev.upload(sa.Q4_K, n_out, n_in, W)
+    W6 = synth.make_weights(sa.Q6_K, 64, 512, rng)
+    w6 = dev.upload(sa.Q6_K, 64, 512, W6)
+    try:
+        before = eager.device_bytes
+        eager.prepare_gemm()
+        grown = eager.device_bytes
+        assert grown > before
+        eager.prepare_gemm()
+        assert eager.device_bytes == grown
+        Ye, Yl = dev.gemm(eager, X), dev.gemm(lazy, X)
+        assert lazy.device_bytes == grown
+        assert np.array_equal(Ye.view(np.uint32), Yl.view(np.uint32))
+        ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
+        assert_close(Ye.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
+                     f"prepared gemm {n_out}x{n_in} M={M}")
+        b6 = w6.device_bytes
+        w6.prepare_gemm()
+        assert w6.device_bytes == b6
+    finally:
+        for w in (eager, lazy, w6):
+            w.free()

@@ -13,7 +13,7 @@ import siphon_amd as sa
 from siphon_amd import synth
 from siphon_amd.build import HIP_SO
 
-SI_ENOENT, SI_EIO = -6, -2
+SI_ENOENT, SI_EIO, SI_EINVAL = -6, -2, -5
 
 
 @pytest.fixture(scope="module")
@@ -132,9 +132,9 @@ def test_reused_address_is_not_served_stale(harness, oracle):
 @pytest.mark.gpu
 def test_load_time_upload(harness, oracle):
     """si_backend_hip_upload puts every tensor of a model on the device at
-    load time: later gemv / gemm calls on them upload nothing, a second
-    upload of the same tensor is a no-op, and a bad tensor is refused with a
-    message."""
+    load time, the matrix-core GEMM copy of Q4_K included: later gemv / gemm
+    calls on them allocate nothing, a second upload of the same tensor is a
+    no-op, and a bad tensor is refused with a message."""
     rc, be = harness.open(HIP_SO)
     assert rc == 0, harness.errstr()
     try:
@@ -159,7 +159,7 @@ def test_load_time_upload(harness, oracle):
             assert np.all(np.abs(Y.astype(np.float64) - R) <= 1e-5 * L1 + 1e-6), sa.NAMES[wt]
         assert harness.weights(be) == (n, nbytes)
         bad = np.zeros(10, np.uint8)  # byte count does not match the shape
-        assert harness.upload(be, sa.Q4_K, 16, 256, bad) == -1
+        assert harness.upload(be, sa.Q4_K, 16, 256, bad) == SI_EINVAL
         assert "upload" in harness.errstr()
         assert harness.weights(be) == (n, nbytes)
     finally:
