@@ -139,6 +139,30 @@ int sihip_gemv_multi_dev(sihip_ctx *ctx, int count,
                          const sihip_weight *const *w, const float *x,
                          float *const *y, void *stream);
 
+/* Decode attention of one layer at position pos over an f16 KV cache, for
+ * every query head h (reference attn_head, engine.c:90-147): the query
+ * narrowed to f16; score j = f16 dot(key j, query) * kq_scale for
+ * j <= pos; softmax; probabilities narrowed to f16; out[h * head_dim + c] =
+ * f16 dot(value row c, probabilities). KV head of h: h / (n_head /
+ * n_head_kv). Device pointers, the layer's slice of the reference's cache
+ * layouts (engine.c:200-203, 345-357):
+ *   q        f32 [n_head * head_dim]
+ *   k_cache  f16 bits [n_head_kv][n_ctx][head_dim]
+ *   v_cache  f16 bits [n_head_kv][head_dim][n_ctx]  (transposed)
+ *   out      f32 [n_head * head_dim]
+ *   scores   f32 [n_head][n_ctx], probs16 f16 bits [n_head][n_ctx]:
+ *            optional (NULL: the context's workspace); the first pos + 1
+ *            entries of each row are written.
+ * Bit-identical to the reference's x86 path (its AVX2 f16 dot, softmax and
+ * exp polynomial), up to the order of the softmax's double total and the
+ * rounding of libm's expf on the last n % 8 positions, which change a
+ * result only in rare cases. head_dim <= 512. Calls sharing a context's
+ * workspace must not overlap. */
+int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint16_t *k_cache,
+                          const uint16_t *v_cache, int64_t n_head, int64_t n_head_kv,
+                          int64_t head_dim, int64_t n_ctx, int64_t pos, float kq_scale,
+                          float *out, float *scores, uint16_t *probs16, void *stream);
+
 /* ---- device memory for hosts without a HIP runtime of their own -------
  * The reference host is plain C17 and never links HIP; these let it (and
  * tests) hold activations and outputs on the device for the *_dev entry

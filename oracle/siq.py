@@ -79,6 +79,14 @@ class Oracle:
         L.siq_vec_dot_dequant.argtypes = [_u32, _i64, _vp, _vp, _vp, _vp]
         L.siq_gemv.argtypes = [_u32, _vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_int]
         L.siq_gemm.argtypes = [_u32, _vp, _i64, _i64, _vp, _i64, _vp, _vp, ctypes.c_int]
+        L.siq_expf_poly.argtypes = [ctypes.c_float]
+        L.siq_expf_poly.restype = ctypes.c_float
+        L.siq_softmax.argtypes = [_vp, _vp, _i64, ctypes.c_float]
+        L.siq_softmax.restype = None
+        L.siq_dot_f16_simd.argtypes = [_i64, _vp, _vp]
+        L.siq_dot_f16_simd.restype = ctypes.c_float
+        L.siq_attn_decode.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
+                                      _vp, _vp, _vp]
         self.L = L
 
     def f16_to_f32(self, h: int) -> float:
@@ -129,6 +137,35 @@ class Oracle:
         return Y, L1
 
 
+    def expf_poly(self, x: np.ndarray) -> np.ndarray:
+        return np.array([self.L.siq_expf_poly(float(v)) for v in np.asarray(x, np.float32)],
+                        dtype=np.float32)
+
+    def softmax(self, x: np.ndarray, max_: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros_like(x)
+        self.L.siq_softmax(_ptr(y), _ptr(x), x.size, max_)
+        return y
+
+    def dot_f16(self, a: np.ndarray, b: np.ndarray) -> float:
+        a = np.ascontiguousarray(a, dtype=np.uint16)
+        b = np.ascontiguousarray(b, dtype=np.uint16)
+        return self.L.siq_dot_f16_simd(a.size, _ptr(a), _ptr(b))
+
+    def attn_decode(self, q, k, v, n_head, n_head_kv, hd, n_ctx, pos, kq_scale):
+        """(out [n_head*hd] f32, scores [n_head][n_ctx] f32, probs16 [n_head][n_ctx] u16);
+        entries past pos of a scores/probs row are zero."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        k = np.ascontiguousarray(k, dtype=np.uint16)
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        out = np.zeros(n_head * hd, np.float32)
+        sc = np.zeros((n_head, n_ctx), np.float32)
+        pr = np.zeros((n_head, n_ctx), np.uint16)
+        assert self.L.siq_attn_decode(_ptr(q), _ptr(k), _ptr(v), n_head, n_head_kv, hd, n_ctx,
+                                      pos, kq_scale, _ptr(out), _ptr(sc), _ptr(pr))
+        return out, sc, pr
+
+
 class Reference:
     """The reference's own kernels (compiled from /root/reference/src by
     oracle/Makefile); None-returning loader when it was not built."""
@@ -156,6 +193,10 @@ class Reference:
                 f.restype = None
         L.ref_shim_gemv.argtypes = [_u32, _vp, _i64, _i64, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp]
         L.ref_shim_gemv.restype = ctypes.c_int
+        L.si_expf.argtypes = [ctypes.c_float]
+        L.si_expf.restype = ctypes.c_float
+        L.si_softmax.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_float]
+        L.si_softmax.restype = None
         self.L = L
         self.avx2 = bool(L.ref_shim_impl())
 
@@ -202,6 +243,49 @@ class Reference:
         f = getattr(self.L, ("si_avx2_dot_" if simd else "si_dot_") + self.DOT_NAMES[wtype])
         f(n, ctypes.byref(s), _ptr(w), _ptr(a))
         return s.value
+
+    def expf(self, x: np.ndarray) -> np.ndarray:
+        return np.array([self.L.si_expf(float(v)) for v in np.asarray(x, np.float32)],
+                        dtype=np.float32)
+
+    def softmax(self, x: np.ndarray, max_: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros_like(x)
+        self.L.si_softmax(_ptr(y), _ptr(x), x.size, max_)
+        return y
+
+    def attn_decode(self, q, k, v, n_head, n_head_kv, hd, n_ctx, pos, kq_scale):
+        """One layer's decode attention composed from the reference's own
+        kernels in the steps of its attn_head (engine.c:90-147): f16 query,
+        the dispatched f16 dot per cached position, the scale, the max, its
+        softmax, f16 probabilities, the dispatched f16 dot per value row.
+        Same return as Oracle.attn_decode."""
+        q = np.asarray(q, np.float32)
+        k = np.asarray(k, np.uint16).reshape(n_head_kv, n_ctx, hd)
+        v = np.asarray(v, np.uint16).reshape(n_head_kv, hd, n_ctx)
+        n, gqa = pos + 1, n_head // n_head_kv
+        ks = np.float32(kq_scale)
+        out = np.zeros(n_head * hd, np.float32)
+        sc_all = np.zeros((n_head, n_ctx), np.float32)
+        pr_all = np.zeros((n_head, n_ctx), np.uint16)
+        for h in range(n_head):
+            hk = h // gqa
+            q16 = self.f16(q[h * hd:(h + 1) * hd])
+            q8 = q16.view(np.uint8)
+            sc = np.array([self.dot(F16, hd, k[hk, j].view(np.uint8), q8, simd=self.avx2)
+                           for j in range(n)], np.float32) * ks
+            mx = np.float32(-np.inf)
+            for s in sc:
+                if s > mx:
+                    mx = s
+            pr16 = self.f16(self.softmax(sc, float(mx)))
+            p8 = pr16.view(np.uint8)
+            out[h * hd:(h + 1) * hd] = [
+                self.dot(F16, n, np.ascontiguousarray(v[hk, c, :n]).view(np.uint8), p8,
+                         simd=self.avx2) for c in range(hd)]
+            sc_all[h, :n] = sc
+            pr_all[h, :n] = pr16
+        return out, sc_all, pr_all
 
     def gemv_timed(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, x: np.ndarray,
                    lanes: int, reps: int):

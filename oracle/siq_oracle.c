@@ -537,3 +537,109 @@ int siq_gemm(uint32_t wtype, const void *W, int64_t n_out, int64_t n_in,
     }
     return 1;
 }
+
+/* ---- decode attention over an f16 KV cache ------------------------------
+ * Restates reference engine.c:90-147 (attn_head) with the pieces its x86
+ * build dispatches to: the f16 dot of kernels_avx2.c:118-148, the softmax
+ * of kernels.c:855-885 and its exp polynomial, kernels.c:820-850. Unlike
+ * the quantized dots above, these are reproduced in the reference's own
+ * floating-point operation order, since their results feed an f16 rounding
+ * (the probabilities) that an exact evaluation would not reproduce. */
+
+float siq_expf_poly(float x) {
+    /* x = n*ln2 + b: n from the 1.5*2^23 rounding shift, ln2 in two parts */
+    const float shift = 0x1.8p23f;
+    const float z = fmaf(x, 0x1.715476p+0f, shift);
+    const float n = z - shift;
+    const float b = fmaf(-n, 0x1.7f7d1cp-20f, fmaf(-n, 0x1.62e4p-1f, x));
+    /* 2^n: the integer in z's low mantissa bits moved to the exponent */
+    const uint32_t e = f2u(z) << 23;
+    const float k = u2f(e + 0x3f800000u);
+    const float u = b * b;
+    const float p = fmaf(fmaf(fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u,
+                              fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
+                         u, 0x1.ffffecp-1f * b);
+    if (!(fabsf(n) > 126.0f)) return fmaf(p, k, k);
+    /* |n| > 126: 2^n split over two factors; |n| > 192: over/underflow */
+    const uint32_t g = n <= 0.0f ? 0x82000000u : 0u;
+    const float s1 = u2f(g + 0x7f000000u);
+    if (fabsf(n) > 192.0f) return s1 * s1;
+    const float s2 = u2f(e - g);
+    return fmaf(s2, p, s2) * s1;
+}
+
+void siq_softmax(float *y, const float *x, int64_t n, float max) {
+    double total = 0.0;
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        float v[8];
+        for (int k = 0; k < 8; k++) v[k] = y[i + k] = siq_expf_poly(x[i + k] - max);
+        /* the 8-lane horizontal sum: lanes l and l+4, then pairs */
+        const float a = (v[0] + v[4]) + (v[2] + v[6]);
+        const float c = (v[1] + v[5]) + (v[3] + v[7]);
+        total += (double)(a + c);
+    }
+    for (; i < n; i++) {
+        const float val = expf(x[i] - max);
+        total += (double)val;
+        y[i] = val;
+    }
+    const float scale = (float)(1.0 / total);
+    for (i = 0; i < n; i++) y[i] *= scale;
+}
+
+float siq_dot_f16_simd(int64_t n, const uint16_t *a, const uint16_t *b) {
+    /* accumulator 8*r + l is lane l of register r: element i of every
+     * 32-element step goes to accumulator i % 32 */
+    float acc[32];
+    for (int k = 0; k < 32; k++) acc[k] = 0.0f;
+    const int64_t body = n & ~(int64_t)31;
+    for (int64_t i = 0; i < body; i += 32)
+        for (int k = 0; k < 32; k++)
+            acc[k] = fmaf(siq_f16_to_f32(a[i + k]), siq_f16_to_f32(b[i + k]), acc[k]);
+    /* registers r0 += r2, r1 += r3, r0 += r1; then lanes l + (l + 4);
+     * then two pairwise rounds */
+    float s[8];
+    for (int l = 0; l < 8; l++) s[l] = (acc[l] + acc[16 + l]) + (acc[8 + l] + acc[24 + l]);
+    float t[4];
+    for (int l = 0; l < 4; l++) t[l] = s[l] + s[l + 4];
+    double total = 0.0;
+    total += (double)((t[0] + t[1]) + (t[2] + t[3]));
+    for (int64_t i = body; i < n; i++)
+        total += (double)(siq_f16_to_f32(a[i]) * siq_f16_to_f32(b[i]));
+    return (float)total;
+}
+
+int siq_attn_decode(const float *q, const uint16_t *k, const uint16_t *v, int64_t n_head,
+                    int64_t n_head_kv, int64_t hd, int64_t n_ctx, int64_t pos, float kq_scale,
+                    float *out, float *scores, uint16_t *probs16) {
+    if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv || hd < 1 || pos < 0 || pos >= n_ctx)
+        return 0;
+    const int64_t n = pos + 1, gqa = n_head / n_head_kv;
+    float *sc = malloc((size_t)n * sizeof *sc);
+    float *pr = malloc((size_t)n * sizeof *pr);
+    uint16_t *p16 = malloc((size_t)n * sizeof *p16);
+    uint16_t *q16 = malloc((size_t)hd * sizeof *q16);
+    if (!sc || !pr || !p16 || !q16) {
+        free(sc), free(pr), free(p16), free(q16);
+        return 0;
+    }
+    for (int64_t h = 0; h < n_head; h++) {
+        const int64_t hk = h / gqa;
+        const uint16_t *kh = k + hk * n_ctx * hd;   /* [n_ctx][hd] */
+        const uint16_t *vh = v + hk * hd * n_ctx;   /* [hd][n_ctx] */
+        for (int64_t d = 0; d < hd; d++) q16[d] = siq_f32_to_f16(q[h * hd + d]);
+        float max = -INFINITY;
+        for (int64_t j = 0; j < n; j++) {
+            sc[j] = siq_dot_f16_simd(hd, kh + j * hd, q16) * kq_scale;
+            if (sc[j] > max) max = sc[j];
+        }
+        siq_softmax(pr, sc, n, max);
+        for (int64_t j = 0; j < n; j++) p16[j] = siq_f32_to_f16(pr[j]);
+        for (int64_t c = 0; c < hd; c++) out[h * hd + c] = siq_dot_f16_simd(n, vh + c * n_ctx, p16);
+        if (scores) memcpy(scores + h * n_ctx, sc, (size_t)n * sizeof *sc);
+        if (probs16) memcpy(probs16 + h * n_ctx, p16, (size_t)n * sizeof *p16);
+    }
+    free(sc), free(pr), free(p16), free(q16);
+    return 1;
+}

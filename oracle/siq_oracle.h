@@ -93,6 +93,29 @@ int siq_gemv(uint32_t wtype, const void *W, int64_t n_out, int64_t n_in,
 int siq_gemm(uint32_t wtype, const void *W, int64_t n_out, int64_t n_in,
              const float *X, int64_t M, float *Y, double *L1, int lanes);
 
+/* ---- decode attention over an f16 KV cache (reference engine.c:90-147) --
+ * Evaluated in the reference's x86 operation order, bit for bit:
+ *   siq_expf_poly     the exp polynomial of softmax groups, kernels.c:820-850
+ *   siq_softmax       groups of 8 with the 8-lane sum order, a double total,
+ *                     libm expf on the tail, kernels.c:855-885
+ *   siq_dot_f16_simd  32 f32 FMA accumulators, the register/lane reduction
+ *                     tree, the tail in double, kernels_avx2.c:118-148
+ * Pinned (tests/test_oracle_attn.py) against the compiled reference's own
+ * functions and an attention golden fixture from it, bit-exact, and against
+ * double-precision mathematics (exp error, softmax sum, dot value). */
+float siq_expf_poly(float x);
+void siq_softmax(float *y, const float *x, int64_t n, float max);
+float siq_dot_f16_simd(int64_t n, const uint16_t *a, const uint16_t *b);
+/* Every head h of one layer at position pos: q f32 [n_head * hd]; the
+ * layer's caches k f16 [n_head_kv][n_ctx][hd] and v f16 [n_head_kv][hd][n_ctx]
+ * (reference engine.c:200-203, 345-357); KV head h / (n_head / n_head_kv).
+ * out f32 [n_head * hd]; scores (scaled, f32) and probs16 (f16 bits), each
+ * [n_head][n_ctx] with the first pos + 1 entries of a row written, are
+ * optional. Returns 1, or 0 on bad arguments. */
+int siq_attn_decode(const float *q, const uint16_t *k, const uint16_t *v, int64_t n_head,
+                    int64_t n_head_kv, int64_t hd, int64_t n_ctx, int64_t pos, float kq_scale,
+                    float *out, float *scores, uint16_t *probs16);
+
 #ifdef __cplusplus
 }
 #endif

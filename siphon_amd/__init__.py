@@ -74,6 +74,8 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_gemv_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
     L.sihip_dequant_row.argtypes = [_vp, _vp, _u64, _vp]
     L.sihip_dequant_rows_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _i64, _vp]
+    L.sihip_attn_decode_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                        ctypes.c_float, _vp, _vp, _vp, _vp]
     L.sihip_gemm_dev.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
     L.sihip_gemv_multi_dev.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(_vp), _vp,
                                        ctypes.POINTER(_vp), _vp]
@@ -190,6 +192,14 @@ class Device:
                          stream: int | None = None):
         self._check(self.L.sihip_dequant_rows_dev(self.ctx, w.handle, row0, nrows, out_ptr, ldo,
                                                   stream))
+
+    def attn_decode_dev(self, q_ptr: int, k_ptr: int, v_ptr: int, n_head: int, n_head_kv: int,
+                        head_dim: int, n_ctx: int, pos: int, kq_scale: float, out_ptr: int,
+                        scores_ptr: int | None = None, probs_ptr: int | None = None,
+                        stream: int | None = None):
+        self._check(self.L.sihip_attn_decode_dev(self.ctx, q_ptr, k_ptr, v_ptr, n_head, n_head_kv,
+                                                 head_dim, n_ctx, pos, kq_scale, out_ptr,
+                                                 scores_ptr, probs_ptr, stream))
 
     def gemm_dev(self, w: Weight, X_ptr: int, M: int, Y_ptr: int, stream: int | None = None):
         self._check(self.L.sihip_gemm_dev(self.ctx, w.handle, X_ptr, M, Y_ptr, stream))

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/sihip.h"
+#include "attn.h"
 #include "formats.h"
 #include "gemm.h"
 #include "matvec.h"
@@ -39,6 +40,8 @@ struct sihip_ctx {
     void *d_gpart = nullptr;  // prefill GEMM K slices: partial sums
     size_t d_gpart_cap = 0;
     uint32_t *d_gcnt = nullptr;  // prefill GEMM K slices: arrival counters (zero between calls)
+    void *d_attn = nullptr;  // decode attention: scores and f16 probabilities
+    size_t d_attn_cap = 0;
 };
 
 // Arrival counters of K-sliced GEMM tiles, allocated (and zeroed) on the
@@ -125,6 +128,7 @@ extern "C" void sihip_shutdown(sihip_ctx *ctx) {
     if (ctx->d_ws) (void)hipFree(ctx->d_ws);
     if (ctx->d_gpart) (void)hipFree(ctx->d_gpart);
     if (ctx->d_gcnt) (void)hipFree(ctx->d_gcnt);
+    if (ctx->d_attn) (void)hipFree(ctx->d_attn);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -731,6 +735,58 @@ extern "C" int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float
     if (M <= 0) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: M must be positive");
     if (!aligned16(X)) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: X must be 16-byte aligned");
     return run_gemm(ctx, w, X, M, Y, (hipStream_t)stream);
+}
+
+extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint16_t *k_cache,
+                                     const uint16_t *v_cache, int64_t n_head, int64_t n_head_kv,
+                                     int64_t head_dim, int64_t n_ctx, int64_t pos, float kq_scale,
+                                     float *out, float *scores, uint16_t *probs16, void *stream) {
+    if (!ctx || !q || !k_cache || !v_cache || !out)
+        return set_err(ctx, SIHIP_EINVAL, "attn_decode_dev: NULL argument");
+    if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv != 0 || n_head > 4096)
+        return set_err(ctx, SIHIP_EINVAL,
+                       "attn_decode_dev: n_head %lld must be a multiple of n_head_kv %lld (<= 4096)",
+                       (long long)n_head, (long long)n_head_kv);
+    if (head_dim < 1 || head_dim > kAttnMaxHd)
+        return set_err(ctx, SIHIP_EINVAL, "attn_decode_dev: head_dim %lld outside 1..%d",
+                       (long long)head_dim, kAttnMaxHd);
+    if (n_ctx < 1 || n_ctx > (int64_t)INT32_MAX || pos < 0 || pos >= n_ctx)
+        return set_err(ctx, SIHIP_EINVAL, "attn_decode_dev: pos %lld outside 0..n_ctx-1 (n_ctx %lld)",
+                       (long long)pos, (long long)n_ctx);
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const int64_t rows = n_head * n_ctx;
+    AttnArgs A;
+    A.q = q;
+    A.k = k_cache;
+    A.v = v_cache;
+    A.out = out;
+    A.n_ctx = n_ctx;
+    A.ld = n_ctx;
+    A.n = (int)(pos + 1);
+    A.hd = (int)head_dim;
+    A.gqa = (int)(n_head / n_head_kv);
+    A.n_head = (int)n_head;
+    A.kq_scale = kq_scale;
+    A.sc = scores;
+    A.p16 = probs16;
+    if (!scores || !probs16) {
+        // scores (f32) then probabilities (f16), [n_head][n_ctx] each
+        const int rc = ensure(ctx, &ctx->d_attn, &ctx->d_attn_cap, (size_t)rows * 6);
+        if (rc) return rc;
+        if (!scores) A.sc = (float *)ctx->d_attn;
+        if (!probs16) A.p16 = (uint16_t *)((uint8_t *)ctx->d_attn + rows * 4);
+    }
+    const int chunks = (A.gqa + kAttnHeads - 1) / kAttnHeads;
+    const dim3 gs((unsigned)((A.n + kAttnRows - 1) / kAttnRows), (unsigned)(n_head_kv * chunks));
+    const dim3 gv((unsigned)((head_dim + kAttnRows - 1) / kAttnRows), (unsigned)(n_head_kv * chunks));
+    if (gs.y > 65535) return set_err(ctx, SIHIP_EINVAL, "attn_decode_dev: too many KV heads");
+    const hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(attn_scores_kernel, gs, dim3(kAttnThreads), 0, st, A);
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3((unsigned)n_head), dim3(kAttnThreads), 0, st, A);
+    hipLaunchKernelGGL(attn_values_kernel, gv, dim3(kAttnThreads), 0, st, A);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "attention launch: %s", hipGetErrorString(e));
+    return SIHIP_OK;
 }
 
 extern "C" int sihip_gemv_multi_dev(sihip_ctx *ctx, int count, const sihip_weight *const *w,
