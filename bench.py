@@ -16,12 +16,13 @@ N(0,1); both are resident in HBM before timing starts.
 
 Extra fields: the dominant kernel's roofline (Q4_K matvec, per-launch HIP
 events), the M=512 prefill GEMM (config 3) in TOPS, the other formats'
-matvec rates at configs 0, 1 and 4 (batch 1 and 8), and the reference's own
-AVX2 gemv (oracle/_ref, through its lane pool) on a bounded sample of the
-same weights on the host cores.
+matvec rates at configs 0, 1 and 4 (batch 1 and 8), the decode attention
+over an f16 KV cache at the 8B shape (positions 511 and 4095), and the
+reference's own AVX2 gemv (oracle/_ref, through its lane pool) on a bounded
+sample of the same weights on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-gemm]
-                    [--no-configs] [--profile gemm|traffic|configs]
+                    [--no-configs] [--no-attn] [--profile gemm|traffic|configs|attn]
 """
 from __future__ import annotations
 
@@ -62,10 +63,11 @@ def parse():
                     help="one launch per matrix instead of fused q/k/v and gate/up launches")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-format matvec measurements (configs 0, 1, 4)")
-    ap.add_argument("--profile", choices=("gemm", "traffic", "configs"),
+    ap.add_argument("--no-attn", action="store_true", help="skip the decode attention")
+    ap.add_argument("--profile", choices=("gemm", "traffic", "configs", "attn"),
                     help="run one workload for a profiler and exit: the GEMM M sweep, "
                          "a 64 MiB copy plus 12 gate/up launches (HBM counter runs), "
-                         "or the per-format matvec measurements")
+                         "the per-format matvec measurements, or the decode attention")
     return ap.parse_args()
 
 
@@ -109,6 +111,8 @@ def main():
             out = bench_gemm(dev, torch, stream, rng)
         elif args.profile == "configs":
             out = bench_configs(dev, torch, stream, rng)
+        elif args.profile == "attn":
+            out = bench_attention(dev, torch, stream)
         else:
             out = profile_traffic(dev, torch, stream, rng)
         dev.close()
@@ -241,6 +245,8 @@ def main():
 
     if not args.no_gemm:
         result["gemm_m512"] = bench_gemm(dev, torch, stream, rng)
+    if not args.no_attn:
+        result["attention"] = bench_attention(dev, torch, stream)
     if not args.no_configs:
         for l in layers:  # the per-format runs upload their own matrices
             for w in l.values():
@@ -257,6 +263,56 @@ def main():
             w.free()
     dev.close()
     print(json.dumps(result), flush=True)
+
+
+def bench_attention(dev, torch, stream, positions=(511, 4095)):
+    """Decode attention over the f16 KV cache at Llama-3-8B's shape (32
+    query heads, 8 KV heads, head_dim 128, n_ctx 4096): the three launches of
+    one layer, the 32 layers' caches (537 MB, past the 256 MB MALL) in one
+    HIP graph. Algorithmic bytes per layer: the K and V slices read (2 x 8 x
+    n x 128 x 2 B), the query and output (2 x 32 x 128 x 4 B)."""
+    n_head, n_kv, hd, n_ctx = 32, 8, 128, 4096
+    sp = stream.cuda_stream
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    caches = [(torch.randn(n_kv * n_ctx * hd, device="cuda", generator=g).half(),
+               torch.randn(n_kv * hd * n_ctx, device="cuda", generator=g).half())
+              for _ in range(N_LAYERS)]
+    q = torch.randn(N_LAYERS, n_head * hd, device="cuda", generator=g)
+    out = torch.empty(N_LAYERS, n_head * hd, device="cuda")
+    kq = float(1.0 / np.sqrt(hd))
+    res = {"shape": {"n_head": n_head, "n_head_kv": n_kv, "head_dim": hd, "n_ctx": n_ctx},
+           "launches_per_layer": 3}
+    for pos in positions:
+        def layer_pass():
+            for il in range(N_LAYERS):
+                k, v = caches[il]
+                dev.attn_decode_dev(q[il].data_ptr(), k.data_ptr(), v.data_ptr(), n_head, n_kv,
+                                    hd, n_ctx, pos, kq, out[il].data_ptr(), None, None, sp)
+        with torch.cuda.stream(stream):
+            layer_pass()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            layer_pass()
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = 10
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            with torch.cuda.stream(stream):
+                graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * N_LAYERS)
+        nbytes = 2 * n_kv * (pos + 1) * hd * 2 + 2 * n_head * hd * 4
+        res[f"pos{pos}"] = {"us_per_layer": round(us, 2), "kv_bytes": nbytes,
+                            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                            "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del graph
+    return res
 
 
 def bench_gemm(dev, torch, stream, rng):

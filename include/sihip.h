@@ -150,9 +150,11 @@ int sihip_gemv_multi_dev(sihip_ctx *ctx, int count,
  *   k_cache  f16 bits [n_head_kv][n_ctx][head_dim]
  *   v_cache  f16 bits [n_head_kv][head_dim][n_ctx]  (transposed)
  *   out      f32 [n_head * head_dim]
- *   scores   f32 [n_head][n_ctx], probs16 f16 bits [n_head][n_ctx]:
- *            optional (NULL: the context's workspace); the first pos + 1
- *            entries of each row are written.
+ *   scores   f32 [n_head][n_ctx] scaled scores, optional (NULL: the
+ *            context's workspace)
+ *   probs16  f16 bits [n_head][n_ctx] probabilities, optional (NULL: not
+ *            written)
+ *   the first pos + 1 entries of each row are written.
  * Bit-identical to the reference's x86 path (its AVX2 f16 dot, softmax and
  * exp polynomial), up to the order of the softmax's double total and the
  * rounding of libm's expf on the last n % 8 positions, which change a

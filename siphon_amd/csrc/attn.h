@@ -5,18 +5,27 @@
 //
 // Three launches on one stream:
 //   attn_scores_kernel   sc[h][j] = dot(K[hk][j], f16(q_h)) * kq_scale
-//   attn_softmax_kernel  p16[h][j] = f16(softmax(sc[h])[j])
-//   attn_values_kernel   out[h][c] = dot(V[hk][c][0..n), p16[h])
+//   attn_softmax_kernel  p[h][j] = f16(softmax(sc[h])[j])
+//   attn_pv_kernel       out[h][c] = dot(V[hk][c][0..n), p[h])
 //
 // The f16 dot is evaluated in the reference's order. Its 32 f32
 // accumulators (accumulator a takes elements i with i % 32 == a, by FMA in
 // increasing i) are spread over 8 lanes of one row, 4 each: lane L of the
 // row holds accumulators 4L..4L+3. The reference reduces them as
 // registers r0+r2, r1+r3, then their sum, then lanes l and l+4, then two
-// pairwise rounds; with that lane assignment these are the lane-xor steps
-// 4, 2, 1 followed by two in-lane additions. Elements past the last
+// pairwise rounds; with that lane assignment these are additions of lanes
+// L + 4, L + 2, L + 1 followed by two in-lane additions. Elements past the last
 // multiple of 32 are added to the double total one by one, as in the
 // reference.
+//
+// Each accumulator is one chain of n / 32 dependent FMAs over the whole
+// context, so the value contraction cannot be split along the positions
+// without changing the result. attn_pv_kernel instead stages a whole
+// chunk of value rows and probabilities in LDS with every thread's loads in
+// flight at once, then runs the chains out of LDS. Workspace rows (scores
+// and probabilities) hold lw >= n entries, lw a multiple of kAttnBlock, so
+// whole-block loads stay inside the allocation; entries past n are loaded
+// but not used.
 //
 // The softmax sums its 8-element group totals in double in a tree rather
 // than in the reference's sequential order. The two double totals differ
@@ -43,26 +52,38 @@ struct AttnArgs {
     const uint16_t *k;     // [n_head_kv][n_ctx][hd]
     const uint16_t *v;     // [n_head_kv][hd][n_ctx]
     float *out;            // [n_head * hd]
-    float *sc;             // [n_head][ld] scaled scores
-    uint16_t *p16;         // [n_head][ld] f16 probabilities
-    int64_t n_ctx, ld;
+    float *sc;             // [n_head][ld] scaled scores (caller's, optional)
+    uint16_t *p16;         // [n_head][ld] f16 probabilities (caller's, optional)
+    float *sw;             // [n_head][lw] scaled scores (workspace)
+    uint16_t *pw;          // [n_head][lw] f16 probabilities (workspace)
+    int64_t n_ctx, ld, lw;
     int n, hd, gqa, n_head;
     float kq_scale;
 };
 
 __device__ inline float f16_at(const uint16_t *p, int64_t i) { return f16_bits_to_f32(p[i]); }
 
+// Lane i receives lane i + K of its 16-lane row (a DPP row shift; lanes
+// whose source lies past the row receive 0, and are not used below).
+template <int K>
+__device__ inline float from_lane_up(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + K, 0xf, 0xf, true));
+}
+
 // The reference's tree over the 32 accumulators of one row; lane L of the
-// row (lane & 7) holds acc[e] = accumulator 4L + e. Every lane of the wave
-// takes part; the result is valid in lane L == 0.
+// row (lane & 7, rows of 8 lanes) holds acc[e] = accumulator 4L + e. Lane
+// L adds lane L + 4 (registers r0 + r2 at L = 0, 1; r1 + r3 at L = 2, 3),
+// then lane L + 2 (the sum of those), then lane L + 1 (lanes l and l + 4
+// of the reference's 8-wide registers); the result is valid in L == 0.
+// Every lane of the wave takes part.
 __device__ inline float dot_tree(const float acc[4]) {
     float x[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) x[e] = acc[e] + __shfl_xor(acc[e], 4);  // r0 + r2, r1 + r3
+    for (int e = 0; e < 4; e++) x[e] = acc[e] + from_lane_up<4>(acc[e]);
 #pragma unroll
-    for (int e = 0; e < 4; e++) x[e] = x[e] + __shfl_xor(x[e], 2);      // (r0+r2) + (r1+r3)
+    for (int e = 0; e < 4; e++) x[e] = x[e] + from_lane_up<2>(x[e]);
 #pragma unroll
-    for (int e = 0; e < 4; e++) x[e] = x[e] + __shfl_xor(x[e], 1);      // lanes l + (l + 4)
+    for (int e = 0; e < 4; e++) x[e] = x[e] + from_lane_up<1>(x[e]);
     return (x[0] + x[1]) + (x[2] + x[3]);
 }
 
@@ -95,6 +116,9 @@ __device__ inline float expf_poly(float x) {
 // workgroup scores kAttnRows cached positions against up to kAttnHeads
 // query heads of one KV head, holding each key row in registers across
 // the heads.
+// VEC: hd % 4 == 0 and k 8-byte aligned (a lane's 4 key elements of a step
+// in one load).
+template <bool VEC>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
     __shared__ uint16_t q16[kAttnHeads * kAttnMaxHd];
     const int chunks = (A.gqa + kAttnHeads - 1) / kAttnHeads;
@@ -102,9 +126,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
     const int h0 = hk * A.gqa + (blockIdx.y % chunks) * kAttnHeads;
     const int nh = min(kAttnHeads, hk * A.gqa + A.gqa - h0);
     const int hd = A.hd;
-    for (int i = threadIdx.x; i < nh * hd; i += kAttnThreads)
-        q16[i] = f32_to_f16_bits(A.q[(int64_t)h0 * hd + i]);
-    __syncthreads();
     const int L = threadIdx.x & (kAttnRowLanes - 1);
     const int64_t j = (int64_t)blockIdx.x * kAttnRows + threadIdx.x / kAttnRowLanes;
     const int64_t jr = j < A.n ? j : A.n - 1;  // rows past n score row n-1, unstored
@@ -113,9 +134,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
     float kv[kAttnMaxHd / 32][4];
 #pragma unroll
     for (int t = 0; t < kAttnMaxHd / 32; t++)
-        if (32 * t < body)
+        if (32 * t < body) {
+            if constexpr (VEC) {
+                const uint2 w = *reinterpret_cast<const uint2 *>(krow + 32 * t + 4 * L);
+                kv[t][0] = f16_bits_to_f32(w.x & 0xffffu);
+                kv[t][1] = f16_bits_to_f32(w.x >> 16);
+                kv[t][2] = f16_bits_to_f32(w.y & 0xffffu);
+                kv[t][3] = f16_bits_to_f32(w.y >> 16);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) kv[t][e] = f16_at(krow, 32 * t + 4 * L + e);
+                for (int e = 0; e < 4; e++) kv[t][e] = f16_at(krow, 32 * t + 4 * L + e);
+            }
+        }
+    // the query heads in f16, staged while the key loads are in flight
+    for (int i = threadIdx.x; i < nh * hd; i += kAttnThreads)
+        q16[i] = f32_to_f16_bits(A.q[(int64_t)h0 * hd + i]);
+    __syncthreads();
     for (int hh = 0; hh < nh; hh++) {
         const uint16_t *qh = q16 + hh * hd;
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -131,113 +165,223 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
             total += (double)res;
             for (int i = body; i < hd; i++)
                 total += (double)(f16_at(krow, i) * f16_bits_to_f32(qh[i]));
-            A.sc[(int64_t)(h0 + hh) * A.ld + j] = (float)total * A.kq_scale;
+            const float v = (float)total * A.kq_scale;
+            A.sw[(int64_t)(h0 + hh) * A.lw + j] = v;
+            if (A.sc) A.sc[(int64_t)(h0 + hh) * A.ld + j] = v;
         }
     }
 }
 
-// Block-wide reductions over kAttnThreads threads.
-__device__ inline float block_max(float m, float *red) {
+constexpr int kAttnBlock = 4096;  // softmax positions per workgroup pass (16 per thread)
+
+// Positions b + 16t .. b + 16t + 15 of a row for thread t: two 8-groups.
+struct SoftBlock {
+    float v[16];
+};
+
+__device__ inline void load_soft_block(const float *row, int b, SoftBlock &blk) {
+    const float4 *p = reinterpret_cast<const float4 *>(row + b + 16 * threadIdx.x);
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float t = __shfl_xor(m, o);
-        m = t > m ? t : m;
+    for (int i = 0; i < 4; i++) {
+        const float4 f = p[i];
+        blk.v[4 * i] = f.x;
+        blk.v[4 * i + 1] = f.y;
+        blk.v[4 * i + 2] = f.z;
+        blk.v[4 * i + 3] = f.w;
     }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = m;
-    __syncthreads();
-    m = red[0];
-    for (int i = 1; i < kAttnThreads / 64; i++) m = red[i] > m ? red[i] : m;
-    __syncthreads();
-    return m;
 }
 
-__device__ inline double block_sum(double s, double *red) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = s;
-    __syncthreads();
-    s = red[0];
-    for (int i = 1; i < kAttnThreads / 64; i++) s += red[i];
-    return s;
-}
+// exp of a tail position's shifted score (positions past the last whole
+// 8-group): exp in double, rounded.
+__device__ inline float tail_exp(float x) { return (float)exp((double)x); }
 
-// Grid n_head: one workgroup per query head. Exponentials are evaluated
-// twice (for the total, then for the probabilities) rather than stored.
+// Grid n_head: one workgroup per query head. The max, the total and the
+// f16 probabilities each take one pass over the row in blocks of
+// kAttnBlock positions; with n <= kAttnBlock the block stays in registers
+// and its exponentials are evaluated once.
 __global__ __launch_bounds__(kAttnThreads) void attn_softmax_kernel(AttnArgs A) {
     __shared__ float redf[kAttnThreads / 64];
     __shared__ double redd[kAttnThreads / 64];
-    const float *sc = A.sc + (int64_t)blockIdx.x * A.ld;
-    uint16_t *p16 = A.p16 + (int64_t)blockIdx.x * A.ld;
-    const int n = A.n;
-    float m = -__builtin_inff();
-    for (int j = threadIdx.x; j < n; j += kAttnThreads) m = sc[j] > m ? sc[j] : m;
-    const float mx = block_max(m, redf);
-    const int groups = n / 8;
-    double part = 0.0;
-    for (int g = threadIdx.x; g < groups; g += kAttnThreads) {
-        float v[8];
+    const int h = blockIdx.x;
+    const float *row = A.sw + (int64_t)h * A.lw;
+    const int n = A.n, gend = n & ~7;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool one = n <= kAttnBlock;
+    SoftBlock blk;
+    float mx = -__builtin_inff();
+    for (int b = 0; b < n; b += kAttnBlock) {
+        load_soft_block(row, b, blk);
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = expf_poly(sc[8 * g + e] - mx);
-        part += (double)(((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7])));
+        for (int e = 0; e < 16; e++)
+            if (b + 16 * (int)threadIdx.x + e < n && blk.v[e] > mx) mx = blk.v[e];
     }
-    if (threadIdx.x == 0)
-        for (int j = 8 * groups; j < n; j++) part += (double)(float)exp((double)(sc[j] - mx));
-    const double total = block_sum(part, redd);
-    const float scale = (float)(1.0 / total);
-    for (int j = threadIdx.x; j < n; j += kAttnThreads) {
-        const float x = sc[j] - mx;
-        const float e = j < 8 * groups ? expf_poly(x) : (float)exp((double)x);
-        p16[j] = f32_to_f16_bits(e * scale);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float t = __shfl_xor(mx, o);
+        mx = t > mx ? t : mx;
     }
+    if (lane == 0) redf[wave] = mx;
+    __syncthreads();
+    mx = redf[0];
+    for (int i = 1; i < kAttnThreads / 64; i++) mx = redf[i] > mx ? redf[i] : mx;
+    // total: the 8-groups (lane order of the reference's 8-wide sum), then
+    // the tail
+    // the thread whose 16 positions hold the tail [gend, n)
+    const int tail_b = gend / kAttnBlock * kAttnBlock;
+    const bool tail_owner = gend < n && (int)threadIdx.x == (gend - tail_b) / 16;
+    double part = 0.0;
+    float ex[16];
+    for (int b = 0; b < n; b += kAttnBlock) {
+        if (!one) load_soft_block(row, b, blk);
+#pragma unroll
+        for (int e = 0; e < 16; e++) ex[e] = expf_poly(blk.v[e] - mx);
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const int j0 = b + 16 * (int)threadIdx.x + 8 * g;
+            const float *v = ex + 8 * g;
+            if (j0 + 8 <= gend)
+                part += (double)(((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7])));
+        }
+    }
+    if (tail_owner)
+        for (int j = gend; j < n; j++) part += (double)tail_exp(row[j] - mx);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+    if (lane == 0) redd[wave] = part;
+    __syncthreads();
+    part = redd[0];
+    for (int i = 1; i < kAttnThreads / 64; i++) part += redd[i];
+    const float scale = (float)(1.0 / part);
+    uint16_t *pw = A.pw + (int64_t)h * A.lw;
+    for (int b = 0; b < n; b += kAttnBlock) {
+        if (!one) {
+            load_soft_block(row, b, blk);
+#pragma unroll
+            for (int e = 0; e < 16; e++) ex[e] = expf_poly(blk.v[e] - mx);
+        }
+        const int j0 = b + 16 * (int)threadIdx.x;
+        uint32_t pk[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            pk[e] = (uint32_t)f32_to_f16_bits(ex[2 * e] * scale) |
+                    ((uint32_t)f32_to_f16_bits(ex[2 * e + 1] * scale) << 16);
+        // whole 32-byte pieces into the workspace row (lw entries)
+        uint4 *dst = reinterpret_cast<uint4 *>(pw + j0);
+        dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        if (A.p16)
+            for (int e = 0; e < 16 && j0 + e < n; e++)
+                A.p16[(int64_t)h * A.ld + j0 + e] = (uint16_t)(pk[e >> 1] >> (16 * (e & 1)));
+    }
+    // the tail's probabilities replace the polynomial's (same thread, later stores)
+    if (tail_owner)
+        for (int j = gend; j < n; j++) {
+            const uint16_t pb = f32_to_f16_bits(tail_exp(row[j] - mx) * scale);
+            pw[j] = pb;
+            if (A.p16) A.p16[(int64_t)h * A.ld + j] = pb;
+        }
 }
 
-// Grid (ceil(hd / kAttnRows), n_head_kv * ceil(gqa / kAttnHeads)): each
-// workgroup contracts kAttnRows value rows with up to kAttnHeads
-// probability rows of one KV head, each value element read once for all
-// of them.
-__global__ __launch_bounds__(kAttnThreads) void attn_values_kernel(AttnArgs A) {
+// Grid (ceil(hd / kAttnPvRows), n_head_kv * ceil(gqa / kAttnHeads)):
+// each workgroup owns kAttnPvRows value rows of one KV head and up to
+// kAttnHeads query heads of it, wave w running head h0 + w. Per chunk of
+// kAttnChunk positions every thread requests its share of the value rows
+// and probability rows at once, stores them to LDS, and each wave runs its
+// accumulator chains over the chunk: lane 8r + L holds accumulators
+// 4L..4L+3 of row r. Then the reduction tree, the tail (inside the last
+// chunk) and the store.
+constexpr int kAttnPvRows = 8;
+constexpr int kAttnChunk = 2048;  // positions per LDS chunk (a multiple of 32, divides kAttnBlock)
+constexpr int kAttnVPieces = kAttnPvRows * kAttnChunk / 8 / kAttnThreads;  // 16-byte pieces
+constexpr int kAttnPPieces = kAttnHeads * kAttnChunk / 8 / kAttnThreads;
+
+// VEC: n_ctx % 8 == 0 and v 16-byte aligned (16-byte value pieces).
+template <bool VEC>
+__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs A) {
+    __shared__ __attribute__((aligned(16))) uint16_t sv[kAttnPvRows * kAttnChunk];
+    __shared__ __attribute__((aligned(16))) uint16_t sp[kAttnHeads * kAttnChunk];
     const int chunks = (A.gqa + kAttnHeads - 1) / kAttnHeads;
     const int hk = blockIdx.y / chunks;
     const int h0 = hk * A.gqa + (blockIdx.y % chunks) * kAttnHeads;
     const int nh = min(kAttnHeads, hk * A.gqa + A.gqa - h0);
-    const int L = threadIdx.x & (kAttnRowLanes - 1);
-    const int c = blockIdx.x * kAttnRows + threadIdx.x / kAttnRowLanes;
-    const int cr = c < A.hd ? c : A.hd - 1;
-    const uint16_t *vrow = A.v + ((int64_t)hk * A.hd + cr) * A.n_ctx;
-    const uint16_t *prow[kAttnHeads];
-#pragma unroll
-    for (int hh = 0; hh < kAttnHeads; hh++)
-        prow[hh] = A.p16 + (int64_t)(h0 + (hh < nh ? hh : nh - 1)) * A.ld;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool active = wave < nh;
     const int n = A.n, body = n & ~31;
-    float acc[kAttnHeads][4];
+    const int r = lane >> 3, L = lane & 7;
+    const int c = blockIdx.x * kAttnPvRows + r;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int s0 = 0;
+    for (;; s0 += kAttnChunk) {
+        const int cl = min(kAttnChunk, n - s0);
+        const int per_row = (cl + 7) / 8;  // 16-byte pieces of a row in this chunk
+        // probability rows: whole pieces of the workspace (lw >= s0 + kAttnChunk);
+        // heads past nh repeat head nh - 1
+        uint4 pq[kAttnPPieces];
 #pragma unroll
-    for (int hh = 0; hh < kAttnHeads; hh++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc[hh][e] = 0.0f;
-#pragma unroll 4
-    for (int i0 = 0; i0 < body; i0 += 32) {
-        const int i = i0 + 4 * L;
-        float vv[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) vv[e] = f16_at(vrow, i + e);
-#pragma unroll
-        for (int hh = 0; hh < kAttnHeads; hh++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                acc[hh][e] = __builtin_fmaf(vv[e], f16_at(prow[hh], i + e), acc[hh][e]);
-    }
-#pragma unroll
-    for (int hh = 0; hh < kAttnHeads; hh++) {
-        const float res = dot_tree(acc[hh]);
-        if (L == 0 && hh < nh && c < A.hd) {
-            double total = 0.0;
-            total += (double)res;
-            for (int i = body; i < n; i++)
-                total += (double)(f16_at(vrow, i) * f16_at(prow[hh], i));
-            A.out[(int64_t)(h0 + hh) * A.hd + c] = (float)total;
+        for (int i = 0; i < kAttnPPieces; i++) {
+            const int t = threadIdx.x + kAttnThreads * i;
+            const int hh = min(t / (kAttnChunk / 8), nh - 1), pc = t % (kAttnChunk / 8);
+            pq[i] = reinterpret_cast<const uint4 *>(A.pw + (int64_t)(h0 + hh) * A.lw + s0)[pc];
         }
+        if constexpr (VEC) {
+            // value rows (rows past hd repeat row hd - 1); pieces past the
+            // chunk's end load the chunk's last piece again (n_ctx % 8 == 0:
+            // it ends inside the row)
+            uint4 vq[kAttnVPieces];
+#pragma unroll
+            for (int i = 0; i < kAttnVPieces; i++) {
+                const int t = threadIdx.x + kAttnThreads * i;
+                const int rr = t / (kAttnChunk / 8), pc = min(t % (kAttnChunk / 8), per_row - 1);
+                const int cr = min(blockIdx.x * kAttnPvRows + rr, A.hd - 1);
+                vq[i] = reinterpret_cast<const uint4 *>(
+                    A.v + ((int64_t)hk * A.hd + cr) * A.n_ctx + s0)[pc];
+            }
+#pragma unroll
+            for (int i = 0; i < kAttnVPieces; i++) {
+                const int t = threadIdx.x + kAttnThreads * i;
+                reinterpret_cast<uint4 *>(sv)[t] = vq[i];
+            }
+        } else {
+#pragma unroll 8
+            for (int t = threadIdx.x; t < kAttnPvRows * cl; t += kAttnThreads) {
+                const int rr = t / cl, i = t - rr * cl;
+                const int cr = min(blockIdx.x * kAttnPvRows + rr, A.hd - 1);
+                sv[rr * kAttnChunk + i] = A.v[((int64_t)hk * A.hd + cr) * A.n_ctx + s0 + i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kAttnPPieces; i++)
+            reinterpret_cast<uint4 *>(sp)[threadIdx.x + kAttnThreads * i] = pq[i];
+        __syncthreads();
+        // the accumulator chains over the chunk's whole 32-steps
+        if (active) {
+            const uint16_t *vr = sv + r * kAttnChunk;
+            const uint16_t *pr = sp + wave * kAttnChunk;
+            const int steps_end = min(body - s0, cl);
+#pragma unroll 4
+            for (int i0 = 0; i0 < steps_end; i0 += 32) {
+                const int i = i0 + 4 * L;
+                const uint2 vw = *reinterpret_cast<const uint2 *>(vr + i);
+                const uint2 pw = *reinterpret_cast<const uint2 *>(pr + i);
+                acc[0] = __builtin_fmaf(f16_bits_to_f32(vw.x & 0xffffu), f16_bits_to_f32(pw.x & 0xffffu), acc[0]);
+                acc[1] = __builtin_fmaf(f16_bits_to_f32(vw.x >> 16), f16_bits_to_f32(pw.x >> 16), acc[1]);
+                acc[2] = __builtin_fmaf(f16_bits_to_f32(vw.y & 0xffffu), f16_bits_to_f32(pw.y & 0xffffu), acc[2]);
+                acc[3] = __builtin_fmaf(f16_bits_to_f32(vw.y >> 16), f16_bits_to_f32(pw.y >> 16), acc[3]);
+            }
+        }
+        if (s0 + cl >= n) break;
+        __syncthreads();  // the next chunk overwrites sv and sp
+    }
+    // the tail [body, n) lies in the last chunk, still in LDS
+    const float res = dot_tree(acc);
+    if (active && L == 0 && c < A.hd) {
+        const int h = h0 + wave;
+        double total = 0.0;
+        total += (double)res;
+        for (int j = body; j < n; j++)
+            total += (double)(f16_bits_to_f32(sv[r * kAttnChunk + j - s0]) *
+                              f16_bits_to_f32(sp[wave * kAttnChunk + j - s0]));
+        A.out[(int64_t)h * A.hd + c] = (float)total;
     }
 }
 

@@ -754,7 +754,6 @@ extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint1
         return set_err(ctx, SIHIP_EINVAL, "attn_decode_dev: pos %lld outside 0..n_ctx-1 (n_ctx %lld)",
                        (long long)pos, (long long)n_ctx);
     HIP_OK(ctx, hipSetDevice(ctx->device));
-    const int64_t rows = n_head * n_ctx;
     AttnArgs A;
     A.q = q;
     A.k = k_cache;
@@ -767,23 +766,33 @@ extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint1
     A.gqa = (int)(n_head / n_head_kv);
     A.n_head = (int)n_head;
     A.kq_scale = kq_scale;
-    A.sc = scores;
-    A.p16 = probs16;
-    if (!scores || !probs16) {
-        // scores (f32) then probabilities (f16), [n_head][n_ctx] each
-        const int rc = ensure(ctx, &ctx->d_attn, &ctx->d_attn_cap, (size_t)rows * 6);
-        if (rc) return rc;
-        if (!scores) A.sc = (float *)ctx->d_attn;
-        if (!probs16) A.p16 = (uint16_t *)((uint8_t *)ctx->d_attn + rows * 4);
-    }
+    A.sc = scores;    // NULL: not written
+    A.p16 = probs16;  // NULL: not written
+    // workspace scores (f32) and probabilities (f16): rows of whole
+    // kAttnBlock blocks, so that block loads stay inside the allocation
+    A.lw = (A.n + kAttnBlock - 1) / kAttnBlock * kAttnBlock;
+    const int rc = ensure(ctx, &ctx->d_attn, &ctx->d_attn_cap, (size_t)(n_head * A.lw * 6));
+    if (rc) return rc;
+    A.sw = (float *)ctx->d_attn;
+    A.pw = (uint16_t *)((uint8_t *)ctx->d_attn + n_head * A.lw * 4);
     const int chunks = (A.gqa + kAttnHeads - 1) / kAttnHeads;
     const dim3 gs((unsigned)((A.n + kAttnRows - 1) / kAttnRows), (unsigned)(n_head_kv * chunks));
-    const dim3 gv((unsigned)((head_dim + kAttnRows - 1) / kAttnRows), (unsigned)(n_head_kv * chunks));
+    const dim3 gv((unsigned)((head_dim + kAttnPvRows - 1) / kAttnPvRows),
+                  (unsigned)(n_head_kv * chunks));
     if (gs.y > 65535) return set_err(ctx, SIHIP_EINVAL, "attn_decode_dev: too many KV heads");
     const hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(attn_scores_kernel, gs, dim3(kAttnThreads), 0, st, A);
+    // wide loads where rows stay aligned: keys 8 bytes, value rows 16
+    const bool kvec = head_dim % 4 == 0 && (uintptr_t)k_cache % 8 == 0;
+    const bool vvec = n_ctx % 8 == 0 && (uintptr_t)v_cache % 16 == 0;
+    if (kvec)
+        hipLaunchKernelGGL(attn_scores_kernel<true>, gs, dim3(kAttnThreads), 0, st, A);
+    else
+        hipLaunchKernelGGL(attn_scores_kernel<false>, gs, dim3(kAttnThreads), 0, st, A);
     hipLaunchKernelGGL(attn_softmax_kernel, dim3((unsigned)n_head), dim3(kAttnThreads), 0, st, A);
-    hipLaunchKernelGGL(attn_values_kernel, gv, dim3(kAttnThreads), 0, st, A);
+    if (vvec)
+        hipLaunchKernelGGL(attn_pv_kernel<true>, gv, dim3(kAttnThreads), 0, st, A);
+    else
+        hipLaunchKernelGGL(attn_pv_kernel<false>, gv, dim3(kAttnThreads), 0, st, A);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "attention launch: %s", hipGetErrorString(e));
     return SIHIP_OK;

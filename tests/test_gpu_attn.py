@@ -75,6 +75,7 @@ def test_golden_cases(dev):
     (16, 1, 96, 200, 199),      # 16 query heads on one KV head (4 passes)
     (6, 2, 256, 33, 0),         # position 0
     (3, 1, 8, 20, 17),          # head dim below one 32-element step
+    (4, 2, 66, 40, 39),         # head dim not a multiple of 4: narrow key loads
 ])
 def test_vs_oracle(dev, oracle, n_head, n_kv, hd, n_ctx, pos):
     rng = np.random.default_rng(n_head * 7919 + hd * 31 + pos)
