@@ -15,6 +15,12 @@
 // |bsum| <= 2032 are exact in f16, and every partial sum stays below 2^24,
 // so the f32 result is exact). Only the per-super-block f32 epilogue rounds.
 //
+// Q2_K (reference kernels.c:249-287) has the same form with 16 groups of
+// 16: S[m,n] = sum_g sc_g[n] * sum_{k in g} q[n,k] * x[m,k] with 4-bit
+// scales and 2-bit quants, so the weight operand sc * q <= 45 fits int8
+// and one MFMA per 32-element unit accumulates S exactly; T takes the
+// 4-bit group mins.
+//
 // MFMA operand layout (gfx950, checked on the device): for the 32x32x32 i8
 // and 32x32x16 f16 forms lane l supplies row (l % 32) of A and column
 // (l % 32) of B at the k positions of its half h = l / 32; A and B use the
@@ -130,9 +136,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_quantize_x(const float *x, 
 // the block record.
 struct GemmW {
     uint2 u[8];
-    uint4 scb;   // sh_0..sh_7 (x, y), sl_0..sl_7 (z, w): one byte per unit
+    uint4 scb;   // Q4_K: sh_0..sh_7 (x, y), sl_0..sl_7 (z, w); Q2_K: sc_0..sc_15
     float2 dd;   // d, dmin
-    v8h_t bm;    // mins of units 4h..4h+3 (this lane's half), each twice
+    v8h_t bm;    // mins of groups 8h..8h+7 (this lane's half; Q4_K: unit mins twice)
 };
 
 // ---- GEMM weight order ---------------------------------------------------------
@@ -145,11 +151,13 @@ struct GemmW {
 //   4 x 1024 B: for q = 0..3 and lane L = 32 h + r (r = row in the block),
 //               bytes 16 L .. 16 L + 7 = half h of unit 2q of row r,
 //               bytes 16 L + 8 .. 16 L + 15 = half h of unit 2q + 1 of row r
+//               (Q2_K: its 2-bit quants widened to the same nibble order)
 //   512 B:      per row, the unit scales sc_j = 8 sh_j + sl_j split in
-//               bytes: sh_0..sh_7, then sl_0..sl_7
+//               bytes: sh_0..sh_7, then sl_0..sl_7 (Q2_K: the 16 group
+//               scales, one byte each)
 //   256 B:      per row, f32 d and dmin
 //   1024 B:     per lane L, f16 mins of units 4h..4h+3 of row r, each twice
-//               (the B operand of the min MFMA)
+//               (Q2_K: of groups 8h..8h+7; the B operand of the min MFMA)
 // so a wave loads a super-block with 8 coalesced loads per lane, each unit
 // half already where the MFMA B operand wants it and no scale decoding left
 // in the loop.
@@ -174,25 +182,45 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
     const int slot = (int)(i % per);
     const int64_t blk = chunk / nb, c = chunk % nb;
     uint32_t v[4] = {0, 0, 0, 0};
+    const bool q2 = L.type == T_Q2_K;
     if (slot < kGemmScOff / 16) {  // unit halves
         const int q = slot >> 6, lane = slot & 63, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out) {
             for (int k = 0; k < 2; k++) {
-                const uint8_t *src = planes + unit_off(L, 0, row, c * 8 + 2 * q + k) + 8 * h;
-                v[2 * k] = ldp<uint32_t>(src);
-                v[2 * k + 1] = ldp<uint32_t>(src + 4);
+                if (q2) {
+                    // Q2_K plane record: element 16 i + 4 t + e of the unit at
+                    // bits 8 e + 2 t of word i; byte b of half h takes element
+                    // 8 h + b (low nibble) and 16 + 8 h + b (high nibble)
+                    const uint8_t *src = planes + unit_off(L, 0, row, c * 8 + 2 * q + k);
+                    const uint32_t w0 = ldp<uint32_t>(src), w1 = ldp<uint32_t>(src + 4);
+                    for (int b = 0; b < 8; b++) {
+                        const int e = 8 * h + b;
+                        const int sh = 8 * (e & 3) + 2 * (e >> 2);
+                        const uint32_t nib = ((w0 >> sh) & 3u) | (((w1 >> sh) & 3u) << 4);
+                        v[2 * k + (b >> 2)] |= nib << (8 * (b & 3));
+                    }
+                } else {
+                    const uint8_t *src = planes + unit_off(L, 0, row, c * 8 + 2 * q + k) + 8 * h;
+                    v[2 * k] = ldp<uint32_t>(src);
+                    v[2 * k + 1] = ldp<uint32_t>(src + 4);
+                }
             }
         }
     } else if (slot < kGemmDOff / 16) {  // scale bytes of one row
         const int64_t row = blk * 32 + (slot - kGemmScOff / 16);
         if (row < L.n_out) {
             const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
-            for (int j = 0; j < 8; j++) {
-                int sc, mn;
-                k4_scale_min(m, j, sc, mn);
-                v[j >> 2] |= (uint32_t)(sc >> 3) << (8 * (j & 3));
-                v[2 + (j >> 2)] |= (uint32_t)(sc & 7) << (8 * (j & 3));
+            if (q2) {  // the 4-bit group scales sc_0..sc_15
+                v[0] = m.x & 0x0F0F0F0Fu; v[1] = m.y & 0x0F0F0F0Fu;
+                v[2] = m.z & 0x0F0F0F0Fu; v[3] = m.w & 0x0F0F0F0Fu;
+            } else {
+                for (int j = 0; j < 8; j++) {
+                    int sc, mn;
+                    k4_scale_min(m, j, sc, mn);
+                    v[j >> 2] |= (uint32_t)(sc >> 3) << (8 * (j & 3));
+                    v[2 + (j >> 2)] |= (uint32_t)(sc & 7) << (8 * (j & 3));
+                }
             }
         }
     } else if (slot < kGemmMinOff / 16) {  // d, dmin of rows 2k, 2k + 1
@@ -200,9 +228,10 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
         for (int t = 0; t < 2; t++) {
             const int64_t row = blk * 32 + 2 * k + t;
             if (row < L.n_out) {
-                const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
-                v[2 * t] = __float_as_uint(half_to_float(m.x & 0xffffu));
-                v[2 * t + 1] = __float_as_uint(half_to_float(m.x >> 16));
+                const uint32_t dd = q2 ? ldp<uint32_t>(planes + block_off(L, 2, row, c * 8))
+                                       : ldp<U4>(planes + block_off(L, 1, row, c * 8)).x;
+                v[2 * t] = __float_as_uint(half_to_float(dd & 0xffffu));
+                v[2 * t + 1] = __float_as_uint(half_to_float(dd >> 16));
             }
         }
     } else {  // mins of lane L
@@ -211,10 +240,18 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
         if (row < L.n_out) {
             const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
             for (int t = 0; t < 4; t++) {
-                int sc, mn;
-                k4_scale_min(m, 4 * h + t, sc, mn);
-                const uint32_t hb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mn);
-                v[t] = hb | (hb << 16);
+                if (q2) {  // groups 8 h + 2 t and 8 h + 2 t + 1: high nibbles
+                    const uint32_t word = (h ? (t < 2 ? m.z : m.w) : (t < 2 ? m.x : m.y));
+                    const int b = 2 * (t & 1);
+                    const uint32_t m0 = (word >> (8 * b + 4)) & 15u, m1 = (word >> (8 * b + 12)) & 15u;
+                    v[t] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)m0) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)m1) << 16);
+                } else {
+                    int sc, mn;
+                    k4_scale_min(m, 4 * h + t, sc, mn);
+                    const uint32_t hb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mn);
+                    v[t] = hb | (hb << 16);
+                }
             }
         }
     }
@@ -258,7 +295,10 @@ __device__ inline uint32_t byte_pair(uint32_t lo, uint32_t hi, int j) {
 template <uint32_t FMT, int MT, int NBUF>
 __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
-    static_assert(FMT == T_Q4_K, "MFMA prefill: Q4_K");
+    static_assert(FMT == T_Q4_K || FMT == T_Q2_K, "MFMA prefill: Q4_K and Q2_K");
+    // Q4_K: two MFMAs per unit (8 sh + sl); Q2_K: sc * q <= 45 fits one
+    constexpr bool kSplit = FMT == T_Q4_K;
+    constexpr int kAccL = kSplit ? MT : 1;
     static_assert(NBUF % 2 == 0, "LDS buffers alternate with the super-block parity");
     using Geo = GemmGeo<MT>;
     constexpr int kGemmMT = MT;
@@ -291,11 +331,15 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
     // one super-block: weights w (this lane's row), activation tile in buf
     auto compute = [&](const uint8_t *buf, const GemmW &w) {
         const float d = w.dd.x, dmin = w.dd.y;
-        v16i_t acc_h[kGemmMT], acc_l[kGemmMT];
+        v16i_t acc_h[kGemmMT], acc_l[kAccL];
 #pragma unroll
         for (int i = 0; i < kGemmMT; i++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc_h[i][r] = acc_l[i][r] = 0;
+            for (int r = 0; r < 16; r++) acc_h[i][r] = 0;
+#pragma unroll
+        for (int i = 0; i < kAccL; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc_l[i][r] = 0;
         // The MFMA section runs at a raised wave priority: of the two waves
         // on a SIMD, the one issuing MFMAs wins the issue slot, and the
         // other one's scalar-core work fills the gaps (measured ~6% faster
@@ -322,15 +366,29 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
             const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
             const uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
             const uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
-            const uint32_t sh = byte_pair(w.scb.x, w.scb.y, j), sl = byte_pair(w.scb.z, w.scb.w, j);
-            const v4i_t bh = {(int)bytes_times(q0, sh), (int)bytes_times(q1, sh),
-                              (int)bytes_times(q2, sh), (int)bytes_times(q3, sh)};
-            const v4i_t bl = {(int)bytes_times(q0, sl), (int)bytes_times(q1, sl),
-                              (int)bytes_times(q2, sl), (int)bytes_times(q3, sl)};
+            if constexpr (kSplit) {
+                const uint32_t sh = byte_pair(w.scb.x, w.scb.y, j), sl = byte_pair(w.scb.z, w.scb.w, j);
+                const v4i_t bh = {(int)bytes_times(q0, sh), (int)bytes_times(q1, sh),
+                                  (int)bytes_times(q2, sh), (int)bytes_times(q3, sh)};
+                const v4i_t bl = {(int)bytes_times(q0, sl), (int)bytes_times(q1, sl),
+                                  (int)bytes_times(q2, sl), (int)bytes_times(q3, sl)};
 #pragma unroll
-            for (int i = 0; i < kGemmMT; i++) {
-                acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bh, acc_h[i], 0, 0, 0);
-                acc_l[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bl, acc_l[i], 0, 0, 0);
+                for (int i = 0; i < kGemmMT; i++) {
+                    acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bh, acc_h[i], 0, 0, 0);
+                    acc_l[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bl, acc_l[i], 0, 0, 0);
+                }
+            } else {
+                // low nibbles (q0, q1) are group 2j of the unit, high
+                // nibbles (q2, q3) group 2j + 1
+                const uint32_t s0 = j < 4 ? byte_pair(w.scb.x, w.scb.y, 2 * j)
+                                          : byte_pair(w.scb.z, w.scb.w, 2 * j - 8);
+                const uint32_t s1 = j < 4 ? byte_pair(w.scb.x, w.scb.y, 2 * j + 1)
+                                          : byte_pair(w.scb.z, w.scb.w, 2 * j - 7);
+                const v4i_t b = {(int)bytes_times(q0, s0), (int)bytes_times(q1, s0),
+                                 (int)bytes_times(q2, s1), (int)bytes_times(q3, s1)};
+#pragma unroll
+                for (int i = 0; i < kGemmMT; i++)
+                    acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], b, acc_h[i], 0, 0, 0);
             }
         }
         __builtin_amdgcn_s_setprio(0);
@@ -347,7 +405,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const float dxr = dx[32 * i + 8 * (r / 4) + 4 * h + (r % 4)];
-                const int S = 8 * acc_h[i][r] + acc_l[i][r];
+                const int S = kSplit ? 8 * acc_h[i][r] + acc_l[kSplit ? i : 0][r] : acc_h[i][r];
                 // y += dx * (d * S - dmin * T)
                 const float u = fma_f32(-dmin, T[r], d * (float)S);
                 y[i][r] = fma_f32(dxr, u, y[i][r]);

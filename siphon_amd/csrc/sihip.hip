@@ -525,7 +525,7 @@ static int64_t gemm_min_m() {
     return v > 0 ? v : 5;
 }
 
-static bool gemm_mfma_supported(uint32_t type) { return type == T_Q4_K; }
+static bool gemm_mfma_supported(uint32_t type) { return type == T_Q4_K || type == T_Q2_K; }
 
 // The weight's copy in the GEMM's order (gemm_layout_kernel), built from
 // its matvec copy on stream st.
@@ -642,13 +642,18 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
         A.part = (float *)ctx->d_gpart;
         A.cnt = ctx->d_gcnt;
     }
-    const int64_t grid = (int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S;
-    if (mt == 1)
-        hipLaunchKernelGGL((gemm_kq_kernel<T_Q4_K, 1, 4>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
-                           st, A);
-    else
-        hipLaunchKernelGGL((gemm_kq_kernel<T_Q4_K, 2, 2>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
-                           st, A);
+    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
+    if (L.type == T_Q2_K) {
+        if (mt == 1)
+            hipLaunchKernelGGL((gemm_kq_kernel<T_Q2_K, 1, 4>), grid, dim3(kGemmThreads), 0, st, A);
+        else
+            hipLaunchKernelGGL((gemm_kq_kernel<T_Q2_K, 2, 2>), grid, dim3(kGemmThreads), 0, st, A);
+    } else {
+        if (mt == 1)
+            hipLaunchKernelGGL((gemm_kq_kernel<T_Q4_K, 1, 4>), grid, dim3(kGemmThreads), 0, st, A);
+        else
+            hipLaunchKernelGGL((gemm_kq_kernel<T_Q4_K, 2, 2>), grid, dim3(kGemmThreads), 0, st, A);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
     return SIHIP_OK;

@@ -1,5 +1,5 @@
-"""GPU parity of the prefill GEMM on the matrix cores (Q4_K x Q8_K rows)
-against the oracle, to the same tolerance as the matvec:
+"""GPU parity of the prefill GEMM on the matrix cores (Q4_K and Q2_K
+weights x Q8_K rows) against the oracle, to the same tolerance as the matvec:
 |gpu - ref| <= 1e-5 * sum|terms| + 1e-6 per output."""
 import numpy as np
 import pytest
@@ -20,43 +20,60 @@ def _rows(rng, M, n_in):
     return X
 
 
+MFMA_TYPES = [sa.Q4_K, sa.Q2_K]
+
+
+def _extreme_q2k(W, n_out, n_in):
+    """Q2_K rows 0 and 1 at the largest operand: every group scale and min
+    15 and every quant 3 (sc * q = 45), one with d, dmin at their f16 maxima
+    of the test range."""
+    blk = W.reshape(n_out, n_in // 256, 84)
+    blk[:2, :, 0:16] = 0xFF
+    blk[:2, :, 16:80] = 0xFF
+    return W
+
+
+@pytest.mark.parametrize("wt", MFMA_TYPES, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("n_out,n_in,M", [
     (200, 1024, 16), (333, 2048, 64), (1000, 256, 100), (130, 4096, 130), (64, 512, 1),
     (129, 768, 65),
 ])
-def test_gemm_mfma_vs_oracle(dev, oracle, monkeypatch, n_out, n_in, M):
+def test_gemm_mfma_vs_oracle(dev, oracle, monkeypatch, wt, n_out, n_in, M):
     monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1")  # the MFMA path even for tiny M
-    rng = np.random.default_rng(n_out * 7 + n_in + M)
-    W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
+    rng = np.random.default_rng(n_out * 7 + n_in + M + wt)
+    W = synth.make_weights(wt, n_out, n_in, rng)
+    if wt == sa.Q2_K:
+        W = _extreme_q2k(W, n_out, n_in)
     X = _rows(rng, M, n_in)
-    w = dev.upload(sa.Q4_K, n_out, n_in, W)
+    w = dev.upload(wt, n_out, n_in, W)
     try:
         Y = dev.gemm(w, X)
     finally:
         w.free()
-    ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
+    ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
-                 f"mfma gemm {n_out}x{n_in} M={M}")
+                 f"mfma gemm {sa.NAMES[wt]} {n_out}x{n_in} M={M}")
 
 
+@pytest.mark.parametrize("wt", MFMA_TYPES, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("G", [1, 4, 16, 64])
-def test_gemm_mfma_every_tile_width(dev, oracle, monkeypatch, G):
+def test_gemm_mfma_every_tile_width(dev, oracle, monkeypatch, wt, G):
     """The GEMM reads the matvec layout of any tile width."""
     monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1")
     monkeypatch.setenv("SIHIP_TILE_COLS", str(G))
-    rng = np.random.default_rng(900 + G)
+    rng = np.random.default_rng(900 + G + wt)
     n_out, n_in, M = 300, 1792, 40
-    W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
+    W = synth.make_weights(wt, n_out, n_in, rng)
     X = _rows(rng, M, n_in)
-    w = dev.upload(sa.Q4_K, n_out, n_in, W)
+    w = dev.upload(wt, n_out, n_in, W)
     try:
         assert w.tile_cols == G
         Y = dev.gemm(w, X)
     finally:
         w.free()
-    ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
+    ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
-                 f"mfma gemm G={G}")
+                 f"mfma gemm {sa.NAMES[wt]} G={G}")
 
 
 def test_gemm_config3_sampled_rows(dev, oracle):
@@ -79,8 +96,29 @@ def test_gemm_config3_sampled_rows(dev, oracle):
                  "config 3 sampled rows")
 
 
+@pytest.mark.parametrize("n_out,n_in,M", [(27648, 5120, 8), (5120, 27648, 8), (5120, 5120, 512)])
+def test_gemm_q2k_config4_sampled_rows(dev, oracle, n_out, n_in, M):
+    """Config 4's Q2_K matrices at batch 8 (ffn_up, ffn_down) and the
+    attention matrix at M = 512 on the default dispatch; 96 weight rows
+    spread over every workgroup tile are checked for every activation row."""
+    rng = np.random.default_rng(n_out + n_in + M)
+    W = synth.make_weights(sa.Q2_K, n_out, n_in, rng)
+    X = rng.standard_normal((M, n_in)).astype(np.float32)
+    w = dev.upload(sa.Q2_K, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+    finally:
+        w.free()
+    rows = np.unique(np.concatenate([rng.choice(n_out, 64, replace=False),
+                                     np.arange(0, n_out, 997), [0, n_out - 1]]))
+    ref, L1 = oracle.gemm(sa.Q2_K, W[rows], len(rows), n_in, X)
+    assert_close(Y[:, rows].reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
+                 f"Q2_K {n_out}x{n_in} M={M} sampled rows")
+
+
+@pytest.mark.parametrize("wt", MFMA_TYPES, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("mt,sbk", [(1, 1), (1, 3), (1, 4), (1, 0), (2, 3), (2, 0)])
-def test_gemm_k_slices(dev, oracle, monkeypatch, mt, sbk):
+def test_gemm_k_slices(dev, oracle, monkeypatch, wt, mt, sbk):
     """K slices of the small-M GEMM (11 super-blocks: ragged last slice,
     several m tiles, a ragged last n tile): every slicing and tile height
     within tolerance of the oracle, and a repeated call gives the same bits
@@ -88,19 +126,19 @@ def test_gemm_k_slices(dev, oracle, monkeypatch, mt, sbk):
     monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1")
     monkeypatch.setenv("SIHIP_GEMM_MT", str(mt))
     monkeypatch.setenv("SIHIP_GEMM_SBK", str(sbk))
-    rng = np.random.default_rng(1100 + 10 * mt + sbk)
+    rng = np.random.default_rng(1100 + 10 * mt + sbk + 1000 * wt)
     n_out, n_in, M = 333, 2816, 70
-    W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
+    W = synth.make_weights(wt, n_out, n_in, rng)
     X = _rows(rng, M, n_in)
-    w = dev.upload(sa.Q4_K, n_out, n_in, W)
+    w = dev.upload(wt, n_out, n_in, W)
     try:
         Y = dev.gemm(w, X)
         Y2 = dev.gemm(w, X)
         Y3 = dev.gemm(w, X[:5])
     finally:
         w.free()
-    ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
-    what = f"gemm MT={mt} SBK={sbk}"
+    ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+    what = f"gemm {sa.NAMES[wt]} MT={mt} SBK={sbk}"
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
     assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
     assert_close(Y3.reshape(-1), ref[:5].reshape(-1).astype(np.float64), L1[:5].reshape(-1),
