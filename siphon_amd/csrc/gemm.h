@@ -19,7 +19,9 @@
 // 16: S[m,n] = sum_g sc_g[n] * sum_{k in g} q[n,k] * x[m,k] with 4-bit
 // scales and 2-bit quants, so the weight operand sc * q <= 45 fits int8
 // and one MFMA per 32-element unit accumulates S exactly; T takes the
-// 4-bit group mins.
+// 4-bit group mins. Q3_K (reference kernels.c:289-347) runs the same way
+// with biased operand bytes and a group-sum correction in place of the mins
+// (q3_neg_scale below).
 //
 // MFMA operand layout (gfx950, checked on the device): for the 32x32x32 i8
 // and 32x32x16 f16 forms lane l supplies row (l % 32) of A and column
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_quantize_x(const float *x, 
 // the block record.
 struct GemmW {
     uint2 u[8];
-    uint4 scb;   // Q4_K: sh_0..sh_7 (x, y), sl_0..sl_7 (z, w); Q2_K: sc_0..sc_15
+    uint4 scb;   // Q4_K: sh_0..sh_7 (x, y), sl_0..sl_7 (z, w); Q2_K: sc_0..sc_15; Q3_K: |s_g|
     float2 dd;   // d, dmin
     v8h_t bm;    // mins of groups 8h..8h+7 (this lane's half; Q4_K: unit mins twice)
 };
@@ -151,13 +153,15 @@ struct GemmW {
 //   4 x 1024 B: for q = 0..3 and lane L = 32 h + r (r = row in the block),
 //               bytes 16 L .. 16 L + 7 = half h of unit 2q of row r,
 //               bytes 16 L + 8 .. 16 L + 15 = half h of unit 2q + 1 of row r
-//               (Q2_K: its 2-bit quants widened to the same nibble order)
+//               (Q2_K: its 2-bit quants widened to the same nibble order;
+//               Q3_K: the sign-folded quants u' of q3_neg_scale)
 //   512 B:      per row, the unit scales sc_j = 8 sh_j + sl_j split in
 //               bytes: sh_0..sh_7, then sl_0..sl_7 (Q2_K: the 16 group
-//               scales, one byte each)
-//   256 B:      per row, f32 d and dmin
+//               scales, one byte each; Q3_K: |s_g|)
+//   256 B:      per row, f32 d and dmin (Q3_K: -d and 0)
 //   1024 B:     per lane L, f16 mins of units 4h..4h+3 of row r, each twice
-//               (Q2_K: of groups 8h..8h+7; the B operand of the min MFMA)
+//               (Q2_K: of groups 8h..8h+7, Q3_K: c_g; the B operand of the
+//               group-sum MFMA)
 // so a wave loads a super-block with 8 coalesced loads per lane, each unit
 // half already where the MFMA B operand wants it and no scale decoding left
 // in the loop.
@@ -168,6 +172,32 @@ constexpr int kGemmChunk = kGemmMinOff + 1024;
 
 __host__ __device__ inline int64_t gemm_layout_bytes(int64_t nblk32, int64_t nb) {
     return nblk32 * nb * kGemmChunk;
+}
+
+// Q2_K / Q3_K plane helpers: the 2-bit quant of element e (0..31) of a unit
+// record (element 16 i + 4 t + k at bits 8 k + 2 t of word i) and the
+// Q3_K high-mask bit of element e (element 4 t + k at bit 8 k + t).
+__device__ inline uint32_t two_bit_quant(uint32_t w0, uint32_t w1, int e) {
+    const int in = e & 15;
+    return ((e < 16 ? w0 : w1) >> (8 * (in & 3) + 2 * (in >> 2))) & 3u;
+}
+__device__ inline uint32_t hmask_bit(uint32_t hb, int e) { return (hb >> (8 * (e & 3) + (e >> 2))) & 1u; }
+
+// Q3_K in the GEMM copy. With s = -sc (sc = 6-bit scale - 32, so s is in
+// -31..32) and u = q + 4 (0..7), the unit operand byte is P - 128 with
+// P = |s| * u', u' = u for s >= 0 and 8 - u otherwise (P <= 248, so
+// P - 128 fits int8 and |s| * (u' - 4) = s * q). Summed over a group g:
+//   sum s q x = sum (P - 128) x + (128 - 4 |s_g|) * bsum_g,
+// so the group-sum MFMA takes c_g = 128 - 4 |s_g| (0..128, exact in f16) in
+// place of the mins, and the super-block sum is -(S + T) with d stored
+// negated.
+__device__ inline int q3_neg_scale(const uint8_t *sc12, int g) {
+    U4 m;
+    m.x = ldp<uint32_t>(sc12);
+    m.y = ldp<uint32_t>(sc12 + 4);
+    m.z = ldp<uint32_t>(sc12 + 8);
+    m.w = 0;
+    return -k3_scale(m, g);
 }
 
 // One thread per (32-row block, super-block, 16-byte slot); rows past n_out
@@ -182,13 +212,27 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
     const int slot = (int)(i % per);
     const int64_t blk = chunk / nb, c = chunk % nb;
     uint32_t v[4] = {0, 0, 0, 0};
-    const bool q2 = L.type == T_Q2_K;
+    const bool q2 = L.type == T_Q2_K, q3 = L.type == T_Q3_K;
     if (slot < kGemmScOff / 16) {  // unit halves
         const int q = slot >> 6, lane = slot & 63, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out) {
             for (int k = 0; k < 2; k++) {
-                if (q2) {
+                if (q3) {
+                    const int j = 2 * q + k;
+                    const uint8_t *src = planes + unit_off(L, 0, row, c * 8 + j);
+                    const uint32_t w0 = ldp<uint32_t>(src), w1 = ldp<uint32_t>(src + 4);
+                    const uint32_t hb = ldp<uint32_t>(planes + unit_off(L, 1, row, c * 8 + j));
+                    const uint8_t *sc12 = planes + block_off(L, 2, row, c * 8);
+                    const int s0 = q3_neg_scale(sc12, 2 * j), s1 = q3_neg_scale(sc12, 2 * j + 1);
+                    for (int b = 0; b < 8; b++) {
+                        const int el = 8 * h + b, eh = 16 + 8 * h + b;
+                        const uint32_t ul = two_bit_quant(w0, w1, el) + 4 * hmask_bit(hb, el);
+                        const uint32_t uh = two_bit_quant(w0, w1, eh) + 4 * hmask_bit(hb, eh);
+                        const uint32_t nib = (s0 >= 0 ? ul : 8 - ul) | ((s1 >= 0 ? uh : 8 - uh) << 4);
+                        v[2 * k + (b >> 2)] |= nib << (8 * (b & 3));
+                    }
+                } else if (q2) {
                     // Q2_K plane record: element 16 i + 4 t + e of the unit at
                     // bits 8 e + 2 t of word i; byte b of half h takes element
                     // 8 h + b (low nibble) and 16 + 8 h + b (high nibble)
@@ -210,11 +254,18 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
     } else if (slot < kGemmDOff / 16) {  // scale bytes of one row
         const int64_t row = blk * 32 + (slot - kGemmScOff / 16);
         if (row < L.n_out) {
-            const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
-            if (q2) {  // the 4-bit group scales sc_0..sc_15
+            if (q3) {  // |s_g| for the 16 groups
+                const uint8_t *sc12 = planes + block_off(L, 2, row, c * 8);
+                for (int g = 0; g < 16; g++) {
+                    const int sg = q3_neg_scale(sc12, g);
+                    v[g >> 2] |= (uint32_t)(sg < 0 ? -sg : sg) << (8 * (g & 3));
+                }
+            } else if (q2) {  // the 4-bit group scales sc_0..sc_15
+                const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
                 v[0] = m.x & 0x0F0F0F0Fu; v[1] = m.y & 0x0F0F0F0Fu;
                 v[2] = m.z & 0x0F0F0F0Fu; v[3] = m.w & 0x0F0F0F0Fu;
             } else {
+                const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
                 for (int j = 0; j < 8; j++) {
                     int sc, mn;
                     k4_scale_min(m, j, sc, mn);
@@ -228,16 +279,31 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
         for (int t = 0; t < 2; t++) {
             const int64_t row = blk * 32 + 2 * k + t;
             if (row < L.n_out) {
-                const uint32_t dd = q2 ? ldp<uint32_t>(planes + block_off(L, 2, row, c * 8))
-                                       : ldp<U4>(planes + block_off(L, 1, row, c * 8)).x;
-                v[2 * t] = __float_as_uint(half_to_float(dd & 0xffffu));
-                v[2 * t + 1] = __float_as_uint(half_to_float(dd >> 16));
+                if (q3) {  // -d; no mins
+                    const uint32_t dh = ldp<uint16_t>(planes + block_off(L, 3, row, c * 8));
+                    v[2 * t] = __float_as_uint(-half_to_float(dh));
+                } else {
+                    const uint32_t dd = q2 ? ldp<uint32_t>(planes + block_off(L, 2, row, c * 8))
+                                           : ldp<U4>(planes + block_off(L, 1, row, c * 8)).x;
+                    v[2 * t] = __float_as_uint(half_to_float(dd & 0xffffu));
+                    v[2 * t + 1] = __float_as_uint(half_to_float(dd >> 16));
+                }
             }
         }
     } else {  // mins of lane L
         const int lane = slot - kGemmMinOff / 16, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
-        if (row < L.n_out) {
+        if (row < L.n_out && q3) {  // c_g = 128 - 4 |s_g| of groups 8 h .. 8 h + 7
+            const uint8_t *sc12 = planes + block_off(L, 2, row, c * 8);
+            for (int t = 0; t < 4; t++) {
+                uint32_t hv[2];
+                for (int e = 0; e < 2; e++) {
+                    const int sg = q3_neg_scale(sc12, 8 * h + 2 * t + e);
+                    hv[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)(128 - 4 * (sg < 0 ? -sg : sg)));
+                }
+                v[t] = hv[0] | (hv[1] << 16);
+            }
+        } else if (row < L.n_out) {
             const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
             for (int t = 0; t < 4; t++) {
                 if (q2) {  // groups 8 h + 2 t and 8 h + 2 t + 1: high nibbles
@@ -295,9 +361,11 @@ __device__ inline uint32_t byte_pair(uint32_t lo, uint32_t hi, int j) {
 template <uint32_t FMT, int MT, int NBUF>
 __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
-    static_assert(FMT == T_Q4_K || FMT == T_Q2_K, "MFMA prefill: Q4_K and Q2_K");
-    // Q4_K: two MFMAs per unit (8 sh + sl); Q2_K: sc * q <= 45 fits one
+    static_assert(FMT == T_Q4_K || FMT == T_Q2_K || FMT == T_Q3_K, "MFMA prefill: Q4_K, Q2_K, Q3_K");
+    // Q4_K: two MFMAs per unit (8 sh + sl); Q2_K (sc * q <= 45) and Q3_K
+    // (bytes P - 128) one
     constexpr bool kSplit = FMT == T_Q4_K;
+    constexpr uint32_t kBias = FMT == T_Q3_K ? 0x80808080u : 0u;
     constexpr int kAccL = kSplit ? MT : 1;
     static_assert(NBUF % 2 == 0, "LDS buffers alternate with the super-block parity");
     using Geo = GemmGeo<MT>;
@@ -384,8 +452,8 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
                                           : byte_pair(w.scb.z, w.scb.w, 2 * j - 8);
                 const uint32_t s1 = j < 4 ? byte_pair(w.scb.x, w.scb.y, 2 * j + 1)
                                           : byte_pair(w.scb.z, w.scb.w, 2 * j - 7);
-                const v4i_t b = {(int)bytes_times(q0, s0), (int)bytes_times(q1, s0),
-                                 (int)bytes_times(q2, s1), (int)bytes_times(q3, s1)};
+                const v4i_t b = {(int)(bytes_times(q0, s0) ^ kBias), (int)(bytes_times(q1, s0) ^ kBias),
+                                 (int)(bytes_times(q2, s1) ^ kBias), (int)(bytes_times(q3, s1) ^ kBias)};
 #pragma unroll
                 for (int i = 0; i < kGemmMT; i++)
                     acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], b, acc_h[i], 0, 0, 0);
@@ -405,9 +473,16 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const float dxr = dx[32 * i + 8 * (r / 4) + 4 * h + (r % 4)];
-                const int S = kSplit ? 8 * acc_h[i][r] + acc_l[kSplit ? i : 0][r] : acc_h[i][r];
-                // y += dx * (d * S - dmin * T)
-                const float u = fma_f32(-dmin, T[r], d * (float)S);
+                float u;
+                if constexpr (FMT == T_Q3_K) {
+                    // -(S + T) in integers (T is an exact integer < 2^24),
+                    // the sign in d
+                    u = d * (float)(acc_h[i][r] + (int)T[r]);
+                } else {
+                    const int S = kSplit ? 8 * acc_h[i][r] + acc_l[kSplit ? i : 0][r] : acc_h[i][r];
+                    // y += dx * (d * S - dmin * T)
+                    u = fma_f32(-dmin, T[r], d * (float)S);
+                }
                 y[i][r] = fma_f32(dxr, u, y[i][r]);
             }
         }

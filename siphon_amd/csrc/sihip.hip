@@ -525,7 +525,9 @@ static int64_t gemm_min_m() {
     return v > 0 ? v : 5;
 }
 
-static bool gemm_mfma_supported(uint32_t type) { return type == T_Q4_K || type == T_Q2_K; }
+static bool gemm_mfma_supported(uint32_t type) {
+    return type == T_Q4_K || type == T_Q2_K || type == T_Q3_K;
+}
 
 // The weight's copy in the GEMM's order (gemm_layout_kernel), built from
 // its matvec copy on stream st.
@@ -643,7 +645,12 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
         A.cnt = ctx->d_gcnt;
     }
     const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
-    if (L.type == T_Q2_K) {
+    if (L.type == T_Q3_K) {
+        if (mt == 1)
+            hipLaunchKernelGGL((gemm_kq_kernel<T_Q3_K, 1, 4>), grid, dim3(kGemmThreads), 0, st, A);
+        else
+            hipLaunchKernelGGL((gemm_kq_kernel<T_Q3_K, 2, 2>), grid, dim3(kGemmThreads), 0, st, A);
+    } else if (L.type == T_Q2_K) {
         if (mt == 1)
             hipLaunchKernelGGL((gemm_kq_kernel<T_Q2_K, 1, 4>), grid, dim3(kGemmThreads), 0, st, A);
         else

@@ -1,4 +1,4 @@
-"""GPU parity of the prefill GEMM on the matrix cores (Q4_K and Q2_K
+"""GPU parity of the prefill GEMM on the matrix cores (Q4_K, Q2_K and Q3_K
 weights x Q8_K rows) against the oracle, to the same tolerance as the matvec:
 |gpu - ref| <= 1e-5 * sum|terms| + 1e-6 per output."""
 import numpy as np
@@ -20,7 +20,7 @@ def _rows(rng, M, n_in):
     return X
 
 
-MFMA_TYPES = [sa.Q4_K, sa.Q2_K]
+MFMA_TYPES = [sa.Q4_K, sa.Q2_K, sa.Q3_K]
 
 
 def _extreme_q2k(W, n_out, n_in):
@@ -30,6 +30,18 @@ def _extreme_q2k(W, n_out, n_in):
     blk = W.reshape(n_out, n_in // 256, 84)
     blk[:2, :, 0:16] = 0xFF
     blk[:2, :, 16:80] = 0xFF
+    return W
+
+
+def _extreme_q3k(W, n_out, n_in):
+    """Q3_K rows 0-3 at the ends of the operand range: 6-bit scales 0 and 63
+    (sc = -32 and 31) against quants -4 and 3, so that -sc * q takes -128,
+    96, 124 and -93 (the GEMM's bytes P - 128 at P = 0 and P = 248)."""
+    blk = W.reshape(n_out, n_in // 256, 110)
+    for row, (scale_byte, quant_byte) in enumerate([(0x00, 0x00), (0x00, 0xFF), (0xFF, 0x00), (0xFF, 0xFF)]):
+        if row < n_out:
+            blk[row, :, 96:108] = scale_byte
+            blk[row, :, 0:96] = quant_byte  # high-mask bits and 2-bit quants
     return W
 
 
@@ -44,6 +56,8 @@ def test_gemm_mfma_vs_oracle(dev, oracle, monkeypatch, wt, n_out, n_in, M):
     W = synth.make_weights(wt, n_out, n_in, rng)
     if wt == sa.Q2_K:
         W = _extreme_q2k(W, n_out, n_in)
+    if wt == sa.Q3_K:
+        W = _extreme_q3k(W, n_out, n_in)
     X = _rows(rng, M, n_in)
     w = dev.upload(wt, n_out, n_in, W)
     try:
@@ -96,24 +110,26 @@ def test_gemm_config3_sampled_rows(dev, oracle):
                  "config 3 sampled rows")
 
 
+@pytest.mark.parametrize("wt", [sa.Q2_K, sa.Q3_K], ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("n_out,n_in,M", [(27648, 5120, 8), (5120, 27648, 8), (5120, 5120, 512)])
-def test_gemm_q2k_config4_sampled_rows(dev, oracle, n_out, n_in, M):
-    """Config 4's Q2_K matrices at batch 8 (ffn_up, ffn_down) and the
-    attention matrix at M = 512 on the default dispatch; 96 weight rows
-    spread over every workgroup tile are checked for every activation row."""
-    rng = np.random.default_rng(n_out + n_in + M)
-    W = synth.make_weights(sa.Q2_K, n_out, n_in, rng)
+def test_gemm_config4_sampled_rows(dev, oracle, wt, n_out, n_in, M):
+    """Config 4's Q2_K and Q3_K matrices at batch 8 (ffn_up, ffn_down) and
+    the attention matrix at M = 512 on the default dispatch; about 96 weight
+    rows spread over every workgroup tile are checked for every activation
+    row."""
+    rng = np.random.default_rng(n_out + n_in + M + wt)
+    W = synth.make_weights(wt, n_out, n_in, rng)
     X = rng.standard_normal((M, n_in)).astype(np.float32)
-    w = dev.upload(sa.Q2_K, n_out, n_in, W)
+    w = dev.upload(wt, n_out, n_in, W)
     try:
         Y = dev.gemm(w, X)
     finally:
         w.free()
     rows = np.unique(np.concatenate([rng.choice(n_out, 64, replace=False),
                                      np.arange(0, n_out, 997), [0, n_out - 1]]))
-    ref, L1 = oracle.gemm(sa.Q2_K, W[rows], len(rows), n_in, X)
+    ref, L1 = oracle.gemm(wt, W[rows], len(rows), n_in, X)
     assert_close(Y[:, rows].reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
-                 f"Q2_K {n_out}x{n_in} M={M} sampled rows")
+                 f"{sa.NAMES[wt]} {n_out}x{n_in} M={M} sampled rows")
 
 
 @pytest.mark.parametrize("wt", MFMA_TYPES, ids=lambda t: sa.NAMES[t])
