@@ -76,7 +76,7 @@ int sihip_weight_upload(sihip_ctx *ctx, uint32_t ggml_type, uint64_t n_out,
                         uint64_t bytes, sihip_weight **out);
 int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w);
 /* Build now the weight's second device copy in the order of the
- * matrix-core GEMM (Q4_K, Q2_K, Q3_K; other types: no-op), which sihip_gemm
+ * matrix-core GEMM (Q4_K, Q5_K, Q2_K, Q3_K; other types: no-op), which sihip_gemm
  * otherwise builds on its first call with M >= 5. No reference
  * counterpart: it belongs to the batched prefill slot, which the reference
  * lacks (its prompt runs token by token, cmd_run.c:275-283). For loaders

@@ -141,6 +141,7 @@ struct GemmW {
     uint4 scb;   // Q4_K: sh_0..sh_7 (x, y), sl_0..sl_7 (z, w); Q2_K: sc_0..sc_15; Q3_K: |s_g|
     float2 dd;   // d, dmin
     v8h_t bm;    // mins of groups 8h..8h+7 (this lane's half; Q4_K: unit mins twice)
+    uint4 hb[2]; // Q5_K: fifth-bit words of units 0..7 (q5_bit_word)
 };
 
 // ---- GEMM weight order ---------------------------------------------------------
@@ -169,9 +170,16 @@ constexpr int kGemmScOff = 4096;
 constexpr int kGemmDOff = kGemmScOff + 512;
 constexpr int kGemmMinOff = kGemmDOff + 256;
 constexpr int kGemmChunk = kGemmMinOff + 1024;
+// Q5_K appends its fifth quant bits: per lane L, 32 bytes, one word per
+// unit (q5_bit_word)
+constexpr int kGemmBitOff = kGemmChunk;
 
-__host__ __device__ inline int64_t gemm_layout_bytes(int64_t nblk32, int64_t nb) {
-    return nblk32 * nb * kGemmChunk;
+__host__ __device__ constexpr int gemm_chunk_bytes(uint32_t type) {
+    return type == T_Q5_K ? kGemmBitOff + 2048 : kGemmChunk;
+}
+
+__host__ __device__ inline int64_t gemm_layout_bytes(int64_t nblk32, int64_t nb, uint32_t type) {
+    return nblk32 * nb * gemm_chunk_bytes(type);
 }
 
 // Q2_K / Q3_K plane helpers: the 2-bit quant of element e (0..31) of a unit
@@ -200,20 +208,43 @@ __device__ inline int q3_neg_scale(const uint8_t *sc12, int g) {
     return -k3_scale(m, g);
 }
 
+// Q5_K fifth bits of one unit for lane half h, placed for the kernel's
+// nibble words: byte b carries at bit 4 the bit of element 8h + b (low
+// nibble word q0), at bit 5 of 8h + 4 + b (q1), at bit 6 of 16 + 8h + b
+// (q2) and at bit 7 of 16 + 8h + 4 + b (q3). hb is the matvec bit record.
+__device__ inline uint32_t q5_bit_word(uint32_t hb, int h) {
+    uint32_t w = 0;
+    for (int b = 0; b < 4; b++) {
+        const uint32_t bits = hmask_bit(hb, 8 * h + b) | (hmask_bit(hb, 8 * h + 4 + b) << 1) |
+                              (hmask_bit(hb, 16 + 8 * h + b) << 2) |
+                              (hmask_bit(hb, 16 + 8 * h + 4 + b) << 3);
+        w |= bits << (8 * b + 4);
+    }
+    return w;
+}
+
 // One thread per (32-row block, super-block, 16-byte slot); rows past n_out
 // are written as zeros.
 __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_t *planes,
                                                           uint8_t *out, int64_t nblk32) {
     const int64_t nb = L.n_in / 256;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t per = kGemmChunk / 16;  // 368 slots per chunk
+    const int64_t per = gemm_chunk_bytes(L.type) / 16;  // 368 slots per chunk (Q5_K: 496)
     if (i >= nblk32 * nb * per) return;
     const int64_t chunk = i / per;
     const int slot = (int)(i % per);
     const int64_t blk = chunk / nb, c = chunk % nb;
     uint32_t v[4] = {0, 0, 0, 0};
     const bool q2 = L.type == T_Q2_K, q3 = L.type == T_Q3_K;
-    if (slot < kGemmScOff / 16) {  // unit halves
+    const int kp = L.type == T_Q5_K ? 2 : 1;  // block plane of d, dmin and the 6-bit scales
+    if (slot >= kGemmBitOff / 16) {  // Q5_K: fifth bits of lane L, units 4 p .. 4 p + 3
+        const int k = slot - kGemmBitOff / 16, lane = k >> 1, p = k & 1;
+        const int h = lane >> 5, r = lane & 31;
+        const int64_t row = blk * 32 + r;
+        if (row < L.n_out)
+            for (int t = 0; t < 4; t++)
+                v[t] = q5_bit_word(ldp<uint32_t>(planes + unit_off(L, 1, row, c * 8 + 4 * p + t)), h);
+    } else if (slot < kGemmScOff / 16) {  // unit halves
         const int q = slot >> 6, lane = slot & 63, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out) {
@@ -265,7 +296,7 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
                 v[0] = m.x & 0x0F0F0F0Fu; v[1] = m.y & 0x0F0F0F0Fu;
                 v[2] = m.z & 0x0F0F0F0Fu; v[3] = m.w & 0x0F0F0F0Fu;
             } else {
-                const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
+                const U4 m = ldp<U4>(planes + block_off(L, kp, row, c * 8));
                 for (int j = 0; j < 8; j++) {
                     int sc, mn;
                     k4_scale_min(m, j, sc, mn);
@@ -284,7 +315,7 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
                     v[2 * t] = __float_as_uint(-half_to_float(dh));
                 } else {
                     const uint32_t dd = q2 ? ldp<uint32_t>(planes + block_off(L, 2, row, c * 8))
-                                           : ldp<U4>(planes + block_off(L, 1, row, c * 8)).x;
+                                           : ldp<U4>(planes + block_off(L, kp, row, c * 8)).x;
                     v[2 * t] = __float_as_uint(half_to_float(dd & 0xffffu));
                     v[2 * t + 1] = __float_as_uint(half_to_float(dd >> 16));
                 }
@@ -304,7 +335,7 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
                 v[t] = hv[0] | (hv[1] << 16);
             }
         } else if (row < L.n_out) {
-            const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
+            const U4 m = ldp<U4>(planes + block_off(L, kp, row, c * 8));
             for (int t = 0; t < 4; t++) {
                 if (q2) {  // groups 8 h + 2 t and 8 h + 2 t + 1: high nibbles
                     const uint32_t word = (h ? (t < 2 ? m.z : m.w) : (t < 2 ? m.x : m.y));
@@ -326,8 +357,9 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
 
 // This lane's operands of super-block c from the GEMM-ordered copy (base of
 // the wave's 32-row block).
+template <uint32_t FMT>
 __device__ inline void gemm_load_w(const uint8_t *blk_base, int64_t c, int lane, GemmW &w) {
-    const uint8_t *chunk = blk_base + c * kGemmChunk;
+    const uint8_t *chunk = blk_base + c * gemm_chunk_bytes(FMT);
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const uint4 v = *reinterpret_cast<const uint4 *>(chunk + q * 1024 + 16 * lane);
@@ -337,6 +369,10 @@ __device__ inline void gemm_load_w(const uint8_t *blk_base, int64_t c, int lane,
     w.scb = *reinterpret_cast<const uint4 *>(chunk + kGemmScOff + 16 * (lane & 31));
     w.dd = *reinterpret_cast<const float2 *>(chunk + kGemmDOff + 8 * (lane & 31));
     w.bm = *reinterpret_cast<const v8h_t *>(chunk + kGemmMinOff + 16 * lane);
+    if constexpr (FMT == T_Q5_K) {
+        w.hb[0] = *reinterpret_cast<const uint4 *>(chunk + kGemmBitOff + 32 * lane);
+        w.hb[1] = *reinterpret_cast<const uint4 *>(chunk + kGemmBitOff + 32 * lane + 16);
+    }
 }
 
 // Bytewise q * f for bytes and products below 256 (no carries between
@@ -361,11 +397,13 @@ __device__ inline uint32_t byte_pair(uint32_t lo, uint32_t hi, int j) {
 template <uint32_t FMT, int MT, int NBUF>
 __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
-    static_assert(FMT == T_Q4_K || FMT == T_Q2_K || FMT == T_Q3_K, "MFMA prefill: Q4_K, Q2_K, Q3_K");
-    // Q4_K: two MFMAs per unit (8 sh + sl); Q2_K (sc * q <= 45) and Q3_K
-    // (bytes P - 128) one
-    constexpr bool kSplit = FMT == T_Q4_K;
-    constexpr uint32_t kBias = FMT == T_Q3_K ? 0x80808080u : 0u;
+    static_assert(FMT == T_Q4_K || FMT == T_Q5_K || FMT == T_Q2_K || FMT == T_Q3_K,
+                  "MFMA prefill: Q4_K, Q5_K, Q2_K, Q3_K");
+    // Q4_K and Q5_K: two MFMAs per unit (8 sh + sl); Q2_K (sc * q <= 45)
+    // and Q3_K (bytes P - 128) one. Q5_K's products sh * q, sl * q <= 217
+    // go in as bytes P - 128 too.
+    constexpr bool kSplit = FMT == T_Q4_K || FMT == T_Q5_K;
+    constexpr uint32_t kBias = (FMT == T_Q3_K || FMT == T_Q5_K) ? 0x80808080u : 0u;
     constexpr int kAccL = kSplit ? MT : 1;
     static_assert(NBUF % 2 == 0, "LDS buffers alternate with the super-block parity");
     using Geo = GemmGeo<MT>;
@@ -388,7 +426,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
     const int ln = lane & 31, h = lane >> 5;
     const int64_t m0 = (int64_t)mblk * kGemmBM;
     const int64_t n = (int64_t)nblk * kGemmBN + wave * 32 + ln;  // this lane's weight row
-    const uint8_t *wblk = A.w + (int64_t)(nblk * (kGemmBN / 32) + wave) * A.nb * kGemmChunk;
+    const uint8_t *wblk = A.w + (int64_t)(nblk * (kGemmBN / 32) + wave) * A.nb * gemm_chunk_bytes(FMT);
 
     v16f_t y[kGemmMT];
 #pragma unroll
@@ -432,14 +470,22 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
             // keep the reads of unit j + 2 ahead of the MFMAs of unit j
             __builtin_amdgcn_sched_barrier(0);
             const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
-            const uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
-            const uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
+            uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
+            uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
+            if constexpr (FMT == T_Q5_K) {  // fifth bits (q5_bit_word)
+                const uint4 hw = w.hb[j >> 2];
+                const uint32_t b = (j & 3) == 0 ? hw.x : (j & 3) == 1 ? hw.y : (j & 3) == 2 ? hw.z : hw.w;
+                q0 |= b & 0x10101010u;
+                q1 |= (b >> 1) & 0x10101010u;
+                q2 |= (b >> 2) & 0x10101010u;
+                q3 |= (b >> 3) & 0x10101010u;
+            }
             if constexpr (kSplit) {
                 const uint32_t sh = byte_pair(w.scb.x, w.scb.y, j), sl = byte_pair(w.scb.z, w.scb.w, j);
-                const v4i_t bh = {(int)bytes_times(q0, sh), (int)bytes_times(q1, sh),
-                                  (int)bytes_times(q2, sh), (int)bytes_times(q3, sh)};
-                const v4i_t bl = {(int)bytes_times(q0, sl), (int)bytes_times(q1, sl),
-                                  (int)bytes_times(q2, sl), (int)bytes_times(q3, sl)};
+                const v4i_t bh = {(int)(bytes_times(q0, sh) ^ kBias), (int)(bytes_times(q1, sh) ^ kBias),
+                                  (int)(bytes_times(q2, sh) ^ kBias), (int)(bytes_times(q3, sh) ^ kBias)};
+                const v4i_t bl = {(int)(bytes_times(q0, sl) ^ kBias), (int)(bytes_times(q1, sl) ^ kBias),
+                                  (int)(bytes_times(q2, sl) ^ kBias), (int)(bytes_times(q3, sl) ^ kBias)};
 #pragma unroll
                 for (int i = 0; i < kGemmMT; i++) {
                     acc_h[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ac[i], bh, acc_h[i], 0, 0, 0);
@@ -470,6 +516,15 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
 #pragma unroll
             for (int r = 0; r < 16; r++) tz[r] = 0.0f;
             const v16f_t T = __builtin_amdgcn_mfma_f32_32x32x16_f16(abs_, bm, tz, 0, 0, 0);
+            // Q5_K: the row's quant sum (sum of its 16 group sums, exact)
+            // for the operand bias, 9 * 128 per element over both passes
+            v16f_t X;
+            if constexpr (FMT == T_Q5_K) {
+                v8h_t ones;
+#pragma unroll
+                for (int e = 0; e < 8; e++) ones[e] = (_Float16)1.0f;
+                X = __builtin_amdgcn_mfma_f32_32x32x16_f16(abs_, ones, tz, 0, 0, 0);
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const float dxr = dx[32 * i + 8 * (r / 4) + 4 * h + (r % 4)];
@@ -479,7 +534,8 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
                     // the sign in d
                     u = d * (float)(acc_h[i][r] + (int)T[r]);
                 } else {
-                    const int S = kSplit ? 8 * acc_h[i][r] + acc_l[kSplit ? i : 0][r] : acc_h[i][r];
+                    int S = kSplit ? 8 * acc_h[i][r] + acc_l[kSplit ? i : 0][r] : acc_h[i][r];
+                    if constexpr (FMT == T_Q5_K) S += 1152 * (int)X[r];
                     // y += dx * (d * S - dmin * T)
                     u = fma_f32(-dmin, T[r], d * (float)S);
                 }
@@ -538,7 +594,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
     GemmW wb[NBUF];
     load_x(c0);
 #pragma unroll
-    for (int k = 0; k < NBUF - 1; k++) gemm_load_w(wblk, clamp(c0 + k), lane, wb[k]);
+    for (int k = 0; k < NBUF - 1; k++) gemm_load_w<FMT>(wblk, clamp(c0 + k), lane, wb[k]);
     store_x(sx[0]);
     __syncthreads();
     for (int64_t c = c0;; c += NBUF) {
@@ -546,7 +602,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
 #pragma unroll
         for (int k = 0; k < NBUF; k++) {
             const int64_t cc = c + k;
-            gemm_load_w(wblk, clamp(cc + NBUF - 1), lane, wb[(k + NBUF - 1) % NBUF]);
+            gemm_load_w<FMT>(wblk, clamp(cc + NBUF - 1), lane, wb[(k + NBUF - 1) % NBUF]);
             load_x(clamp(cc + 1));
             compute(sx[k & 1], wb[k]);
             store_x(sx[(k + 1) & 1]);

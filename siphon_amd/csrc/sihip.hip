@@ -526,7 +526,7 @@ static int64_t gemm_min_m() {
 }
 
 static bool gemm_mfma_supported(uint32_t type) {
-    return type == T_Q4_K || type == T_Q2_K || type == T_Q3_K;
+    return type == T_Q4_K || type == T_Q5_K || type == T_Q2_K || type == T_Q3_K;
 }
 
 // The weight's copy in the GEMM's order (gemm_layout_kernel), built from
@@ -535,13 +535,13 @@ static int build_gemm_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     const Layout &L = w->L;
     const int64_t nb = L.n_in / 256;
     const int64_t nblk32 = (L.n_out + kGemmBN - 1) / kGemmBN * (kGemmBN / 32);
-    const int64_t bytes = gemm_layout_bytes(nblk32, nb);
+    const int64_t bytes = gemm_layout_bytes(nblk32, nb, L.type);
     uint8_t *g = nullptr;
     hipError_t e = hipMalloc(&g, (size_t)bytes);
     if (e != hipSuccess)
         return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
                        hipGetErrorString(e));
-    const int64_t threads = nblk32 * nb * (kGemmChunk / 16);
+    const int64_t threads = nblk32 * nb * (gemm_chunk_bytes(L.type) / 16);
     hipLaunchKernelGGL(gemm_layout_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        st, L, (const uint8_t *)w->dev, g, nblk32);
     e = hipGetLastError();
@@ -580,6 +580,9 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
     // of weights in flight per wave; SIHIP_GEMM_MT (1 or 2) overrides
     int mt = M <= 128 ? 1 : 2;
     if (const char *e = getenv("SIHIP_GEMM_MT")) mt = atoi(e) == 1 ? 1 : 2;
+    // Q5_K's fifth-bit words and bias term do not fit two 32-row tiles or
+    // four super-blocks in flight in 256 VGPRs: 32-row tiles, two in flight
+    if (L.type == T_Q5_K) mt = 1;
     const int64_t BM = 32 * mt;
     const int64_t Mp = (M + BM - 1) / BM * BM;
     const int64_t ws = gemm_x_bytes(Mp, K);
@@ -645,7 +648,9 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
         A.cnt = ctx->d_gcnt;
     }
     const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
-    if (L.type == T_Q3_K) {
+    if (L.type == T_Q5_K) {
+        hipLaunchKernelGGL((gemm_kq_kernel<T_Q5_K, 1, 2>), grid, dim3(kGemmThreads), 0, st, A);
+    } else if (L.type == T_Q3_K) {
         if (mt == 1)
             hipLaunchKernelGGL((gemm_kq_kernel<T_Q3_K, 1, 4>), grid, dim3(kGemmThreads), 0, st, A);
         else

@@ -1,5 +1,5 @@
-"""GPU parity of the prefill GEMM on the matrix cores (Q4_K, Q2_K and Q3_K
-weights x Q8_K rows) against the oracle, to the same tolerance as the matvec:
+"""GPU parity of the prefill GEMM on the matrix cores (Q4_K, Q5_K, Q2_K and
+Q3_K weights x Q8_K rows) against the oracle, to the same tolerance as the matvec:
 |gpu - ref| <= 1e-5 * sum|terms| + 1e-6 per output."""
 import numpy as np
 import pytest
@@ -20,7 +20,7 @@ def _rows(rng, M, n_in):
     return X
 
 
-MFMA_TYPES = [sa.Q4_K, sa.Q2_K, sa.Q3_K]
+MFMA_TYPES = [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K]
 
 
 def _extreme_q2k(W, n_out, n_in):
@@ -45,6 +45,17 @@ def _extreme_q3k(W, n_out, n_in):
     return W
 
 
+def _extreme_q5k(W, n_out, n_in):
+    """Q5_K rows 0-1 with every 6-bit scale and min 63 (sh = sl = 7) and
+    every quant 31 or 0: operand bytes sh * q - 128 = 89 and -128."""
+    blk = W.reshape(n_out, n_in // 256, 176)
+    for row, quant_byte in enumerate([0xFF, 0x00]):
+        if row < n_out:
+            blk[row, :, 4:16] = 0xFF
+            blk[row, :, 16:176] = quant_byte  # fifth bits and nibbles
+    return W
+
+
 @pytest.mark.parametrize("wt", MFMA_TYPES, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("n_out,n_in,M", [
     (200, 1024, 16), (333, 2048, 64), (1000, 256, 100), (130, 4096, 130), (64, 512, 1),
@@ -58,6 +69,8 @@ def test_gemm_mfma_vs_oracle(dev, oracle, monkeypatch, wt, n_out, n_in, M):
         W = _extreme_q2k(W, n_out, n_in)
     if wt == sa.Q3_K:
         W = _extreme_q3k(W, n_out, n_in)
+    if wt == sa.Q5_K:
+        W = _extreme_q5k(W, n_out, n_in)
     X = _rows(rng, M, n_in)
     w = dev.upload(wt, n_out, n_in, W)
     try:
@@ -110,10 +123,10 @@ def test_gemm_config3_sampled_rows(dev, oracle):
                  "config 3 sampled rows")
 
 
-@pytest.mark.parametrize("wt", [sa.Q2_K, sa.Q3_K], ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("wt", [sa.Q2_K, sa.Q3_K, sa.Q5_K], ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("n_out,n_in,M", [(27648, 5120, 8), (5120, 27648, 8), (5120, 5120, 512)])
 def test_gemm_config4_sampled_rows(dev, oracle, wt, n_out, n_in, M):
-    """Config 4's Q2_K and Q3_K matrices at batch 8 (ffn_up, ffn_down) and
+    """Config 4's Q2_K, Q3_K and Q5_K matrices at batch 8 (ffn_up, ffn_down) and
     the attention matrix at M = 512 on the default dispatch; about 96 weight
     rows spread over every workgroup tile are checked for every activation
     row."""

@@ -138,7 +138,7 @@ def test_gemv_f32_vs_oracle(dev, oracle, wt):
         w.free()
 
 
-@pytest.mark.parametrize("wt", [sa.Q4_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.Q8_0, sa.Q5_0, sa.F16],
+@pytest.mark.parametrize("wt", [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.Q8_0, sa.Q5_0, sa.F16],
                          ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("M", [1, 3, 8, 13])
 def test_gemm_small_M_vs_oracle(dev, oracle, wt, M):
