@@ -4,7 +4,8 @@ shapes for Q2_K, Q3_K, Q5_K, Q5_0 and F16).
 
 Each matrix is checked two ways:
 - sampled rows against the oracle, batch 1 and (config 4) batch 8, to the
-  bar |gpu - ref| <= 1e-5 * sum|terms| + 1e-6;
+  bar |gpu - ref| <= 1e-5 * sum|terms| + 1e-6; for config 4 also every
+  row of two batch columns and of batch-1 calls on them;
 - every row through a property the arithmetic fixes exactly: doubling the
   activation leaves its Q8_K / Q8_0 quants unchanged and doubles the block
   scales (scaling by 2 commutes with every rounding step: the divisions
@@ -70,9 +71,14 @@ def test_full_shape(dev, oracle, label, wt, n_out, n_in, batches):
             sub = rows[:16]
             refm, l1m = oracle.gemm(wt, W[sub], len(sub), n_in, X)
             _close(Y[:, sub].reshape(-1), refm.reshape(-1), l1m.reshape(-1), f"{label} batch 8")
-            for m in (0, 7):  # each column of the batch equals a batch-1 call
-                ym = dev.gemv(w, X[m])
-                _close(Y[m], ym.astype(np.float64), np.abs(ym).astype(np.float64) + 1.0,
-                       f"{label} batch 8 column {m} vs batch 1")
+            for m in (0, 7):
+                # every row of two batch columns and of the batch-1 calls on
+                # the same activations, against the oracle (batches of the
+                # K-quants run on the matrix cores, whose f32 order differs
+                # from the matvec's, so the two GPU paths agree to the bar,
+                # not bit for bit)
+                refc, l1c = oracle.gemv(wt, W, n_out, n_in, X[m])
+                _close(Y[m], refc, l1c, f"{label} batch 8 column {m}, every row")
+                _close(dev.gemv(w, X[m]), refc, l1c, f"{label} batch 1 on column {m}, every row")
     finally:
         w.free()
