@@ -141,7 +141,7 @@ struct GemmW {
     uint4 scb;   // Q4_K: sh_0..sh_7 (x, y), sl_0..sl_7 (z, w); Q2_K: sc_0..sc_15; Q3_K: |s_g|
     float2 dd;   // d, dmin
     v8h_t bm;    // mins of groups 8h..8h+7 (this lane's half; Q4_K: unit mins twice)
-    uint4 hb[2]; // Q5_K: fifth-bit words of units 0..7 (q5_bit_word)
+    uint4 hb[2]; // Q5_K: fifth-bit words (q5_bit_word); Q2_K: quant words (q2_word) of units 0..7
 };
 
 // ---- GEMM weight order ---------------------------------------------------------
@@ -150,12 +150,12 @@ struct GemmW {
 // 32 rows one GEMM wave needs for a super-block are spread over many cache
 // lines. Prefill uses a second copy in GEMM order, built on device from the
 // matvec planes on first use: for each block of 32 rows and super-block c,
-// 5888 contiguous bytes
+// 5888 contiguous bytes (Q2_K 3840, Q5_K 7936; see gemm_quant_bytes)
 //   4 x 1024 B: for q = 0..3 and lane L = 32 h + r (r = row in the block),
 //               bytes 16 L .. 16 L + 7 = half h of unit 2q of row r,
 //               bytes 16 L + 8 .. 16 L + 15 = half h of unit 2q + 1 of row r
-//               (Q2_K: its 2-bit quants widened to the same nibble order;
-//               Q3_K: the sign-folded quants u' of q3_neg_scale)
+//               (Q3_K: the sign-folded quants u' of q3_neg_scale; Q2_K
+//               instead 2048 B, per lane L one q2_word per unit at 32 L)
 //   512 B:      per row, the unit scales sc_j = 8 sh_j + sl_j split in
 //               bytes: sh_0..sh_7, then sl_0..sl_7 (Q2_K: the 16 group
 //               scales, one byte each; Q3_K: |s_g|)
@@ -166,16 +166,17 @@ struct GemmW {
 // so a wave loads a super-block with 8 coalesced loads per lane, each unit
 // half already where the MFMA B operand wants it and no scale decoding left
 // in the loop.
-constexpr int kGemmScOff = 4096;
-constexpr int kGemmDOff = kGemmScOff + 512;
-constexpr int kGemmMinOff = kGemmDOff + 256;
-constexpr int kGemmChunk = kGemmMinOff + 1024;
-// Q5_K appends its fifth quant bits: per lane L, 32 bytes, one word per
-// unit (q5_bit_word)
-constexpr int kGemmBitOff = kGemmChunk;
-
+// Q2_K keeps 2-bit quants: per lane L, 32 bytes at 32 L, one word per unit
+// (q2_word), so its quant section is 2048 bytes and the later sections move
+// up. Q5_K appends its fifth quant bits: per lane L, 32 bytes, one word per
+// unit (q5_bit_word).
+__host__ __device__ constexpr int gemm_quant_bytes(uint32_t type) { return type == T_Q2_K ? 2048 : 4096; }
+__host__ __device__ constexpr int gemm_sc_off(uint32_t type) { return gemm_quant_bytes(type); }
+__host__ __device__ constexpr int gemm_d_off(uint32_t type) { return gemm_sc_off(type) + 512; }
+__host__ __device__ constexpr int gemm_min_off(uint32_t type) { return gemm_d_off(type) + 256; }
+__host__ __device__ constexpr int gemm_bit_off(uint32_t type) { return gemm_min_off(type) + 1024; }
 __host__ __device__ constexpr int gemm_chunk_bytes(uint32_t type) {
-    return type == T_Q5_K ? kGemmBitOff + 2048 : kGemmChunk;
+    return gemm_bit_off(type) + (type == T_Q5_K ? 2048 : 0);
 }
 
 __host__ __device__ inline int64_t gemm_layout_bytes(int64_t nblk32, int64_t nb, uint32_t type) {
@@ -208,6 +209,21 @@ __device__ inline int q3_neg_scale(const uint8_t *sc12, int g) {
     return -k3_scale(m, g);
 }
 
+// Q2_K quants of one unit for lane half h, placed for the kernel's words:
+// byte b carries at bits 0-1 element 8h + b (q0), at bits 2-3 element
+// 8h + 4 + b (q1), at bits 4-5 element 16 + 8h + b (q2) and at bits 6-7
+// element 16 + 8h + 4 + b (q3). w0, w1 are the matvec unit record.
+__device__ inline uint32_t q2_word(uint32_t w0, uint32_t w1, int h) {
+    uint32_t w = 0;
+    for (int b = 0; b < 4; b++) {
+        const uint32_t f = two_bit_quant(w0, w1, 8 * h + b) | (two_bit_quant(w0, w1, 8 * h + 4 + b) << 2) |
+                           (two_bit_quant(w0, w1, 16 + 8 * h + b) << 4) |
+                           (two_bit_quant(w0, w1, 16 + 8 * h + 4 + b) << 6);
+        w |= f << (8 * b);
+    }
+    return w;
+}
+
 // Q5_K fifth bits of one unit for lane half h, placed for the kernel's
 // nibble words: byte b carries at bit 4 the bit of element 8h + b (low
 // nibble word q0), at bit 5 of 8h + 4 + b (q1), at bit 6 of 16 + 8h + b
@@ -237,14 +253,24 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
     uint32_t v[4] = {0, 0, 0, 0};
     const bool q2 = L.type == T_Q2_K, q3 = L.type == T_Q3_K;
     const int kp = L.type == T_Q5_K ? 2 : 1;  // block plane of d, dmin and the 6-bit scales
-    if (slot >= kGemmBitOff / 16) {  // Q5_K: fifth bits of lane L, units 4 p .. 4 p + 3
-        const int k = slot - kGemmBitOff / 16, lane = k >> 1, p = k & 1;
+    const int sc_off = gemm_sc_off(L.type), d_off = gemm_d_off(L.type);
+    const int min_off = gemm_min_off(L.type), bit_off = gemm_bit_off(L.type);
+    if (slot >= bit_off / 16) {  // Q5_K: fifth bits of lane L, units 4 p .. 4 p + 3
+        const int k = slot - bit_off / 16, lane = k >> 1, p = k & 1;
         const int h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out)
             for (int t = 0; t < 4; t++)
                 v[t] = q5_bit_word(ldp<uint32_t>(planes + unit_off(L, 1, row, c * 8 + 4 * p + t)), h);
-    } else if (slot < kGemmScOff / 16) {  // unit halves
+    } else if (q2 && slot < sc_off / 16) {  // Q2_K: 2-bit words of lane L, units 4 p .. 4 p + 3
+        const int lane = slot >> 1, p = slot & 1, h = lane >> 5, r = lane & 31;
+        const int64_t row = blk * 32 + r;
+        if (row < L.n_out)
+            for (int t = 0; t < 4; t++) {
+                const uint8_t *src = planes + unit_off(L, 0, row, c * 8 + 4 * p + t);
+                v[t] = q2_word(ldp<uint32_t>(src), ldp<uint32_t>(src + 4), h);
+            }
+    } else if (slot < sc_off / 16) {  // unit halves
         const int q = slot >> 6, lane = slot & 63, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out) {
@@ -282,8 +308,8 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
                 }
             }
         }
-    } else if (slot < kGemmDOff / 16) {  // scale bytes of one row
-        const int64_t row = blk * 32 + (slot - kGemmScOff / 16);
+    } else if (slot < d_off / 16) {  // scale bytes of one row
+        const int64_t row = blk * 32 + (slot - sc_off / 16);
         if (row < L.n_out) {
             if (q3) {  // |s_g| for the 16 groups
                 const uint8_t *sc12 = planes + block_off(L, 2, row, c * 8);
@@ -305,8 +331,8 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
                 }
             }
         }
-    } else if (slot < kGemmMinOff / 16) {  // d, dmin of rows 2k, 2k + 1
-        const int k = slot - kGemmDOff / 16;
+    } else if (slot < min_off / 16) {  // d, dmin of rows 2k, 2k + 1
+        const int k = slot - d_off / 16;
         for (int t = 0; t < 2; t++) {
             const int64_t row = blk * 32 + 2 * k + t;
             if (row < L.n_out) {
@@ -322,7 +348,7 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
             }
         }
     } else {  // mins of lane L
-        const int lane = slot - kGemmMinOff / 16, h = lane >> 5, r = lane & 31;
+        const int lane = slot - min_off / 16, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out && q3) {  // c_g = 128 - 4 |s_g| of groups 8 h .. 8 h + 7
             const uint8_t *sc12 = planes + block_off(L, 2, row, c * 8);
@@ -360,18 +386,23 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
 template <uint32_t FMT>
 __device__ inline void gemm_load_w(const uint8_t *blk_base, int64_t c, int lane, GemmW &w) {
     const uint8_t *chunk = blk_base + c * gemm_chunk_bytes(FMT);
+    if constexpr (FMT == T_Q2_K) {
+        w.hb[0] = *reinterpret_cast<const uint4 *>(chunk + 32 * lane);
+        w.hb[1] = *reinterpret_cast<const uint4 *>(chunk + 32 * lane + 16);
+    } else {
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(chunk + q * 1024 + 16 * lane);
-        w.u[2 * q] = make_uint2(v.x, v.y);
-        w.u[2 * q + 1] = make_uint2(v.z, v.w);
+        for (int q = 0; q < 4; q++) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(chunk + q * 1024 + 16 * lane);
+            w.u[2 * q] = make_uint2(v.x, v.y);
+            w.u[2 * q + 1] = make_uint2(v.z, v.w);
+        }
     }
-    w.scb = *reinterpret_cast<const uint4 *>(chunk + kGemmScOff + 16 * (lane & 31));
-    w.dd = *reinterpret_cast<const float2 *>(chunk + kGemmDOff + 8 * (lane & 31));
-    w.bm = *reinterpret_cast<const v8h_t *>(chunk + kGemmMinOff + 16 * lane);
+    w.scb = *reinterpret_cast<const uint4 *>(chunk + gemm_sc_off(FMT) + 16 * (lane & 31));
+    w.dd = *reinterpret_cast<const float2 *>(chunk + gemm_d_off(FMT) + 8 * (lane & 31));
+    w.bm = *reinterpret_cast<const v8h_t *>(chunk + gemm_min_off(FMT) + 16 * lane);
     if constexpr (FMT == T_Q5_K) {
-        w.hb[0] = *reinterpret_cast<const uint4 *>(chunk + kGemmBitOff + 32 * lane);
-        w.hb[1] = *reinterpret_cast<const uint4 *>(chunk + kGemmBitOff + 32 * lane + 16);
+        w.hb[0] = *reinterpret_cast<const uint4 *>(chunk + gemm_bit_off(FMT) + 32 * lane);
+        w.hb[1] = *reinterpret_cast<const uint4 *>(chunk + gemm_bit_off(FMT) + 32 * lane + 16);
     }
 }
 
@@ -469,12 +500,22 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
             }
             // keep the reads of unit j + 2 ahead of the MFMAs of unit j
             __builtin_amdgcn_sched_barrier(0);
-            const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
-            uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
-            uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
+            const uint4 hw = w.hb[j >> 2];
+            const uint32_t b = (j & 3) == 0 ? hw.x : (j & 3) == 1 ? hw.y : (j & 3) == 2 ? hw.z : hw.w;
+            uint32_t q0, q1, q2, q3;
+            if constexpr (FMT == T_Q2_K) {  // quant words (q2_word)
+                q0 = b & 0x03030303u;
+                q1 = (b >> 2) & 0x03030303u;
+                q2 = (b >> 4) & 0x03030303u;
+                q3 = (b >> 6) & 0x03030303u;
+            } else {
+                const uint32_t w0 = w.u[j].x, w1 = w.u[j].y;
+                q0 = w0 & 0x0F0F0F0Fu;
+                q1 = w1 & 0x0F0F0F0Fu;
+                q2 = (w0 >> 4) & 0x0F0F0F0Fu;
+                q3 = (w1 >> 4) & 0x0F0F0F0Fu;
+            }
             if constexpr (FMT == T_Q5_K) {  // fifth bits (q5_bit_word)
-                const uint4 hw = w.hb[j >> 2];
-                const uint32_t b = (j & 3) == 0 ? hw.x : (j & 3) == 1 ? hw.y : (j & 3) == 2 ? hw.z : hw.w;
                 q0 |= b & 0x10101010u;
                 q1 |= (b >> 1) & 0x10101010u;
                 q2 |= (b >> 2) & 0x10101010u;
