@@ -141,7 +141,7 @@ struct GemmW {
     uint4 scb;   // Q4_K: sh_0..sh_7 (x, y), sl_0..sl_7 (z, w); Q2_K: sc_0..sc_15; Q3_K: |s_g|
     float2 dd;   // d, dmin
     v8h_t bm;    // mins of groups 8h..8h+7 (this lane's half; Q4_K: unit mins twice)
-    uint4 hb[2]; // Q5_K: fifth-bit words (q5_bit_word); Q2_K: quant words (q2_word) of units 0..7
+    uint4 hb[2]; // Q2_K: quant words (q2_word) of units 0..7; Q5_K: hb[0], fifth-bit words
 };
 
 // ---- GEMM weight order ---------------------------------------------------------
@@ -150,7 +150,7 @@ struct GemmW {
 // 32 rows one GEMM wave needs for a super-block are spread over many cache
 // lines. Prefill uses a second copy in GEMM order, built on device from the
 // matvec planes on first use: for each block of 32 rows and super-block c,
-// 5888 contiguous bytes (Q2_K 3840, Q5_K 7936; see gemm_quant_bytes)
+// 5888 contiguous bytes (Q2_K 3840, Q5_K 6912; see gemm_quant_bytes)
 //   4 x 1024 B: for q = 0..3 and lane L = 32 h + r (r = row in the block),
 //               bytes 16 L .. 16 L + 7 = half h of unit 2q of row r,
 //               bytes 16 L + 8 .. 16 L + 15 = half h of unit 2q + 1 of row r
@@ -168,15 +168,16 @@ struct GemmW {
 // in the loop.
 // Q2_K keeps 2-bit quants: per lane L, 32 bytes at 32 L, one word per unit
 // (q2_word), so its quant section is 2048 bytes and the later sections move
-// up. Q5_K appends its fifth quant bits: per lane L, 32 bytes, one word per
-// unit (q5_bit_word).
+// up. Q5_K appends its fifth quant bits: per lane L, 16 bytes at 16 L, word
+// t holding units 2t (bits 4-7 of each byte, q5_bit_word) and 2t + 1 (bits
+// 0-3).
 __host__ __device__ constexpr int gemm_quant_bytes(uint32_t type) { return type == T_Q2_K ? 2048 : 4096; }
 __host__ __device__ constexpr int gemm_sc_off(uint32_t type) { return gemm_quant_bytes(type); }
 __host__ __device__ constexpr int gemm_d_off(uint32_t type) { return gemm_sc_off(type) + 512; }
 __host__ __device__ constexpr int gemm_min_off(uint32_t type) { return gemm_d_off(type) + 256; }
 __host__ __device__ constexpr int gemm_bit_off(uint32_t type) { return gemm_min_off(type) + 1024; }
 __host__ __device__ constexpr int gemm_chunk_bytes(uint32_t type) {
-    return gemm_bit_off(type) + (type == T_Q5_K ? 2048 : 0);
+    return gemm_bit_off(type) + (type == T_Q5_K ? 1024 : 0);
 }
 
 __host__ __device__ inline int64_t gemm_layout_bytes(int64_t nblk32, int64_t nb, uint32_t type) {
@@ -255,13 +256,13 @@ __global__ __launch_bounds__(256) void gemm_layout_kernel(Layout L, const uint8_
     const int kp = L.type == T_Q5_K ? 2 : 1;  // block plane of d, dmin and the 6-bit scales
     const int sc_off = gemm_sc_off(L.type), d_off = gemm_d_off(L.type);
     const int min_off = gemm_min_off(L.type), bit_off = gemm_bit_off(L.type);
-    if (slot >= bit_off / 16) {  // Q5_K: fifth bits of lane L, units 4 p .. 4 p + 3
-        const int k = slot - bit_off / 16, lane = k >> 1, p = k & 1;
-        const int h = lane >> 5, r = lane & 31;
+    if (slot >= bit_off / 16) {  // Q5_K: fifth bits of lane L, units 2t and 2t + 1 per word
+        const int lane = slot - bit_off / 16, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
         if (row < L.n_out)
             for (int t = 0; t < 4; t++)
-                v[t] = q5_bit_word(ldp<uint32_t>(planes + unit_off(L, 1, row, c * 8 + 4 * p + t)), h);
+                v[t] = q5_bit_word(ldp<uint32_t>(planes + unit_off(L, 1, row, c * 8 + 2 * t)), h) |
+                       (q5_bit_word(ldp<uint32_t>(planes + unit_off(L, 1, row, c * 8 + 2 * t + 1)), h) >> 4);
     } else if (q2 && slot < sc_off / 16) {  // Q2_K: 2-bit words of lane L, units 4 p .. 4 p + 3
         const int lane = slot >> 1, p = slot & 1, h = lane >> 5, r = lane & 31;
         const int64_t row = blk * 32 + r;
@@ -400,10 +401,7 @@ __device__ inline void gemm_load_w(const uint8_t *blk_base, int64_t c, int lane,
     w.scb = *reinterpret_cast<const uint4 *>(chunk + gemm_sc_off(FMT) + 16 * (lane & 31));
     w.dd = *reinterpret_cast<const float2 *>(chunk + gemm_d_off(FMT) + 8 * (lane & 31));
     w.bm = *reinterpret_cast<const v8h_t *>(chunk + gemm_min_off(FMT) + 16 * lane);
-    if constexpr (FMT == T_Q5_K) {
-        w.hb[0] = *reinterpret_cast<const uint4 *>(chunk + gemm_bit_off(FMT) + 32 * lane);
-        w.hb[1] = *reinterpret_cast<const uint4 *>(chunk + gemm_bit_off(FMT) + 32 * lane + 16);
-    }
+    if constexpr (FMT == T_Q5_K) w.hb[0] = *reinterpret_cast<const uint4 *>(chunk + gemm_bit_off(FMT) + 16 * lane);
 }
 
 // Bytewise q * f for bytes and products below 256 (no carries between
@@ -500,8 +498,12 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
             }
             // keep the reads of unit j + 2 ahead of the MFMAs of unit j
             __builtin_amdgcn_sched_barrier(0);
-            const uint4 hw = w.hb[j >> 2];
-            const uint32_t b = (j & 3) == 0 ? hw.x : (j & 3) == 1 ? hw.y : (j & 3) == 2 ? hw.z : hw.w;
+            // Q2_K: word j & 3 of hb[j / 4]; Q5_K: word j / 2 of hb[0], unit
+            // j odd in its low nibbles
+            const uint4 hw = w.hb[FMT == T_Q5_K ? 0 : j >> 2];
+            const int wi = FMT == T_Q5_K ? j >> 1 : j & 3;
+            uint32_t b = wi == 0 ? hw.x : wi == 1 ? hw.y : wi == 2 ? hw.z : hw.w;
+            if (FMT == T_Q5_K && (j & 1)) b <<= 4;
             uint32_t q0, q1, q2, q3;
             if constexpr (FMT == T_Q2_K) {  // quant words (q2_word)
                 q0 = b & 0x03030303u;
