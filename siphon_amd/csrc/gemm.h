@@ -499,11 +499,14 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
             // keep the reads of unit j + 2 ahead of the MFMAs of unit j
             __builtin_amdgcn_sched_barrier(0);
             // Q2_K: word j & 3 of hb[j / 4]; Q5_K: word j / 2 of hb[0], unit
-            // j odd in its low nibbles
-            const uint4 hw = w.hb[FMT == T_Q5_K ? 0 : j >> 2];
-            const int wi = FMT == T_Q5_K ? j >> 1 : j & 3;
-            uint32_t b = wi == 0 ? hw.x : wi == 1 ? hw.y : wi == 2 ? hw.z : hw.w;
-            if (FMT == T_Q5_K && (j & 1)) b <<= 4;
+            // j odd in its low nibbles (the other formats load no hb)
+            uint32_t b = 0;
+            if constexpr (FMT == T_Q2_K || FMT == T_Q5_K) {
+                const uint4 hw = w.hb[FMT == T_Q5_K ? 0 : j >> 2];
+                const int wi = FMT == T_Q5_K ? j >> 1 : j & 3;
+                b = wi == 0 ? hw.x : wi == 1 ? hw.y : wi == 2 ? hw.z : hw.w;
+                if (FMT == T_Q5_K && (j & 1)) b <<= 4;
+            }
             uint32_t q0, q1, q2, q3;
             if constexpr (FMT == T_Q2_K) {  // quant words (q2_word)
                 q0 = b & 0x03030303u;
