@@ -518,7 +518,10 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 // Smallest M that takes the MFMA GEMM (below it the matvec kernel, which
 // streams the weights once per 1-4 columns, is cheaper: Q4_K 14336 x 4096
 // at M = 4 takes 17.5 us there against 22 us on the matrix cores, at M = 8
-// 33.7 against 22). SIHIP_GEMM_MIN_M overrides it (tests force both paths).
+// 33.7 against 22). Q5_K, Q2_K and Q3_K use the same threshold: at M = 8
+// (config 4's 32B-class shapes) their matrix-core calls take 2.0-3.9x less
+// time than the matvec kernel's. SIHIP_GEMM_MIN_M overrides it (tests force
+// both paths).
 static int64_t gemm_min_m() {
     const char *e = getenv("SIHIP_GEMM_MIN_M");
     const long v = e ? atol(e) : 0;
