@@ -11,6 +11,13 @@
  * weight tensor once, and forwards gemv calls here. Plain C types only;
  * no HIP or torch types cross this boundary (streams are opaque void*).
  *
+ * Graph capture: the *_dev entry points may be captured into a HIP graph
+ * once their workspaces exist. A call that would have to allocate during
+ * capture (a context workspace growing, a weight's GEMM copy not yet built)
+ * returns SIHIP_EINVAL instead. A workspace that grows is replaced, not
+ * freed: graphs captured earlier keep using the old buffer, which stays
+ * allocated until sihip_shutdown.
+ *
  * Conventions (mirroring the reference):
  *  - return 0 (SI_OK) or a negative SI_* code (reference
  *    include/siphon/common.h:25-34); SIHIP_EDEVICE is added for HIP
@@ -33,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SIHIP_ABI_VERSION 2
+#define SIHIP_ABI_VERSION 3
 
 /* error codes: the reference's SI_* values plus one for the device */
 #define SIHIP_OK        0
@@ -60,6 +67,13 @@ void sihip_shutdown(sihip_ctx *ctx);
 /* Message of the most recent failure on ctx ("" if none). With ctx NULL,
  * the most recent failure of sihip_init. */
 const char *sihip_last_error(const sihip_ctx *ctx);
+/* Tuning knob of a context (no reference counterpart: layout and launch
+ * choices of this backend, for tests and tuning). Each is read once from
+ * the environment variable SIHIP_<name> at sihip_init; a negative value
+ * restores the built-in rule. Names: WG_PER_CU, WAVE_TARGET, SPLIT_ELEMS,
+ * TILE_COLS (these four apply to later uploads and launches), GEMM_MIN_M,
+ * GEMM_MT, GEMM_SBK. Unknown names: SIHIP_EINVAL. */
+int sihip_set_option(sihip_ctx *ctx, const char *name, int64_t value);
 
 /* ---- weights --------------------------------------------------------- */
 
@@ -88,13 +102,13 @@ uint64_t sihip_weight_device_bytes(const sihip_weight *w);
 /* Layout introspection: row columns (256-element super-blocks for the
  * K-quants, 32-element blocks otherwise) handled side by side by one
  * wavefront, 1..64 (a power of two). Chosen at upload from the shape; the
- * environment variable SIHIP_TILE_COLS forces it (tests, tuning). */
+ * option TILE_COLS (sihip_set_option) forces it (tests, tuning). */
 int sihip_weight_tile_cols(const sihip_weight *w);
 /* Layout introspection: rounds of a wave tile (tile_cols columns each) per
  * column slice of the matvec. Rows of 8192 elements or more are cut into
  * slices of about 4096 elements computed by separate workgroups and added
  * in slice order; equal to the tile's round count when the rows are not
- * sliced. The environment variable SIHIP_SPLIT_ELEMS sets the slice length
+ * sliced. The option SPLIT_ELEMS (sihip_set_option) sets the slice length
  * in elements at upload (0: no slices). */
 int sihip_weight_slice_rounds(const sihip_weight *w);
 

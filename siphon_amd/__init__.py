@@ -25,7 +25,7 @@ NAMES = {F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_
 TYPES = {v: k for k, v in NAMES.items()}
 WEIGHT_TYPES = [Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F16]
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def row_bytes(wtype: int, n_in: int) -> int:
@@ -62,6 +62,7 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_shutdown.restype = None
     L.sihip_last_error.argtypes = [_vp]
     L.sihip_last_error.restype = ctypes.c_char_p
+    L.sihip_set_option.argtypes = [_vp, ctypes.c_char_p, _i64]
     L.sihip_weight_upload.argtypes = [_vp, _u32, _u64, _u64, _vp, _u64, ctypes.POINTER(_vp)]
     L.sihip_weight_free.argtypes = [_vp, _vp]
     L.sihip_weight_device_bytes.argtypes = [_vp]
@@ -153,6 +154,11 @@ class Device:
     def _check(self, rc: int):
         if rc != 0:
             raise SihipError(rc, self.L.sihip_last_error(self.ctx).decode())
+
+    def set_option(self, name: str, value: int):
+        """A tuning knob of this context (sihip_set_option); -1 restores the
+        built-in rule."""
+        self._check(self.L.sihip_set_option(self.ctx, name.encode(), int(value)))
 
     def close(self):
         if self.ctx:

@@ -23,12 +23,38 @@
 
 using namespace sihip;
 
+// Tuning knobs, read once from the environment at sihip_init (variable
+// SIHIP_<NAME>) and changed afterwards only through sihip_set_option; a
+// negative value means "the built-in rule".
+struct Options {
+    int64_t wg_per_cu = -1;    // matvec workgroups per CU when rows exceed waves (rule: 2)
+    int64_t wave_target = -1;  // row tiles a matvec layout aims for (rule: 800)
+    int64_t split_elems = -1;  // column-slice length in elements, 0: none (rule: kSliceElems)
+    int64_t tile_cols = -1;    // matvec tile width at upload (rule: choose_G)
+    int64_t gemm_min_m = -1;   // smallest M on the matrix cores (rule: 5)
+    int64_t gemm_mt = -1;      // GEMM m-tile rows / 32 (rule: by M)
+    int64_t gemm_sbk = -1;     // GEMM K-slice length in super-blocks, 0: none (rule: by tiles)
+};
+
+struct OptionName {
+    const char *name;
+    int64_t Options::*field;
+};
+
+static const OptionName kOptionNames[] = {
+    {"WG_PER_CU", &Options::wg_per_cu},   {"WAVE_TARGET", &Options::wave_target},
+    {"SPLIT_ELEMS", &Options::split_elems}, {"TILE_COLS", &Options::tile_cols},
+    {"GEMM_MIN_M", &Options::gemm_min_m}, {"GEMM_MT", &Options::gemm_mt},
+    {"GEMM_SBK", &Options::gemm_sbk},
+};
+
 struct sihip_ctx {
     int device;
     int n_cu;
     size_t lds_limit;
     hipStream_t stream;  // for host-pointer entry points
     char err[512];
+    Options opt;
     void *d_in = nullptr;
     size_t d_in_cap = 0;
     void *d_out = nullptr;
@@ -42,10 +68,13 @@ struct sihip_ctx {
     uint32_t *d_gcnt = nullptr;  // prefill GEMM K slices: arrival counters (zero between calls)
     void *d_attn = nullptr;  // decode attention: scores and f16 probabilities
     size_t d_attn_cap = 0;
+    // workspaces replaced by larger ones: a graph captured earlier may still
+    // hold their addresses, so they stay allocated until sihip_shutdown
+    std::vector<void *> retired;
 };
 
-// Arrival counters of K-sliced GEMM tiles, allocated (and zeroed) on the
-// first sliced call; launches with more tiles than this are not sliced.
+// Arrival counters of K-sliced GEMM tiles, allocated (and zeroed) at
+// sihip_init; launches with more tiles than this are not sliced.
 constexpr int64_t kGemmCounters = 65536;
 
 struct sihip_weight {
@@ -79,20 +108,43 @@ static int set_err(sihip_ctx *ctx, int code, const char *fmt, ...) {
             return set_err((ctx), SIHIP_EDEVICE, "%s: %s", #call, hipGetErrorString(e_)); \
     } while (0)
 
-static int ensure(sihip_ctx *ctx, void **buf, size_t *cap, size_t bytes) {
+// True if work on st is being captured into a graph (allocations and
+// synchronous calls are not allowed then).
+static bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return false;
+    return cs != hipStreamCaptureStatusNone;
+}
+
+// A context workspace of at least `bytes`. Growing it allocates a new
+// buffer and retires the old one (kept until sihip_shutdown, since a graph
+// captured before may reference it); under graph capture growing is an
+// error, as allocation is not allowed there.
+static int ensure(sihip_ctx *ctx, void **buf, size_t *cap, size_t bytes, hipStream_t st = nullptr) {
     if (*cap >= bytes) return SIHIP_OK;
-    if (*buf) HIP_OK(ctx, hipFree(*buf));
-    *buf = nullptr;
-    *cap = 0;
-    if (hipMalloc(buf, bytes) != hipSuccess) {
-        *buf = nullptr;
+    if (st && capturing(st))
+        return set_err(ctx, SIHIP_EINVAL,
+                       "workspace of %zu bytes needed during graph capture (it holds %zu): run "
+                       "the call once outside capture first",
+                       bytes, *cap);
+    void *nb = nullptr;
+    if (hipMalloc(&nb, bytes) != hipSuccess)
         return set_err(ctx, SIHIP_ENOMEM, "device allocation of %zu bytes failed", bytes);
-    }
+    if (*buf) ctx->retired.push_back(*buf);
+    *buf = nb;
     *cap = bytes;
     return SIHIP_OK;
 }
 
 extern "C" int sihip_abi_version(void) { return SIHIP_ABI_VERSION; }
+
+static void read_env_options(Options &o) {
+    char name[64];
+    for (const OptionName &n : kOptionNames) {
+        snprintf(name, sizeof name, "SIHIP_%s", n.name);
+        if (const char *e = getenv(name)) o.*(n.field) = atoll(e);
+    }
+}
 
 extern "C" int sihip_init(int device, sihip_ctx **out) {
     if (!out) return set_err(nullptr, SIHIP_EINVAL, "sihip_init: out is NULL");
@@ -106,12 +158,22 @@ extern "C" int sihip_init(int device, sihip_ctx **out) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess)
         return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: hipGetDeviceProperties failed");
+    void *cnt = nullptr;
+    if (hipMalloc(&cnt, kGemmCounters * 4) != hipSuccess)
+        return set_err(nullptr, SIHIP_ENOMEM, "sihip_init: GEMM slice counters");
+    if (hipMemset(cnt, 0, kGemmCounters * 4) != hipSuccess) {
+        (void)hipFree(cnt);
+        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: GEMM slice counters: memset failed");
+    }
     sihip_ctx *c = new sihip_ctx();
     c->device = device;
     c->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     c->lds_limit = prop.sharedMemPerBlock;
     c->err[0] = 0;
+    c->d_gcnt = (uint32_t *)cnt;
+    read_env_options(c->opt);
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipFree(cnt);
         delete c;
         return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: stream creation failed");
     }
@@ -122,15 +184,23 @@ extern "C" int sihip_init(int device, sihip_ctx **out) {
 extern "C" void sihip_shutdown(sihip_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
-    if (ctx->d_in) (void)hipFree(ctx->d_in);
-    if (ctx->d_out) (void)hipFree(ctx->d_out);
-    if (ctx->d_aux) (void)hipFree(ctx->d_aux);
-    if (ctx->d_ws) (void)hipFree(ctx->d_ws);
-    if (ctx->d_gpart) (void)hipFree(ctx->d_gpart);
-    if (ctx->d_gcnt) (void)hipFree(ctx->d_gcnt);
-    if (ctx->d_attn) (void)hipFree(ctx->d_attn);
+    (void)hipDeviceSynchronize();
+    for (void *p : {ctx->d_in, ctx->d_out, ctx->d_aux, ctx->d_ws, ctx->d_gpart,
+                    (void *)ctx->d_gcnt, ctx->d_attn})
+        if (p) (void)hipFree(p);
+    for (void *p : ctx->retired) (void)hipFree(p);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
+}
+
+extern "C" int sihip_set_option(sihip_ctx *ctx, const char *name, int64_t value) {
+    if (!ctx || !name) return set_err(ctx, SIHIP_EINVAL, "set_option: NULL argument");
+    for (const OptionName &n : kOptionNames)
+        if (!strcmp(name, n.name)) {
+            ctx->opt.*(n.field) = value < 0 ? -1 : value;
+            return SIHIP_OK;
+        }
+    return set_err(ctx, SIHIP_EINVAL, "set_option: unknown option %s", name);
 }
 
 extern "C" const char *sihip_last_error(const sihip_ctx *ctx) {
@@ -145,24 +215,13 @@ extern "C" const char *sihip_last_error(const sihip_ctx *ctx) {
 // tiles) instead of several generations that each repeat the prologue
 // (measured 2-4% faster than 4 or 8 on heads and 27648-row matrices).
 // SIHIP_WG_PER_CU overrides.
-static int wgs_per_cu() {
-    const char *e = getenv("SIHIP_WG_PER_CU");
-    const int v = e ? atoi(e) : 0;
-    return v > 0 ? v : 2;
-}
+static int wgs_per_cu(const Options &o) { return o.wg_per_cu > 0 ? (int)o.wg_per_cu : 2; }
 
-static int wave_target() {
-    const char *e = getenv("SIHIP_WAVE_TARGET");
-    const int v = e ? atoi(e) : 0;
-    return v > 0 ? v : 800;
-}
+static int64_t wave_target(const Options &o) { return o.wave_target > 0 ? o.wave_target : 800; }
 
-// Activation elements per column slice (slice_rounds in formats.h);
-// SIHIP_SPLIT_ELEMS overrides kSliceElems (0: no slices).
-static int64_t split_elems() {
-    const char *e = getenv("SIHIP_SPLIT_ELEMS");
-    return e ? atol(e) : kSliceElems;
-}
+// Activation elements per column slice (slice_rounds in formats.h); the
+// SPLIT_ELEMS option overrides kSliceElems (0: no slices).
+static int64_t split_elems(const Options &o) { return o.split_elems >= 0 ? o.split_elems : kSliceElems; }
 
 // Columns (super-blocks for K-quants, 32-element units otherwise) per wave
 // tile: the smallest power of two that keeps at least 80% of the lanes busy
@@ -179,13 +238,13 @@ static int64_t split_elems() {
 // keeps several rounds per slice (measured on rows of 14336 and 27648: 4-29%
 // faster than the widest tiles without slices), and wider only while the
 // launch would have fewer than 256 workgroups.
-static int choose_G(uint32_t type, int64_t n_out, int64_t n_in) {
+static int choose_G(const Options &o, uint32_t type, int64_t n_out, int64_t n_in) {
     const int64_t ncols = is_kquant(type) ? n_in / 256 : n_in / 32;
-    if (const char *f = getenv("SIHIP_TILE_COLS")) {
-        const int G = atoi(f);
+    if (o.tile_cols > 0) {
+        const int G = (int)o.tile_cols;
         if (G >= 1 && G <= 64 && !(G & (G - 1))) return G;
     }
-    const int64_t elems = split_elems();
+    const int64_t elems = split_elems(o);
     if (sliced_rows(n_in, elems)) {
         int G = is_kquant(type) ? 4 : 8;
         for (; G < 64; G *= 2) {
@@ -197,7 +256,7 @@ static int choose_G(uint32_t type, int64_t n_out, int64_t n_in) {
         }
         return G;
     }
-    const int64_t target = wave_target();
+    const int64_t target = wave_target(o);
     auto pick = [&](int pct) {
         int best = 1;
         int64_t best_tiles = 0;
@@ -235,9 +294,9 @@ extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out
     HIP_OK(ctx, hipSetDevice(ctx->device));
     const int64_t nunits = (int64_t)n_in / 32;
     Layout L;
-    if (!make_layout(type, (int64_t)n_out, (int64_t)n_in, choose_G(type, n_out, n_in), &L))
+    if (!make_layout(type, (int64_t)n_out, (int64_t)n_in, choose_G(ctx->opt, type, n_out, n_in), &L))
         return set_err(ctx, SIHIP_EINVAL, "weight_upload: no layout for this shape");
-    const uint32_t spr = (uint32_t)slice_rounds(L, split_elems());
+    const uint32_t spr = (uint32_t)slice_rounds(L, split_elems(ctx->opt));
     const uint32_t split = (uint32_t)((L.S + spr - 1) / spr);
     // slices: partial sums for up to kMaxCols columns, then one counter per
     // group of kWaves row tiles
@@ -441,7 +500,7 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
     const int64_t cb = col_bytes_aligned(pair, n_lds);
     // workgroups: one row tile per wave when the chip has room; otherwise
     // each matrix gets a share of the cap proportional to its bytes
-    const int64_t wg_cap = (int64_t)ctx->n_cu * wgs_per_cu();
+    const int64_t wg_cap = (int64_t)ctx->n_cu * wgs_per_cu(ctx->opt);
     // (a sliced matrix always takes one workgroup per tile group and slice)
     int64_t want[kMaxSegs], nwg[kMaxSegs], want_sum = 0, bytes_sum = 0;
     for (int i = 0; i < count; i++) {
@@ -520,13 +579,9 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 // at M = 4 takes 17.5 us there against 22 us on the matrix cores, at M = 8
 // 33.7 against 22). Q5_K, Q2_K and Q3_K use the same threshold: at M = 8
 // (config 4's 32B-class shapes) their matrix-core calls take 2.0-3.9x less
-// time than the matvec kernel's. SIHIP_GEMM_MIN_M overrides it (tests force
-// both paths).
-static int64_t gemm_min_m() {
-    const char *e = getenv("SIHIP_GEMM_MIN_M");
-    const long v = e ? atol(e) : 0;
-    return v > 0 ? v : 5;
-}
+// time than the matvec kernel's. The GEMM_MIN_M option overrides it (tests
+// force both paths).
+static int64_t gemm_min_m(const Options &o) { return o.gemm_min_m > 0 ? o.gemm_min_m : 5; }
 
 static bool gemm_mfma_supported(uint32_t type) {
     return type == T_Q4_K || type == T_Q5_K || type == T_Q2_K || type == T_Q3_K;
@@ -535,6 +590,10 @@ static bool gemm_mfma_supported(uint32_t type) {
 // The weight's copy in the GEMM's order (gemm_layout_kernel), built from
 // its matvec copy on stream st.
 static int build_gemm_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
+    if (capturing(st))
+        return set_err(ctx, SIHIP_EINVAL,
+                       "the weight's GEMM copy would be built during graph capture: call "
+                       "sihip_weight_prepare_gemm before capturing");
     const Layout &L = w->L;
     const int64_t nb = L.n_in / 256;
     const int64_t nblk32 = (L.n_out + kGemmBN - 1) / kGemmBN * (kGemmBN / 32);
@@ -567,34 +626,77 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
     return SIHIP_OK;
 }
 
-// Y[m, :] = W x[m, :] for m < M on the matrix cores. The activation planes
-// live in the context's workspace, so calls on one context must not overlap.
-static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X, int64_t ldx,
-                         int64_t M, float *Y, int64_t ldy, hipStream_t st) {
-    sihip_weight *w = const_cast<sihip_weight *>(wc);  // the GEMM copy is a cache of w
+// Shape of one matrix-core GEMM call: tile height, padded rows, workspace
+// sizes and K slices.
+struct GemmPlan {
+    int mt;            // 32-row MFMA tiles per wave along m
+    int64_t Mp;        // M rounded up to the workgroup's rows
+    int64_t ws_bytes;  // quantized activation planes
+    int S, SBK;        // K slices (S == 1: none) and super-blocks per slice
+    int64_t part_bytes;
+};
+
+static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
+    GemmPlan p;
+    const int64_t K = L.n_in, nb = K / 256;
+    const int64_t NB = (L.n_out + kGemmBN - 1) / kGemmBN;
+    // small M: 32-row m tiles (twice the workgroups) with four super-blocks
+    // of weights in flight per wave; the GEMM_MT option (1 or 2) overrides
+    p.mt = M <= 128 ? 1 : 2;
+    if (ctx->opt.gemm_mt > 0) p.mt = ctx->opt.gemm_mt == 1 ? 1 : 2;
+    // Q5_K's fifth-bit words and bias term do not fit two 32-row tiles or
+    // four super-blocks in flight in 256 VGPRs: 32-row tiles, two in flight
+    if (L.type == T_Q5_K) p.mt = 1;
+    const int64_t BM = 32 * p.mt;
+    p.Mp = (M + BM - 1) / BM * BM;
+    p.ws_bytes = gemm_x_bytes(p.Mp, K);
+    // K slices of SBK super-blocks when the output tiles alone would leave
+    // CUs idle (M <= 32 at the benchmark shapes: 112 tiles on 256 CUs):
+    // about one workgroup per CU, at least 4 super-blocks per slice. The
+    // partial sums cost a write and a read of S x M x N floats, which
+    // outweighs the extra parallelism once the tiles fill the chip
+    // (measured M = 64: 26.2 us unsliced, 32.3 us in 4 slices).
+    // The GEMM_SBK option overrides (0: no slices).
+    const int64_t tiles = (p.Mp / BM) * NB;
+    int64_t sbk = 0;
+    if (tiles < ctx->n_cu) {
+        int64_t S = (ctx->n_cu + tiles - 1) / tiles;
+        if (S > nb / 4) S = nb / 4;
+        if (S > 1) sbk = (nb + S - 1) / S;
+    }
+    if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
+    p.S = 1;
+    p.SBK = (int)nb;
+    p.part_bytes = 0;
+    if (sbk > 0 && sbk < nb && tiles <= kGemmCounters) {
+        p.S = (int)((nb + sbk - 1) / sbk);
+        p.SBK = (int)sbk;
+        p.part_bytes = (int64_t)p.S * p.Mp * NB * kGemmBN * (int64_t)sizeof(float);
+    }
+    return p;
+}
+
+// Device buffers of one GEMM call: the activation planes, and for K slices
+// the partial sums and the arrival counters (zero between calls).
+struct GemmBufs {
+    uint8_t *ws;
+    float *part;
+    uint32_t *cnt;
+};
+
+// Y[m, :] = W x[m, :] for m < M on the matrix cores, with the workspaces
+// in B (sized by plan_gemm); the weight's GEMM copy must exist.
+static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPlan &p,
+                            const GemmBufs &B, const float *X, int64_t ldx, int64_t M, float *Y,
+                            int64_t ldy, hipStream_t st) {
     const Layout &L = w->L;
     const int64_t K = L.n_in, nb = K / 256;
     const int NB = (int)((L.n_out + kGemmBN - 1) / kGemmBN);
-    if (!w->gemm) {
-        const int rc = build_gemm_copy(ctx, w, st);
-        if (rc) return rc;
-    }
-    // small M: 32-row m tiles (twice the workgroups) with four super-blocks
-    // of weights in flight per wave; SIHIP_GEMM_MT (1 or 2) overrides
-    int mt = M <= 128 ? 1 : 2;
-    if (const char *e = getenv("SIHIP_GEMM_MT")) mt = atoi(e) == 1 ? 1 : 2;
-    // Q5_K's fifth-bit words and bias term do not fit two 32-row tiles or
-    // four super-blocks in flight in 256 VGPRs: 32-row tiles, two in flight
-    if (L.type == T_Q5_K) mt = 1;
-    const int64_t BM = 32 * mt;
-    const int64_t Mp = (M + BM - 1) / BM * BM;
-    const int64_t ws = gemm_x_bytes(Mp, K);
-    int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)ws);
-    if (rc) return rc;
+    const int64_t BM = 32 * p.mt, Mp = p.Mp;
     GemmX XP;
-    XP.q = (int8_t *)ctx->d_ws;
-    XP.d = (float *)((uint8_t *)ctx->d_ws + Mp * K);
-    XP.bs = (_Float16 *)((uint8_t *)ctx->d_ws + Mp * K + nb * Mp * 4);
+    XP.q = (int8_t *)B.ws;
+    XP.d = (float *)(B.ws + Mp * K);
+    XP.bs = (_Float16 *)(B.ws + Mp * K + nb * Mp * 4);
     const int64_t blocks = Mp * nb;
     hipLaunchKernelGGL(gemm_quantize_x, dim3((unsigned)((blocks + 15) / 16)), dim3(kGemmThreads), 0,
                        st, X, ldx, M, Mp, nb, XP);
@@ -611,46 +713,12 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
     A.ldy = ldy;
     A.MB = (int)(Mp / BM);
     A.NB = NB;
-    // K slices of SBK super-blocks when the output tiles alone would leave
-    // CUs idle (M <= 32 at the benchmark shapes: 112 tiles on 256 CUs):
-    // about one workgroup per CU, at least 4 super-blocks per slice. The
-    // partial sums cost a write and a read of S x M x N floats, which
-    // outweighs the extra parallelism once the tiles fill the chip
-    // (measured M = 64: 26.2 us unsliced, 32.3 us in 4 slices).
-    // SIHIP_GEMM_SBK overrides (0: no slices).
-    const int64_t tiles = (int64_t)A.MB * NB;
-    int64_t sbk = 0;
-    if (tiles < ctx->n_cu) {
-        int64_t S = (ctx->n_cu + tiles - 1) / tiles;
-        if (S > nb / 4) S = nb / 4;
-        if (S > 1) sbk = (nb + S - 1) / S;
-    }
-    if (const char *e = getenv("SIHIP_GEMM_SBK")) sbk = atol(e);
-    A.S = 1;
-    A.SBK = (int)nb;
-    A.part = nullptr;
-    A.cnt = nullptr;
-    if (sbk > 0 && sbk < nb && (int64_t)A.MB * NB <= kGemmCounters) {
-        const int S = (int)((nb + sbk - 1) / sbk);
-        rc = ensure(ctx, &ctx->d_gpart, &ctx->d_gpart_cap,
-                    (size_t)S * Mp * NB * kGemmBN * sizeof(float));
-        if (rc) return rc;
-        if (!ctx->d_gcnt) {
-            void *p = nullptr;
-            if (hipMalloc(&p, kGemmCounters * 4) != hipSuccess)
-                return set_err(ctx, SIHIP_ENOMEM, "gemm slice counters");
-            if (hipMemset(p, 0, kGemmCounters * 4) != hipSuccess) {
-                (void)hipFree(p);
-                return set_err(ctx, SIHIP_EDEVICE, "gemm slice counters: memset failed");
-            }
-            ctx->d_gcnt = (uint32_t *)p;
-        }
-        A.S = S;
-        A.SBK = (int)sbk;
-        A.part = (float *)ctx->d_gpart;
-        A.cnt = ctx->d_gcnt;
-    }
+    A.S = p.S;
+    A.SBK = p.SBK;
+    A.part = p.S > 1 ? B.part : nullptr;
+    A.cnt = p.S > 1 ? B.cnt : nullptr;
     const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
+    const int mt = p.mt;
     if (L.type == T_Q5_K) {
         hipLaunchKernelGGL((gemm_kq_kernel<T_Q5_K, 1, 2>), grid, dim3(kGemmThreads), 0, st, A);
     } else if (L.type == T_Q3_K) {
@@ -674,12 +742,37 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
     return SIHIP_OK;
 }
 
+// The MFMA GEMM on the context's workspaces (grown as needed, outside
+// graph capture) and the weight's GEMM copy (built on first use). The
+// activation planes live in the context, so calls on one context must not
+// overlap.
+static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X, int64_t ldx,
+                         int64_t M, float *Y, int64_t ldy, hipStream_t st) {
+    sihip_weight *w = const_cast<sihip_weight *>(wc);  // the GEMM copy is a cache of w
+    if (!w->gemm) {
+        const int rc = build_gemm_copy(ctx, w, st);
+        if (rc) return rc;
+    }
+    const GemmPlan p = plan_gemm(ctx, w->L, M);
+    int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)p.ws_bytes, st);
+    if (rc) return rc;
+    if (p.S > 1) {
+        rc = ensure(ctx, &ctx->d_gpart, &ctx->d_gpart_cap, (size_t)p.part_bytes, st);
+        if (rc) return rc;
+    }
+    const GemmBufs B{(uint8_t *)ctx->d_ws, (float *)ctx->d_gpart, ctx->d_gcnt};
+    return launch_gemm_mfma(ctx, w, p, B, X, ldx, M, Y, ldy, st);
+}
+
 // Prefill dispatch: MFMA GEMM where supported and M is large enough,
 // otherwise the matvec kernel over column groups.
+static bool gemm_on_mfma(const sihip_ctx *ctx, const sihip_weight *w, int64_t M) {
+    return gemm_mfma_supported(w->L.type) && M >= gemm_min_m(ctx->opt);
+}
+
 static int run_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64_t M, float *Y,
                     hipStream_t st) {
-    if (gemm_mfma_supported(w->L.type) && M >= gemm_min_m())
-        return run_gemm_mfma(ctx, w, X, w->L.n_in, M, Y, w->L.n_out, st);
+    if (gemm_on_mfma(ctx, w, M)) return run_gemm_mfma(ctx, w, X, w->L.n_in, M, Y, w->L.n_out, st);
     return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out, st);
 }
 
@@ -791,7 +884,8 @@ extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint1
     // workspace scores (f32) and probabilities (f16): rows of whole
     // kAttnBlock blocks, so that block loads stay inside the allocation
     A.lw = (A.n + kAttnBlock - 1) / kAttnBlock * kAttnBlock;
-    const int rc = ensure(ctx, &ctx->d_attn, &ctx->d_attn_cap, (size_t)(n_head * A.lw * 6));
+    const int rc = ensure(ctx, &ctx->d_attn, &ctx->d_attn_cap, (size_t)(n_head * A.lw * 6),
+                          (hipStream_t)stream);
     if (rc) return rc;
     A.sw = (float *)ctx->d_attn;
     A.pw = (uint16_t *)((uint8_t *)ctx->d_attn + n_head * A.lw * 4);

@@ -40,3 +40,18 @@ def dev():
     d = siphon_amd.Device(0)
     yield d
     d.close()
+
+
+@pytest.fixture
+def option(dev):
+    """Set tuning options on the session device for one test: option(name,
+    value); every option set is restored to its built-in rule afterwards."""
+    touched = []
+
+    def set_(name, value):
+        dev.set_option(name, value)
+        touched.append(name)
+
+    yield set_
+    for name in touched:
+        dev.set_option(name, -1)

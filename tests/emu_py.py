@@ -25,8 +25,9 @@ class Emulator:
         self.L = L
 
     def gemv_pair(self, wtype, n_out, n_in, G, rows, xq, slice_elems=None):
-        """slice_elems: column slice length as the library reads it from
-        SIHIP_SPLIT_ELEMS at upload (None: that variable, else the default)."""
+        """slice_elems: column slice length the library applies at upload
+        (None: SIHIP_SPLIT_ELEMS, which the library reads once at
+        sihip_init, else the default)."""
         if slice_elems is None:
             slice_elems = int(os.environ.get("SIHIP_SPLIT_ELEMS", "-1"))
         rows = np.ascontiguousarray(rows, dtype=np.uint8)

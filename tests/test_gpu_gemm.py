@@ -61,8 +61,8 @@ def _extreme_q5k(W, n_out, n_in):
     (200, 1024, 16), (333, 2048, 64), (1000, 256, 100), (130, 4096, 130), (64, 512, 1),
     (129, 768, 65),
 ])
-def test_gemm_mfma_vs_oracle(dev, oracle, monkeypatch, wt, n_out, n_in, M):
-    monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1")  # the MFMA path even for tiny M
+def test_gemm_mfma_vs_oracle(dev, oracle, option, wt, n_out, n_in, M):
+    option("GEMM_MIN_M", "1")  # the MFMA path even for tiny M
     rng = np.random.default_rng(n_out * 7 + n_in + M + wt)
     W = synth.make_weights(wt, n_out, n_in, rng)
     if wt == sa.Q2_K:
@@ -84,10 +84,10 @@ def test_gemm_mfma_vs_oracle(dev, oracle, monkeypatch, wt, n_out, n_in, M):
 
 @pytest.mark.parametrize("wt", MFMA_TYPES, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("G", [1, 4, 16, 64])
-def test_gemm_mfma_every_tile_width(dev, oracle, monkeypatch, wt, G):
+def test_gemm_mfma_every_tile_width(dev, oracle, option, wt, G):
     """The GEMM reads the matvec layout of any tile width."""
-    monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1")
-    monkeypatch.setenv("SIHIP_TILE_COLS", str(G))
+    option("GEMM_MIN_M", "1")
+    option("TILE_COLS", str(G))
     rng = np.random.default_rng(900 + G + wt)
     n_out, n_in, M = 300, 1792, 40
     W = synth.make_weights(wt, n_out, n_in, rng)
@@ -147,14 +147,14 @@ def test_gemm_config4_sampled_rows(dev, oracle, wt, n_out, n_in, M):
 
 @pytest.mark.parametrize("wt", MFMA_TYPES, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("mt,sbk", [(1, 1), (1, 3), (1, 4), (1, 0), (2, 3), (2, 0)])
-def test_gemm_k_slices(dev, oracle, monkeypatch, wt, mt, sbk):
+def test_gemm_k_slices(dev, oracle, option, wt, mt, sbk):
     """K slices of the small-M GEMM (11 super-blocks: ragged last slice,
     several m tiles, a ragged last n tile): every slicing and tile height
     within tolerance of the oracle, and a repeated call gives the same bits
     (the last slice of each tile resets its arrival counter)."""
-    monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1")
-    monkeypatch.setenv("SIHIP_GEMM_MT", str(mt))
-    monkeypatch.setenv("SIHIP_GEMM_SBK", str(sbk))
+    option("GEMM_MIN_M", "1")
+    option("GEMM_MT", str(mt))
+    option("GEMM_SBK", str(sbk))
     rng = np.random.default_rng(1100 + 10 * mt + sbk + 1000 * wt)
     n_out, n_in, M = 333, 2816, 70
     W = synth.make_weights(wt, n_out, n_in, rng)

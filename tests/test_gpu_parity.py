@@ -95,7 +95,7 @@ def tile_cols_for(wt):
 
 
 @pytest.mark.parametrize("wt", sa.WEIGHT_TYPES, ids=lambda t: sa.NAMES[t])
-def test_gemv_pair_vs_emulator_and_oracle(dev, oracle, emu, wt, monkeypatch):
+def test_gemv_pair_vs_emulator_and_oracle(dev, oracle, emu, wt, option):
     rng = np.random.default_rng(wt)
     for (n_out, n_in) in shapes_for(wt):
         W = synth.make_weights(wt, n_out, n_in, rng)
@@ -108,7 +108,7 @@ def test_gemv_pair_vs_emulator_and_oracle(dev, oracle, emu, wt, monkeypatch):
         for G in tile_cols_for(wt):
             # every power-of-two tile width, also those that leave padding
             # columns in the last round of a tile
-            monkeypatch.setenv("SIHIP_TILE_COLS", str(G))
+            option("TILE_COLS", str(G))
             y = dev.gemv_pair(wt, n_out, n_in, W, xq)
             assert_close(y, ref, l1, f"{sa.NAMES[wt]} {n_out}x{n_in} G={G}")
             if wt != sa.F16:
@@ -211,7 +211,7 @@ def test_gemv_multi_matches_single_and_oracle(dev, oracle, combo):
 
 
 @pytest.mark.parametrize("wt", sa.WEIGHT_TYPES, ids=lambda t: sa.NAMES[t])
-def test_dequant_rows_bitexact(dev, oracle, monkeypatch, wt):
+def test_dequant_rows_bitexact(dev, oracle, option, wt):
     """row_to_f32 from the device copy: bit-identical to the reference
     dequantizer, for one row at a time (host pointer) and for a range of rows
     into device memory, at a narrow and a wide tile (padding included)."""
@@ -220,7 +220,7 @@ def test_dequant_rows_bitexact(dev, oracle, monkeypatch, wt):
     W = synth.make_weights(wt, n_out, n_in, rng)
     ref = np.stack([oracle.dequant(wt, W[r], n_in) for r in range(n_out)])
     for G in (1, 16):
-        monkeypatch.setenv("SIHIP_TILE_COLS", str(G))
+        option("TILE_COLS", str(G))
         w = dev.upload(wt, n_out, n_in, W)
         buf = dev.alloc(n_out * n_in * 4)
         try:

@@ -28,7 +28,7 @@ def bits(a):
 
 
 @pytest.mark.parametrize("wt", sa.WEIGHT_TYPES, ids=lambda t: sa.NAMES[t])
-def test_slices_vs_emulator_and_oracle(dev, oracle, emu, wt, monkeypatch):
+def test_slices_vs_emulator_and_oracle(dev, oracle, emu, wt, option):
     rng = np.random.default_rng(900 + wt)
     n_out, n_in = (150, 2304) if wt in KQ else (150, 1120)
     W = synth.make_weights(wt, n_out, n_in, rng)
@@ -39,9 +39,9 @@ def test_slices_vs_emulator_and_oracle(dev, oracle, emu, wt, monkeypatch):
     for r in range(n_out):
         ref[r], l1[r] = oracle.vec_dot(wt, n_in, W[r], xq)
     for G in (1, 4, 16):
-        monkeypatch.setenv("SIHIP_TILE_COLS", str(G))
+        option("TILE_COLS", str(G))
         for elems in (1, 256, 1024, 0):
-            monkeypatch.setenv("SIHIP_SPLIT_ELEMS", str(elems))
+            option("SPLIT_ELEMS", str(elems))
             what = f"{sa.NAMES[wt]} {n_out}x{n_in} G={G} slice={elems}"
             y = dev.gemv_pair(wt, n_out, n_in, W, xq)
             assert_close(y, ref, l1, what)
@@ -51,13 +51,13 @@ def test_slices_vs_emulator_and_oracle(dev, oracle, emu, wt, monkeypatch):
 
 
 @pytest.mark.parametrize("wt", [sa.Q4_K, sa.Q6_K, sa.Q8_0, sa.F16], ids=lambda t: sa.NAMES[t])
-def test_sliced_calls_repeat_bit_exact(dev, oracle, monkeypatch, wt):
+def test_sliced_calls_repeat_bit_exact(dev, oracle, option, wt):
     """Default slicing of long rows (n_in >= 8192; here 3 slices, the last
     one shorter): a sequence of calls with different activations, fewer rows
     and batched columns, each against the oracle, and the first activation
     again at the end gives the same bits."""
-    monkeypatch.setenv("SIHIP_GEMM_MIN_M", "1000")  # batches take the matvec kernel
-    monkeypatch.setenv("SIHIP_TILE_COLS", "4")  # several rounds per tile (the default is 1 here)
+    option("GEMM_MIN_M", "1000")  # batches take the matvec kernel
+    option("TILE_COLS", "4")  # several rounds per tile (the default is 1 here)
     rng = np.random.default_rng(950 + wt)
     n_out, n_in = 300, 9216
     W = synth.make_weights(wt, n_out, n_in, rng)
@@ -89,7 +89,7 @@ def test_sliced_calls_repeat_bit_exact(dev, oracle, monkeypatch, wt):
         w.free()
 
 
-def test_sliced_multi_matches_single(dev, oracle, monkeypatch):
+def test_sliced_multi_matches_single(dev, oracle, option):
     """A fused launch of sliced and unsliced matrices gives the bits of one
     launch per matrix."""
     rng = np.random.default_rng(977)
@@ -98,8 +98,8 @@ def test_sliced_multi_matches_single(dev, oracle, monkeypatch):
     Ws = [synth.make_weights(wt, n, n_in, rng) for wt, n in shapes]
     ws = []
     for (wt, n), W, (G, elems) in zip(shapes, Ws, [(8, 4096), (4, 4096), (8, 0)]):
-        monkeypatch.setenv("SIHIP_TILE_COLS", str(G))
-        monkeypatch.setenv("SIHIP_SPLIT_ELEMS", str(elems))
+        option("TILE_COLS", str(G))
+        option("SPLIT_ELEMS", str(elems))
         ws.append(dev.upload(wt, n, n_in, W))
     assert [w.slice_rounds for w in ws] == [2, 4, 4]
     bufs = []
