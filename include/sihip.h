@@ -140,6 +140,19 @@ int sihip_gemv_dev(sihip_ctx *ctx, const sihip_weight *w, const float *x,
                    float *y, int64_t n_out, void *stream);
 int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float *X,
                    int64_t M, float *Y, void *stream);
+/* sihip_gemm_dev that allocates nothing. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc). Same
+ * kernels and results as sihip_gemm_dev; the quantized activation planes,
+ * K-slice partial sums and arrival counters live in a static scratch of
+ * 16 MiB + 256 KiB per device instead of the context's workspaces. Limits:
+ * the activation planes must fit the scratch (about M * n_in <= 14.7e6;
+ * larger calls return SIHIP_ERANGE); where the K-slice partial sums do not
+ * fit as well, the call runs without K slices. The weight's GEMM copy must
+ * exist (sihip_weight_prepare_gemm), else SIHIP_EINVAL. All calls on one
+ * device share the scratch: calls that overlap on a device race. */
+int sihip_gemm_dev_noalloc(sihip_ctx *ctx, const sihip_weight *w, const float *X,
+                           int64_t M, float *Y, void *stream);
 /* Rows [row0, row0 + nrows) dequantized as sihip_dequant_row, row r at
  * out + (r - row0) * ldo (out 16-byte aligned, ldo >= n_in, a multiple of
  * 4): an embedding lookup for a host that keeps activations on the device. */

@@ -78,6 +78,7 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_attn_decode_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                         ctypes.c_float, _vp, _vp, _vp, _vp]
     L.sihip_gemm_dev.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
+    L.sihip_gemm_dev_noalloc.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
     L.sihip_gemv_multi_dev.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(_vp), _vp,
                                        ctypes.POINTER(_vp), _vp]
     for fn in ("sihip_quantize_q8_K", "sihip_quantize_q8_0", "sihip_convert_f16"):
@@ -209,6 +210,12 @@ class Device:
 
     def gemm_dev(self, w: Weight, X_ptr: int, M: int, Y_ptr: int, stream: int | None = None):
         self._check(self.L.sihip_gemm_dev(self.ctx, w.handle, X_ptr, M, Y_ptr, stream))
+
+    def gemm_dev_noalloc(self, w: Weight, X_ptr: int, M: int, Y_ptr: int,
+                         stream: int | None = None):
+        """gemm_dev on the library's static scratch: allocates nothing (the
+        weight's GEMM copy must be prepared)."""
+        self._check(self.L.sihip_gemm_dev_noalloc(self.ctx, w.handle, X_ptr, M, Y_ptr, stream))
 
     def gemv_multi_dev(self, ws, x_ptr: int, y_ptrs, stream: int | None = None):
         n = len(ws)

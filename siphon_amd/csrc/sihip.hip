@@ -71,6 +71,8 @@ struct sihip_ctx {
     // workspaces replaced by larger ones: a graph captured earlier may still
     // hold their addresses, so they stay allocated until sihip_shutdown
     std::vector<void *> retired;
+    // this device's copy of the static scratch of sihip_gemm_dev_noalloc
+    uint8_t *scratch = nullptr;
 };
 
 // Arrival counters of K-sliced GEMM tiles, allocated (and zeroed) at
@@ -125,7 +127,7 @@ static int ensure(sihip_ctx *ctx, void **buf, size_t *cap, size_t bytes, hipStre
     if (st && capturing(st))
         return set_err(ctx, SIHIP_EINVAL,
                        "workspace of %zu bytes needed during graph capture (it holds %zu): run "
-                       "the call once outside capture first",
+                       "the call once outside capture first, or use sihip_gemm_dev_noalloc",
                        bytes, *cap);
     void *nb = nullptr;
     if (hipMalloc(&nb, bytes) != hipSuccess)
@@ -135,6 +137,19 @@ static int ensure(sihip_ctx *ctx, void **buf, size_t *cap, size_t bytes, hipStre
     *cap = bytes;
     return SIHIP_OK;
 }
+
+// ---- the scratch of sihip_gemm_dev_noalloc ------------------------------------
+//
+// Device memory of fixed size that the allocation-free GEMM entry point
+// uses in place of the context's workspaces: the quantized activation
+// planes and K-slice partial sums from offset 0, and kGemmCounters arrival
+// counters in the last kNoAllocCntBytes (zero at module load; each sliced
+// launch leaves them zero again). Each device holds its own copy for the
+// life of the process. In host code `scratch` only names the symbol: its
+// device address comes from hipGetSymbolAddress at sihip_init (ctx->scratch).
+constexpr size_t kNoAllocCntBytes = (size_t)kGemmCounters * 4;
+constexpr size_t kNoAllocBytes = ((size_t)16 << 20) + kNoAllocCntBytes;  // 16 MiB + counters
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
 extern "C" int sihip_abi_version(void) { return SIHIP_ABI_VERSION; }
 
@@ -158,6 +173,11 @@ extern "C" int sihip_init(int device, sihip_ctx **out) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess)
         return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: hipGetDeviceProperties failed");
+    void *sp = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (se != hipSuccess || !sp)
+        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: scratch symbol address: %s",
+                       hipGetErrorString(se));
     void *cnt = nullptr;
     if (hipMalloc(&cnt, kGemmCounters * 4) != hipSuccess)
         return set_err(nullptr, SIHIP_ENOMEM, "sihip_init: GEMM slice counters");
@@ -165,12 +185,19 @@ extern "C" int sihip_init(int device, sihip_ctx **out) {
         (void)hipFree(cnt);
         return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: GEMM slice counters: memset failed");
     }
+    // the scratch counters start at zero (each sliced launch leaves them so)
+    if (hipMemset((uint8_t *)sp + (kNoAllocBytes - kNoAllocCntBytes), 0, kNoAllocCntBytes) !=
+        hipSuccess) {
+        (void)hipFree(cnt);
+        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: scratch counters: memset failed");
+    }
     sihip_ctx *c = new sihip_ctx();
     c->device = device;
     c->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     c->lds_limit = prop.sharedMemPerBlock;
     c->err[0] = 0;
     c->d_gcnt = (uint32_t *)cnt;
+    c->scratch = (uint8_t *)sp;
     read_env_options(c->opt);
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         (void)hipFree(cnt);
@@ -848,6 +875,44 @@ extern "C" int sihip_gemm_dev(sihip_ctx *ctx, const sihip_weight *w, const float
     if (M <= 0) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: M must be positive");
     if (!aligned16(X)) return set_err(ctx, SIHIP_EINVAL, "gemm_dev: X must be 16-byte aligned");
     return run_gemm(ctx, w, X, M, Y, (hipStream_t)stream);
+}
+
+// sihip_gemm_dev without any allocation: the MFMA path takes its workspaces
+// from this device's static scratch (kNoAllocBytes, split as described at
+// `scratch`); the matvec path (small M, other formats) uses only the
+// weight's own buffers. No hipMalloc, hipFree or allocating library call is
+// made, so the call may be captured into a graph.
+extern "C" int sihip_gemm_dev_noalloc(sihip_ctx *ctx, const sihip_weight *w, const float *X,
+                                      int64_t M, float *Y, void *stream) {
+    if (!ctx || !w || !X || !Y) return set_err(ctx, SIHIP_EINVAL, "gemm_dev_noalloc: NULL argument");
+    if (M <= 0) return set_err(ctx, SIHIP_EINVAL, "gemm_dev_noalloc: M must be positive");
+    if (!aligned16(X)) return set_err(ctx, SIHIP_EINVAL, "gemm_dev_noalloc: X must be 16-byte aligned");
+    const hipStream_t st = (hipStream_t)stream;
+    if (!gemm_on_mfma(ctx, w, M))
+        return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out, st);
+    if (!w->gemm)
+        return set_err(ctx, SIHIP_EINVAL,
+                       "gemm_dev_noalloc: the weight has no GEMM copy; call "
+                       "sihip_weight_prepare_gemm first");
+    GemmPlan p = plan_gemm(ctx, w->L, M);
+    const size_t room = kNoAllocBytes - kNoAllocCntBytes;
+    if ((size_t)p.ws_bytes > room)
+        return set_err(ctx, SIHIP_ERANGE,
+                       "gemm_dev_noalloc: M = %lld x n_in = %lld needs %lld bytes of activation "
+                       "planes; the static scratch holds %zu (M * n_in up to about %zu)",
+                       (long long)M, (long long)w->L.n_in, (long long)p.ws_bytes, room,
+                       room * 256 / 292);
+    // K-slice partial sums go after the planes; where they do not fit, the
+    // call runs without K slices (same results, fewer workgroups)
+    const size_t part_off = ((size_t)p.ws_bytes + 255) & ~(size_t)255;
+    if (p.S > 1 && part_off + (size_t)p.part_bytes > room) {
+        p.S = 1;
+        p.SBK = (int)(w->L.n_in / 256);
+        p.part_bytes = 0;
+    }
+    const GemmBufs B{ctx->scratch, (float *)(ctx->scratch + part_off),
+                     (uint32_t *)(ctx->scratch + room)};
+    return launch_gemm_mfma(ctx, w, p, B, X, w->L.n_in, M, Y, w->L.n_out, st);
 }
 
 extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint16_t *k_cache,
