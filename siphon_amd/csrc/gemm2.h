@@ -1,0 +1,379 @@
+// Prefill GEMM for Q4_K weights on v_mfma_i32_16x16x64_i8 (gfx950):
+// Y[M x n_out] = X[M x n_in] * W^T with X quantized per row to Q8_K by the
+// bit-exact quantizer (reference kernels.c:561-595), each output within
+// the tolerance of the reference dot (reference kernels.c:349-410).
+//
+// Arithmetic per super-block c, weight row n, activation row m (the
+// reference dot restated):
+//   S[m,n] = sum_j sc_j[n] * sum_{k in unit j} q[n,k] * x[m,k]    (exact int)
+//   T[m,n] = sum_g mn_{g/2}[n] * bsum_g[m]                          (exact)
+//   y[m,n] += dx[m,c] * (d[n,c] * S - dmin[n,c] * T)
+// The 6-bit unit scale is split as sc = 8 sh + sl (sh, sl in 0..7), so both
+// weight operands sh * q and sl * q fit in int8 (<= 105); two accumulators
+// H and L give S = 8 H + L exactly. The min term runs on one
+// v_mfma_f32_16x16x32_f16 whose 32 k-slots hold the 16 group sums twice,
+// against hi and lo halves of -dmin * mn * 2^E: dmin * mn has at most
+// 17 significant bits, so hi + lo (two f16) is exact and the products with
+// the group sums (at most 11 bits) are exact in f32. With d' = d * 2^E
+// (exact) the epilogue is two FMAs per output,
+//   u = d' * S + T',  yacc += dx * u,
+// and the result is yacc * 2^-E at the end. E is chosen per weight so that
+// hi stays far inside the f16 range (at most 2^15).
+//
+// Tiles. A workgroup of 4 waves computes BM = 16 * MT activation rows
+// against 128 weight rows; wave w owns weight rows 32 w .. 32 w + 31 (two
+// 16-column n tiles). Per super-block each wave decodes its weights once
+// (the split operands of 4 K-steps x 2 n tiles: 64 VGPRs) and applies them
+// to its MT m tiles one after the other, so the decode is shared by MT m
+// tiles while only one m tile's accumulators are live. The activation
+// record of the super-block (quants in MFMA operand order, group sums and
+// scales of the BM rows) is copied to LDS by DMA, double buffered.
+//
+// Operand layout of the 16x16 MFMAs (checked on the device): A lane l holds
+// row l % 16 at k = KG * (l / 16) + slot (KG = 16 for i8 x64, 8 for f16
+// x32); B lane l holds column l % 16 at the same k; result register i of
+// lane l is D[4 (l / 16) + i][l % 16]. K-step ks of a super-block covers its
+// elements 64 ks .. 64 ks + 63; lane group g takes 64 ks + 16 g + slot,
+// which is unit 2 ks + g / 2, elements 16 (g % 2) + slot of the unit.
+#pragma once
+
+#include "formats.h"
+#include "quant.h"
+#include "unit.h"
+
+namespace sihip {
+
+typedef int v4i2_t __attribute__((ext_vector_type(4)));
+typedef float v4f2_t __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h2_t __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2b_t __attribute__((ext_vector_type(2)));
+
+constexpr int kG2Threads = 256;
+constexpr int kG2BN = 128;  // weight rows per workgroup
+
+// ---- activation records ----------------------------------------------------
+//
+// One record per (m block of BM rows, super-block c), KiB aligned so it is
+// copied to LDS in whole 1 KiB DMA pieces:
+//   [0, 256 BM):        quants, fragment (mt, ks) at 1024 (4 mt + ks); its
+//                       lane l holds 16 bytes: row 16 mt + l % 16, elements
+//                       64 ks + 16 (l / 16) .. + 15 of the super-block
+//   [256 BM, 288 BM):   f16 group sums, 32 bytes per row
+//   [288 BM, 292 BM):   f32 block scale dx per row
+__host__ __device__ constexpr int g2_rec_bytes(int BM) { return (BM * 292 + 1023) / 1024 * 1024; }
+__host__ __device__ constexpr int g2_rec_bsum(int BM) { return 256 * BM; }
+__host__ __device__ constexpr int g2_rec_dx(int BM) { return 288 * BM; }
+
+// One 16-lane row per Q8_K block (row m, super-block c) of X; rows M..Mp-1
+// are zero. Grid: ceil(Mp * nb / 16) workgroups of 256.
+template <int BM>
+__global__ __launch_bounds__(kG2Threads) void gemm2_quantize_x(const float *x, int64_t ldx,
+                                                               int64_t M, int64_t Mp, int64_t nb,
+                                                               uint8_t *rec) {
+    const int lane16 = threadIdx.x & 15;
+    const int64_t blk = (int64_t)blockIdx.x * (kG2Threads / 16) + (threadIdx.x >> 4);
+    if (blk >= Mp * nb) return;  // whole 16-lane rows leave together
+    const int64_t m = blk / nb, c = blk % nb;
+    Q8KRow r;
+    if (m < M) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + m * ldx + c * 256 + lane16 * 16);
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 t = src[i];
+            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
+        r = q8k_block_row16(v, lane16);
+    } else {
+        r.q = make_uint4(0, 0, 0, 0);
+        r.gsum = 0;
+        r.d = 0.0f;
+    }
+    const int64_t mb = m / BM;
+    const int mr = (int)(m % BM);
+    uint8_t *R = rec + (mb * nb + c) * g2_rec_bytes(BM);
+    // elements 16 lane16 .. + 15: K-step lane16 / 4, lane group lane16 % 4
+    const int mt = mr >> 4, ks = lane16 >> 2, g = lane16 & 3;
+    *reinterpret_cast<uint4 *>(R + (4 * mt + ks) * 1024 + (16 * g + (mr & 15)) * 16) = r.q;
+    reinterpret_cast<_Float16 *>(R + g2_rec_bsum(BM) + mr * 32)[lane16] = (_Float16)(float)r.gsum;
+    if (lane16 == 0) reinterpret_cast<float *>(R + g2_rec_dx(BM))[mr] = r.d;
+}
+
+// ---- weight copy in the order of this kernel (Q4_K) ---------------------------
+//
+// Per block of 32 weight rows and super-block c, one chunk of 6784 bytes:
+//   [0, 4096):     quants, 4 pieces (ks) of 64 lanes x 16 bytes: lane l, rows
+//                  16 nt + l % 16 for nt = 0, 1 in bytes 8 nt .. 8 nt + 7:
+//                  the 16 nibbles of lane group l / 16 as two words w0, w1,
+//                  byte b of w0 = slot b | slot 8 + b << 4, of w1 = slot
+//                  4 + b | slot 12 + b << 4 (masks and one shift decode them)
+//   [4096, 4608):  per row, sh_0..sh_7 then sl_0..sl_7 (sc_j = 8 sh_j + sl_j)
+//   [4608, 4736):  per row, f32 d * 2^E
+//   [4736, 6784):  min operand, 2 n tiles x 64 lanes x 8 f16: lane l, row
+//                  16 nt + l % 16, groups 8 (l / 16 % 2) .. + 7: hi (l < 32)
+//                  or lo (l >= 32) half of -dmin * mn_{group / 2} * 2^E
+constexpr int kG2ChunkQ4K = 6784;
+constexpr int kG2Scl = 4096, kG2D = 4608, kG2Min = 4736;
+
+__host__ __device__ inline int64_t gemm2_layout_bytes(int64_t nblk32, int64_t nb) {
+    return nblk32 * nb * kG2ChunkQ4K;
+}
+
+// One thread per 16-byte piece of a chunk (424 per chunk); rows past n_out
+// are zero.
+__global__ __launch_bounds__(256) void gemm2_layout_q4k(Layout L, const uint8_t *planes,
+                                                        uint8_t *out, int64_t nblk32, float e2) {
+    const int64_t nb = L.n_in / 256;
+    constexpr int per = kG2ChunkQ4K / 16;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nblk32 * nb * per) return;
+    const int64_t chunk = i / per;
+    const int p = (int)(i % per);
+    const int64_t blk = chunk / nb, c = chunk % nb;
+    uint32_t v[4] = {0, 0, 0, 0};
+    if (p < kG2Scl / 16) {  // quants: K-step p / 64, lane p % 64
+        const int ks = p >> 6, l = p & 63, g = l >> 4;
+        const int h = g & 1;
+        for (int nt = 0; nt < 2; nt++) {
+            const int64_t row = blk * 32 + 16 * nt + (l & 15);
+            if (row >= L.n_out) continue;
+            const uint8_t *rec = planes + unit_off(L, 0, row, c * 8 + 2 * ks + (g >> 1));
+            auto slot = [&](int s) -> uint32_t {
+                const uint32_t byte = rec[s];
+                return h ? byte >> 4 : byte & 15u;
+            };
+            uint32_t w0 = 0, w1 = 0;
+            for (int b = 0; b < 4; b++) {
+                w0 |= (slot(b) | (slot(8 + b) << 4)) << (8 * b);
+                w1 |= (slot(4 + b) | (slot(12 + b) << 4)) << (8 * b);
+            }
+            v[2 * nt] = w0;
+            v[2 * nt + 1] = w1;
+        }
+    } else if (p < kG2D / 16) {  // split scales of one row
+        const int64_t row = blk * 32 + (p - kG2Scl / 16);
+        if (row < L.n_out) {
+            const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
+            for (int j = 0; j < 8; j++) {
+                int sc, mn;
+                k4_scale_min(m, j, sc, mn);
+                v[j >> 2] |= (uint32_t)(sc >> 3) << (8 * (j & 3));
+                v[2 + (j >> 2)] |= (uint32_t)(sc & 7) << (8 * (j & 3));
+            }
+        }
+    } else if (p < kG2Min / 16) {  // d * 2^E of rows 4 k .. 4 k + 3
+        const int k = p - kG2D / 16;
+        for (int t = 0; t < 4; t++) {
+            const int64_t row = blk * 32 + 4 * k + t;
+            if (row < L.n_out) {
+                const uint32_t dd = ldp<U4>(planes + block_off(L, 1, row, c * 8)).x;
+                v[t] = __float_as_uint(half_to_float(dd & 0xffffu) * e2);
+            }
+        }
+    } else {  // min operand of one lane
+        const int q = p - kG2Min / 16, nt = q >> 6, l = q & 63;
+        const int64_t row = blk * 32 + 16 * nt + (l & 15);
+        if (row < L.n_out) {
+            const U4 m = ldp<U4>(planes + block_off(L, 1, row, c * 8));
+            const float dmin = half_to_float(m.x >> 16);
+            const bool lo = l >= 32;
+            for (int s = 0; s < 8; s++) {
+                const int grp = 8 * ((l >> 4) & 1) + s;
+                int sc, mn;
+                k4_scale_min(m, grp >> 1, sc, mn);
+                const float val = -dmin * (float)mn * e2;  // exact: 17 significant bits
+                const _Float16 hi = (_Float16)val;
+                const _Float16 part = lo ? (_Float16)(val - (float)hi) : hi;
+                v[s >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, part) << (16 * (s & 1));
+            }
+        }
+    }
+    *reinterpret_cast<uint4 *>(out + i * 16) = make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// ---- the GEMM -----------------------------------------------------------------
+
+struct G2Args {
+    const uint8_t *w;     // weight chunks [nblk32][nb]
+    const uint8_t *x;     // activation records [MB][nb]
+    float *y;             // Y[m * ldy + n]
+    int64_t ldy;
+    int64_t n_out, M;
+    int nb, MB, NB;       // super-blocks; m blocks of BM rows; n blocks of 128 rows
+    float yscale;         // 2^-E
+};
+
+// q * f bytewise for bytes and products below 256 (no carries between
+// bytes); f2 holds the factor in both 16-bit halves.
+__device__ inline uint32_t g2_bytes_times(uint32_t q, uint32_t f2) {
+    const u16x2b_t a = __builtin_bit_cast(u16x2b_t, q);
+    const u16x2b_t b = __builtin_bit_cast(u16x2b_t, f2);
+    return __builtin_bit_cast(uint32_t, (u16x2b_t)(a * b));
+}
+
+// W: waves per SIMD the kernel is built for (2: 256 registers each, two
+// workgroups per CU; 1: 512, one workgroup per CU).
+template <int MT, int W>
+__global__ __launch_bounds__(kG2Threads)
+__attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
+    constexpr int BM = 16 * MT;
+    constexpr int kRec = g2_rec_bytes(BM);
+    constexpr int kPieces = kRec / 1024;
+    __shared__ __attribute__((aligned(16))) uint8_t sx[2][kRec];
+    // XCD-aware order: workgroups go round-robin over the 8 XCDs, so the m
+    // blocks of one n block (which read the same weights) are consecutive
+    // workgroups of one XCD and share its L2
+    const int b = blockIdx.x;
+    const int xcd = b & 7, t = b >> 3;
+    const int nblk = (t / A.MB) * 8 + xcd, mblk = t % A.MB;
+    if (nblk >= A.NB) return;
+    // wave index as a scalar: the buffer resources below derive from it
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, r16 = lane & 15;
+    // buffer resources over this wave's weight chunks and this block's
+    // activation records: per-lane offsets are constants, the super-block
+    // moves the scalar offset, so no address arithmetic runs on the VALU
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(A.w + (int64_t)(nblk * 4 + wave) * A.nb * kG2ChunkQ4K), (short)0,
+        A.nb * kG2ChunkQ4K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(A.x + (int64_t)mblk * A.nb * kRec), (short)0, A.nb * kRec, 0x00020000);
+    const int v_nib = lane * 16, v_scl = kG2Scl + r16 * 16, v_d = kG2D + r16 * 4;
+    const int v_min = kG2Min + lane * 16;
+
+    // this wave's share of the 1 KiB pieces of a record
+    auto dma = [&](int c, int buf) {
+#pragma unroll
+        for (int k = 0; k < (kPieces + 3) / 4; k++) {
+            const int i = wave + 4 * k;
+            if (i < kPieces)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    xr, (__attribute__((address_space(3))) void *)(&sx[buf][i * 1024]), 16, v_nib,
+                    c * kRec + i * 1024, 0, 0);
+        }
+    };
+    struct Raw {
+        uint4 nib[4];  // K-step ks: nt 0 in x, y; nt 1 in z, w
+        uint4 scl[2];
+        float d[2];
+        uint4 mn[2];
+    };
+    auto ld4 = [&](int voff, int soff, int imm) {
+        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff + imm, soff, 0));
+    };
+    auto load_w = [&](int c, Raw &r) {
+        const int so = c * kG2ChunkQ4K;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) r.nib[ks] = ld4(v_nib, so, ks * 1024);
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            r.scl[nt] = ld4(v_scl, so, nt * 256);
+            r.d[nt] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, v_d + nt * 64, so, 0));
+            r.mn[nt] = ld4(v_min, so, nt * 1024);
+        }
+    };
+    // byte selector of this lane's unit (2 ks + g / 2) in both 16-bit halves
+    uint32_t sel[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const uint32_t u = (uint32_t)(2 * ks + (g >> 1));
+        sel[ks] = u | (0x0cu << 8) | (u << 16) | (0x0cu << 24);
+    }
+
+    v4f2_t y[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) y[mt][nt] = (v4f2_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+    Raw raw;
+    dma(0, 0);
+    load_w(0, raw);
+    for (int c = 0; c < A.nb; c++) {
+        const int buf = c & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // decode this super-block's operands
+        v4i2_t bh[4][2], bl[4][2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                const uint32_t w0 = nt ? raw.nib[ks].z : raw.nib[ks].x;
+                const uint32_t w1 = nt ? raw.nib[ks].w : raw.nib[ks].y;
+                const uint32_t q0 = w0 & 0x0F0F0F0Fu, q1 = w1 & 0x0F0F0F0Fu;
+                const uint32_t q2 = (w0 >> 4) & 0x0F0F0F0Fu, q3 = (w1 >> 4) & 0x0F0F0F0Fu;
+                const uint32_t sh = __builtin_amdgcn_perm(raw.scl[nt].y, raw.scl[nt].x, sel[ks]);
+                const uint32_t sl = __builtin_amdgcn_perm(raw.scl[nt].w, raw.scl[nt].z, sel[ks]);
+                bh[ks][nt] = (v4i2_t){(int)g2_bytes_times(q0, sh), (int)g2_bytes_times(q1, sh),
+                                      (int)g2_bytes_times(q2, sh), (int)g2_bytes_times(q3, sh)};
+                bl[ks][nt] = (v4i2_t){(int)g2_bytes_times(q0, sl), (int)g2_bytes_times(q1, sl),
+                                      (int)g2_bytes_times(q2, sl), (int)g2_bytes_times(q3, sl)};
+            }
+        const float dw[2] = {raw.d[0], raw.d[1]};
+        const v8h2_t bm[2] = {__builtin_bit_cast(v8h2_t, raw.mn[0]), __builtin_bit_cast(v8h2_t, raw.mn[1])};
+        // the next super-block's record and weights, a whole super-block
+        // ahead; unconditional (the last super-block loads itself again), so
+        // the registers of the prefetch are the ones decoded next
+        const int cn = c + 1 < A.nb ? c + 1 : c;
+        dma(cn, buf ^ 1);
+        load_w(cn, raw);
+        const uint8_t *X = sx[buf];
+        // quants of m tile mt + 1 are read while mt computes (ping-pong by
+        // the parity of the unrolled tile index); group sums and scales at
+        // the start of their own tile, in time for its epilogue
+        v4i2_t a[2][4];
+        auto lds_q = [&](int mt, v4i2_t (&aa)[4]) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+                aa[ks] = *reinterpret_cast<const v4i2_t *>(X + (4 * mt + ks) * 1024 + lane * 16);
+        };
+        lds_q(0, a[0]);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            if (mt + 1 < MT) lds_q(mt + 1, a[(mt + 1) & 1]);
+            const v8h2_t bs = *reinterpret_cast<const v8h2_t *>(X + g2_rec_bsum(BM) + (16 * mt + r16) * 32 + (g & 1) * 16);
+            const float4 dx = *reinterpret_cast<const float4 *>(X + g2_rec_dx(BM) + (16 * mt + 4 * g) * 4);
+            const v4i2_t(&am)[4] = a[mt & 1];
+            const v4f2_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+            const v4f2_t t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bs, bm[0], z, 0, 0, 0);
+            const v4f2_t t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bs, bm[1], z, 0, 0, 0);
+            v4i2_t h0 = {0, 0, 0, 0}, h1 = {0, 0, 0, 0}, l0 = {0, 0, 0, 0}, l1 = {0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                h0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], bh[ks][0], h0, 0, 0, 0);
+                l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], bl[ks][0], l0, 0, 0, 0);
+                h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], bh[ks][1], h1, 0, 0, 0);
+                l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], bl[ks][1], l1, 0, 0, 0);
+            }
+            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float u0 = fma_f32(dw[0], (float)(8 * h0[i] + l0[i]), t0[i]);
+                const float u1 = fma_f32(dw[1], (float)(8 * h1[i] + l1[i]), t1[i]);
+                y[mt][0][i] = fma_f32(dxv[i], u0, y[mt][0][i]);
+                y[mt][1][i] = fma_f32(dxv[i], u1, y[mt][1][i]);
+            }
+        }
+    }
+    // result register i of lane l: row 4 (l / 16) + i of the m tile,
+    // column l % 16 of the n tile; whole tiles inside M and n_out store
+    // without per-element tests
+    const int64_t n0 = (int64_t)nblk * kG2BN + 32 * wave;
+    const int64_t m0 = (int64_t)mblk * BM;
+    const bool full = n0 + 32 <= A.n_out && m0 + BM <= A.M;
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        const int64_t n = n0 + 16 * nt + r16;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t m = m0 + 16 * mt + 4 * g + i;
+                if (full || (m < A.M && n < A.n_out)) A.y[m * A.ldy + n] = y[mt][nt][i] * A.yscale;
+            }
+    }
+}
+
+}  // namespace sihip

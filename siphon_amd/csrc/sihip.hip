@@ -11,6 +11,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <cmath>
 #include <utility>
 #include <vector>
 
@@ -18,6 +19,7 @@
 #include "attn.h"
 #include "formats.h"
 #include "gemm.h"
+#include "gemm2.h"
 #include "matvec.h"
 #include "quant.h"
 
@@ -34,6 +36,8 @@ struct Options {
     int64_t gemm_min_m = -1;   // smallest M on the matrix cores (rule: 5)
     int64_t gemm_mt = -1;      // GEMM m-tile rows / 32 (rule: by M)
     int64_t gemm_sbk = -1;     // GEMM K-slice length in super-blocks, 0: none (rule: by tiles)
+    int64_t gemm2_min_m = -1;  // smallest M on the 16x16 Q4_K GEMM (rule: kGemm2MinM)
+    int64_t gemm2_waves = -1;  // waves per SIMD of the 16x16 Q4_K GEMM, 1 or 2 (rule: 2)
 };
 
 struct OptionName {
@@ -45,7 +49,8 @@ static const OptionName kOptionNames[] = {
     {"WG_PER_CU", &Options::wg_per_cu},   {"WAVE_TARGET", &Options::wave_target},
     {"SPLIT_ELEMS", &Options::split_elems}, {"TILE_COLS", &Options::tile_cols},
     {"GEMM_MIN_M", &Options::gemm_min_m}, {"GEMM_MT", &Options::gemm_mt},
-    {"GEMM_SBK", &Options::gemm_sbk},
+    {"GEMM_SBK", &Options::gemm_sbk},     {"GEMM2_MIN_M", &Options::gemm2_min_m},
+    {"GEMM2_WAVES", &Options::gemm2_waves},
 };
 
 struct sihip_ctx {
@@ -84,6 +89,11 @@ struct sihip_weight {
     uint8_t *dev;
     uint8_t *gemm = nullptr;  // GEMM-ordered copy, built on the first prefill call
     int64_t gemm_bytes = 0;
+    // Q4_K: the copy of the 16x16 matrix-core GEMM (gemm2.h) and its
+    // exponent E (the min operand holds -dmin * mn * 2^E)
+    uint8_t *gemm2 = nullptr;
+    int64_t gemm2_bytes = 0;
+    int gexp = 0;
     // column slices of the matvec (split == 1: whole rows per workgroup);
     // part and cnt live in the same allocation as the planes
     uint32_t split = 1, spr = 0;
@@ -301,6 +311,22 @@ static int choose_G(const Options &o, uint32_t type, int64_t n_out, int64_t n_in
     return G;
 }
 
+// Exponent E of the Q4_K 16x16 GEMM's min operand (gemm2.h): the largest
+// E <= 14 with max |dmin| * 63 * 2^E <= 2^15 over the tensor's blocks, so
+// the hi halves stay far inside the f16 range. dmin is the f16 at bytes
+// 2..3 of each 144-byte block (reference quant.h:71-78).
+static int q4k_min_exponent(const uint8_t *blocks, uint64_t nblocks) {
+    float mx = 0.0f;
+    for (uint64_t i = 0; i < nblocks; i++) {
+        const uint8_t *b = blocks + i * 144;
+        const float v = fabsf(half_to_float((uint32_t)b[2] | ((uint32_t)b[3] << 8)));
+        if (v > mx) mx = v;  // NaN never enters
+    }
+    int e = 14;
+    while (e > -24 && (double)mx * 63.0 * std::ldexp(1.0, e) > 32768.0) e--;
+    return e;
+}
+
 extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out,
                                    uint64_t n_in, const void *host_blocks, uint64_t bytes,
                                    sihip_weight **out) {
@@ -362,6 +388,7 @@ extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out
     w->dev = dev;
     w->split = split;
     w->spr = spr;
+    if (type == T_Q4_K) w->gexp = q4k_min_exponent((const uint8_t *)host_blocks, bytes / bb);
     if (split > 1) {
         w->part = reinterpret_cast<float *>(dev + L.total_bytes);
         w->cnt = reinterpret_cast<uint32_t *>(dev + L.total_bytes + part_bytes);
@@ -376,12 +403,13 @@ extern "C" int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w) {
     if (ctx) HIP_OK(ctx, hipSetDevice(ctx->device));
     (void)hipFree(w->dev);
     if (w->gemm) (void)hipFree(w->gemm);
+    if (w->gemm2) (void)hipFree(w->gemm2);
     delete w;
     return SIHIP_OK;
 }
 
 extern "C" uint64_t sihip_weight_device_bytes(const sihip_weight *w) {
-    return w ? (uint64_t)(w->L.total_bytes + w->split_bytes + w->gemm_bytes) : 0;
+    return w ? (uint64_t)(w->L.total_bytes + w->split_bytes + w->gemm_bytes + w->gemm2_bytes) : 0;
 }
 
 extern "C" int sihip_weight_tile_cols(const sihip_weight *w) { return w ? w->L.G : 0; }
@@ -643,19 +671,61 @@ static int build_gemm_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     return SIHIP_OK;
 }
 
+// Q4_K: the weight's copy in the order of the 16x16 GEMM (gemm2.h).
+static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
+    if (capturing(st))
+        return set_err(ctx, SIHIP_EINVAL,
+                       "the weight's GEMM copy would be built during graph capture: call "
+                       "sihip_weight_prepare_gemm before capturing");
+    const Layout &L = w->L;
+    const int64_t nb = L.n_in / 256;
+    const int64_t nblk32 = (L.n_out + kG2BN - 1) / kG2BN * (kG2BN / 32);
+    const int64_t bytes = gemm2_layout_bytes(nblk32, nb);
+    uint8_t *g = nullptr;
+    hipError_t e = hipMalloc(&g, (size_t)bytes);
+    if (e != hipSuccess)
+        return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
+                       hipGetErrorString(e));
+    const int64_t threads = nblk32 * nb * (kG2ChunkQ4K / 16);
+    hipLaunchKernelGGL(gemm2_layout_q4k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       L, (const uint8_t *)w->dev, g, nblk32, std::ldexp(1.0f, w->gexp));
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        (void)hipFree(g);
+        return set_err(ctx, SIHIP_EDEVICE, "gemm layout: %s", hipGetErrorString(e));
+    }
+    w->gemm2 = g;
+    w->gemm2_bytes = bytes;
+    return SIHIP_OK;
+}
+
 extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
     if (!ctx || !w) return set_err(ctx, SIHIP_EINVAL, "weight_prepare_gemm: NULL argument");
-    if (!gemm_mfma_supported(w->L.type) || w->gemm) return SIHIP_OK;
+    if (!gemm_mfma_supported(w->L.type)) return SIHIP_OK;
     HIP_OK(ctx, hipSetDevice(ctx->device));
-    const int rc = build_gemm_copy(ctx, w, ctx->stream);
-    if (rc) return rc;
+    if (!w->gemm) {
+        const int rc = build_gemm_copy(ctx, w, ctx->stream);
+        if (rc) return rc;
+    }
+    if (w->L.type == T_Q4_K && !w->gemm2) {
+        const int rc = build_gemm2_copy(ctx, w, ctx->stream);
+        if (rc) return rc;
+    }
     HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
     return SIHIP_OK;
 }
 
+// Smallest M that takes the 16x16 Q4_K GEMM (gemm2.h); option GEMM2_MIN_M.
+// It needs two of its 128-row workgroups per CU to hide latency: at the
+// 14336 x 4096 shape it is faster from M = 512 (83 against 95 us per call;
+// M = 2048: 323 against 357 us) and slower at M = 256 (67 against 50 us).
+constexpr int64_t kGemm2MinM = 384;
+static int64_t gemm2_min_m(const Options &o) { return o.gemm2_min_m > 0 ? o.gemm2_min_m : kGemm2MinM; }
+
 // Shape of one matrix-core GEMM call: tile height, padded rows, workspace
 // sizes and K slices.
 struct GemmPlan {
+    bool v2;           // the 16x16 Q4_K kernel (gemm2.h); mt then counts its 16-row m tiles
     int mt;            // 32-row MFMA tiles per wave along m
     int64_t Mp;        // M rounded up to the workgroup's rows
     int64_t ws_bytes;  // quantized activation planes
@@ -667,6 +737,21 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     GemmPlan p;
     const int64_t K = L.n_in, nb = K / 256;
     const int64_t NB = (L.n_out + kGemmBN - 1) / kGemmBN;
+    if (L.type == T_Q4_K && M >= gemm2_min_m(ctx->opt)) {
+        // 128-row m blocks; the GEMM_MT option (2, 4 or 8) overrides
+        p.v2 = true;
+        p.mt = 8;
+        if (ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4)
+            p.mt = (int)ctx->opt.gemm_mt;
+        const int64_t BM = 16 * p.mt;
+        p.Mp = (M + BM - 1) / BM * BM;
+        p.ws_bytes = p.Mp / BM * nb * g2_rec_bytes((int)BM);
+        p.S = 1;
+        p.SBK = (int)nb;
+        p.part_bytes = 0;
+        return p;
+    }
+    p.v2 = false;
     // small M: 32-row m tiles (twice the workgroups) with four super-blocks
     // of weights in flight per wave; the GEMM_MT option (1 or 2) overrides
     p.mt = M <= 128 ? 1 : 2;
@@ -713,10 +798,49 @@ struct GemmBufs {
 
 // Y[m, :] = W x[m, :] for m < M on the matrix cores, with the workspaces
 // in B (sized by plan_gemm); the weight's GEMM copy must exist.
+template <int MT, int W>
+static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, uint8_t *ws,
+                               const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
+                               hipStream_t st) {
+    constexpr int BM = 16 * MT;
+    const Layout &L = w->L;
+    const int64_t nb = L.n_in / 256;
+    const int64_t blocks = p.Mp * nb;
+    hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)), dim3(kG2Threads),
+                       0, st, X, ldx, M, p.Mp, nb, ws);
+    G2Args A;
+    A.w = w->gemm2;
+    A.x = ws;
+    A.y = Y;
+    A.ldy = ldy;
+    A.n_out = L.n_out;
+    A.M = M;
+    A.nb = (int)nb;
+    A.MB = (int)(p.Mp / BM);
+    A.NB = (int)((L.n_out + kG2BN - 1) / kG2BN);
+    A.yscale = std::ldexp(1.0f, -w->gexp);
+    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB));
+    hipLaunchKernelGGL((gemm2_q4k_kernel<MT, W>), grid, dim3(kG2Threads), 0, st, A);
+    return hipGetLastError();
+}
+
 static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPlan &p,
                             const GemmBufs &B, const float *X, int64_t ldx, int64_t M, float *Y,
                             int64_t ldy, hipStream_t st) {
     const Layout &L = w->L;
+    if (p.v2) {
+        hipError_t e;
+        const bool w1 = ctx->opt.gemm2_waves == 1;
+        switch (p.mt) {
+            case 2: e = launch_gemm2<2, 2>(w, p, B.ws, X, ldx, M, Y, ldy, st); break;
+            case 4: e = w1 ? launch_gemm2<4, 1>(w, p, B.ws, X, ldx, M, Y, ldy, st)
+                           : launch_gemm2<4, 2>(w, p, B.ws, X, ldx, M, Y, ldy, st); break;
+            default: e = w1 ? launch_gemm2<8, 1>(w, p, B.ws, X, ldx, M, Y, ldy, st)
+                            : launch_gemm2<8, 2>(w, p, B.ws, X, ldx, M, Y, ldy, st); break;
+        }
+        if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+        return SIHIP_OK;
+    }
     const int64_t K = L.n_in, nb = K / 256;
     const int NB = (int)((L.n_out + kGemmBN - 1) / kGemmBN);
     const int64_t BM = 32 * p.mt, Mp = p.Mp;
@@ -775,12 +899,16 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
 // overlap.
 static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X, int64_t ldx,
                          int64_t M, float *Y, int64_t ldy, hipStream_t st) {
-    sihip_weight *w = const_cast<sihip_weight *>(wc);  // the GEMM copy is a cache of w
-    if (!w->gemm) {
+    sihip_weight *w = const_cast<sihip_weight *>(wc);  // the GEMM copies are caches of w
+    const GemmPlan p = plan_gemm(ctx, w->L, M);
+    if (p.v2 && !w->gemm2) {
+        const int rc = build_gemm2_copy(ctx, w, st);
+        if (rc) return rc;
+    }
+    if (!p.v2 && !w->gemm) {
         const int rc = build_gemm_copy(ctx, w, st);
         if (rc) return rc;
     }
-    const GemmPlan p = plan_gemm(ctx, w->L, M);
     int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)p.ws_bytes, st);
     if (rc) return rc;
     if (p.S > 1) {
@@ -890,11 +1018,11 @@ extern "C" int sihip_gemm_dev_noalloc(sihip_ctx *ctx, const sihip_weight *w, con
     const hipStream_t st = (hipStream_t)stream;
     if (!gemm_on_mfma(ctx, w, M))
         return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out, st);
-    if (!w->gemm)
+    GemmPlan p = plan_gemm(ctx, w->L, M);
+    if (!(p.v2 ? w->gemm2 : w->gemm))
         return set_err(ctx, SIHIP_EINVAL,
                        "gemm_dev_noalloc: the weight has no GEMM copy; call "
                        "sihip_weight_prepare_gemm first");
-    GemmPlan p = plan_gemm(ctx, w->L, M);
     const size_t room = kNoAllocBytes - kNoAllocCntBytes;
     if ((size_t)p.ws_bytes > room)
         return set_err(ctx, SIHIP_ERANGE,

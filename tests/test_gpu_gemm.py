@@ -175,9 +175,11 @@ def test_gemm_k_slices(dev, oracle, option, wt, mt, sbk):
 
 
 def test_prepare_gemm_matches_lazy_copy(dev, oracle):
-    """sihip_weight_prepare_gemm builds the GEMM copy at once (device bytes
-    grow by it, a second call adds nothing); a later gemm gives the bits of a
-    weight whose copy its first gemm built. Other types: a no-op."""
+    """sihip_weight_prepare_gemm builds the GEMM copies at once (device bytes
+    grow by them, a second call adds nothing; Q4_K has two, one per GEMM
+    kernel, and a lazy call builds only the one it uses); a later gemm gives
+    the bits of a weight whose copy its first gemm built. Other types: a
+    no-op."""
     rng = np.random.default_rng(4242)
     n_out, n_in, M = 700, 2048, 40
     W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
@@ -193,7 +195,7 @@ def test_prepare_gemm_matches_lazy_copy(dev, oracle):
         eager.prepare_gemm()
         assert eager.device_bytes == grown
         Ye, Yl = dev.gemm(eager, X), dev.gemm(lazy, X)
-        assert lazy.device_bytes == grown
+        assert before < lazy.device_bytes < grown
         assert np.array_equal(Ye.view(np.uint32), Yl.view(np.uint32))
         ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
         assert_close(Ye.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
@@ -204,3 +206,44 @@ def test_prepare_gemm_matches_lazy_copy(dev, oracle):
     finally:
         for w in (eager, lazy, w6):
             w.free()
+
+
+def _extreme_q4k(W, n_out, n_in, huge_dmin):
+    """Q4_K rows at the ends of the 16x16 GEMM's operand ranges: row 0 with
+    every 6-bit scale and min 63 and every quant 15 (sh * q = sl * q = 105),
+    row 1 with d = 0, row 2 with dmin = 0 and, when huge_dmin, row 3 with
+    dmin = 1000 (which lowers the tensor's min-operand exponent E below 0)."""
+    blk = W.reshape(n_out, n_in // 256, 144)
+    blk[0, :, 4:144] = 0xFF
+    if n_out > 1:
+        blk[1, :, 0:2] = 0
+    if n_out > 2:
+        blk[2, :, 2:4] = 0
+    if n_out > 3 and huge_dmin:
+        blk[3, :, 2:4] = np.frombuffer(np.float16(1000.0).tobytes(), np.uint8)
+    return W
+
+
+@pytest.mark.parametrize("n_out,n_in,M,mt,huge", [
+    (200, 1024, 16, 8, False), (333, 2048, 130, 8, True), (1000, 256, 100, 4, False),
+    (129, 768, 65, 2, True), (130, 4096, 257, 8, False), (4096, 1280, 384, 8, True),
+])
+def test_gemm2_q4k_vs_oracle(dev, oracle, option, n_out, n_in, M, mt, huge):
+    """The 16x16 Q4_K GEMM (gemm2.h) forced at every M, m-tile count 2, 4
+    and 8, ragged M and n_out, one super-block per row, and rows at the ends
+    of its operand ranges, against the oracle."""
+    option("GEMM2_MIN_M", "1")
+    option("GEMM_MT", str(mt))
+    rng = np.random.default_rng(n_out + 3 * n_in + M + mt)
+    W = _extreme_q4k(synth.make_weights(sa.Q4_K, n_out, n_in, rng), n_out, n_in, huge)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(sa.Q4_K, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+        Y2 = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
+    what = f"gemm2 Q4_K {n_out}x{n_in} M={M} MT={mt}"
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
+    assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
