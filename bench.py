@@ -482,6 +482,31 @@ def profile_traffic(dev, torch, stream, rng):
             "gate_up_weight_bytes": 2 * 33030144}
 
 
+def host_cpus():
+    """Lanes for the CPU baseline: every CPU this process may run on (its
+    affinity set, the host's share granted to the job), one lane each; and a
+    description of the host: CPU model, logical CPUs and physical cores of
+    the machine, and the affinity count."""
+    allowed = len(os.sched_getaffinity(0))
+    model, phys = "unknown", set()
+    try:
+        cur = {}
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model == "unknown":
+                model = v
+            if k in ("physical id", "core id"):
+                cur[k] = v
+            if not line.strip() and cur:
+                phys.add((cur.get("physical id"), cur.get("core id")))
+                cur = {}
+    except OSError:
+        pass
+    return allowed, {"cpu_model": model, "host_logical_cpus": os.cpu_count(),
+                     "host_physical_cores": len(phys) or None, "affinity_cpus": allowed}
+
+
 def cpu_baseline(host_layers, pass_bytes, budget_s=10.0):
     """The reference's own AVX2 gemv (compiled from the reference sources into
     oracle/_ref) through its lane pool, on a bounded sample of the same
@@ -493,7 +518,7 @@ def cpu_baseline(host_layers, pass_bytes, budget_s=10.0):
     from oracle import siq
     ref = siq.Reference.load()
     kind = "reference" if ref is not None else "port"
-    lanes = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+    lanes, host = host_cpus()
     from siphon_amd import synth
     shapes = {name: (wt, n_out, n_in) for (name, wt, n_out, n_in) in synth.LLAMA3_8B_LAYER}
     rng = np.random.default_rng(7)
@@ -521,7 +546,7 @@ def cpu_baseline(host_layers, pass_bytes, budget_s=10.0):
     total_bytes = sum(it[1].nbytes for it in items)
     total_s = sum(float(np.median(it[5])) for it in items)
     gbs = total_bytes / total_s / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": lanes, "kind": kind,
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": lanes, "kind": kind, **host,
             "impl": ("avx2" if ref.avx2 else "scalar") if ref is not None else "oracle",
             "sample": f"{len(host_layers)} layers x 7 matrices ({total_bytes} weight bytes), "
                       f"round-robin gemv calls (quantize + dots) through a {lanes}-lane pool, "

@@ -22,9 +22,9 @@ F32, F16, Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 6, 8, 
 GEOM = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34),
         Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176),
         Q6_K: (256, 210), Q8_K: (256, 292)}
-PAIR = {F16: F16, Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K,
+PAIR = {F32: F32, F16: F16, Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K,
         Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
-NAMES = {F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K",
+NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K",
          Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_K: "Q8_K"}
 WEIGHT_TYPES = [Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F16]
 

@@ -50,6 +50,7 @@ int siq_geometry(uint32_t type, uint32_t *blk_elems, uint32_t *blk_bytes) {
 int siq_pair(uint32_t wtype, uint32_t *pair) {
     uint32_t p;
     switch (wtype) {
+        case SIQ_F32: p = SIQ_F32; break; /* x passes through (backend.c:102-103) */
         case SIQ_F16: p = SIQ_F16; break;
         case SIQ_Q4_0: case SIQ_Q5_0: case SIQ_Q8_0: p = SIQ_Q8_0; break;
         case SIQ_Q2_K: case SIQ_Q3_K: case SIQ_Q4_K: case SIQ_Q5_K:
@@ -210,6 +211,7 @@ void siq_convert_f16(const float *x, uint16_t *out, int64_t n) {
 
 int siq_quantize_pair(uint32_t pair, const float *x, void *out, int64_t n) {
     switch (pair) {
+        case SIQ_F32: memcpy(out, x, (size_t)n * sizeof(float)); return 1;
         case SIQ_F16: siq_convert_f16(x, out, n); return 1;
         case SIQ_Q8_0: siq_quantize_q8_0(x, out, n); return 1;
         case SIQ_Q8_K: siq_quantize_q8_K(x, out, n); return 1;
@@ -341,6 +343,10 @@ static int decode_block(uint32_t type, const uint8_t *b, blk_vals *v) {
 
 int siq_dequant_row(uint32_t type, const void *w, float *out, int64_t n) {
     uint32_t be, bb;
+    if (type == SIQ_F32) {
+        memcpy(out, w, (size_t)n * sizeof(float));
+        return 1;
+    }
     if (type == SIQ_F16) {
         const uint8_t *p = w;
         for (int64_t i = 0; i < n; i++) out[i] = siq_f16_to_f32(rd16(p + 2 * i));
@@ -396,6 +402,17 @@ int siq_vec_dot(uint32_t wtype, int64_t n, const void *w, const void *a,
     uint32_t pair, be, bb;
     if (!siq_pair(wtype, &pair)) return 0;
     double s = 0.0, m = 0.0;
+    if (wtype == SIQ_F32) {
+        /* reference si_dot_f32 (kernels.c:180-187) sums the float products
+         * in double; here each product is exact (24 + 24 bits) */
+        const float *pw = w, *pa = a;
+        for (int64_t i = 0; i < n; i++) {
+            const double t = (double)pw[i] * (double)pa[i];
+            s += t; m += fabs(t);
+        }
+        *dot = s; if (l1) *l1 = m;
+        return 1;
+    }
     if (wtype == SIQ_F16) {
         const uint8_t *pw = w, *pa = a;
         for (int64_t i = 0; i < n; i++) {
@@ -432,7 +449,7 @@ int siq_vec_dot_dequant(uint32_t wtype, int64_t n, const void *w,
                         const void *a, double *dot, double *l1) {
     uint32_t pair, be, bb;
     if (!siq_pair(wtype, &pair)) return 0;
-    if (wtype == SIQ_F16) return siq_vec_dot(wtype, n, w, a, dot, l1);
+    if (wtype == SIQ_F16 || wtype == SIQ_F32) return siq_vec_dot(wtype, n, w, a, dot, l1);
     siq_geometry(wtype, &be, &bb);
     float *wf = malloc((size_t)n * sizeof(float));
     if (!wf) return 0;
@@ -486,6 +503,7 @@ static void *row_task_fn(void *p) {
 
 static size_t pair_bytes(uint32_t pair, int64_t n) {
     switch (pair) {
+        case SIQ_F32: return (size_t)n * 4;
         case SIQ_F16: return (size_t)n * 2;
         case SIQ_Q8_0: return (size_t)(n / 32) * 34;
         case SIQ_Q8_K: return (size_t)(n / 256) * 292;

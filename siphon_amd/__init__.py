@@ -14,15 +14,17 @@ import numpy as np
 from .build import HIP_SO
 
 # ggml type ids (reference include/siphon/quant.h:103-119)
-F16, Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 1, 2, 6, 8, 10, 11, 12, 13, 14, 15
-GEOM = {F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q2_K: (256, 84),
+F32, F16, Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 6, 8, 10, 11, 12, 13, 14, 15
+GEOM = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q2_K: (256, 84),
         Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
         Q8_K: (256, 292)}
-PAIR = {F16: F16, Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K,
+PAIR = {F32: F32, F16: F16, Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K,
         Q5_K: Q8_K, Q6_K: Q8_K}
-NAMES = {F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K",
+NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K",
          Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_K: "Q8_K"}
 TYPES = {v: k for k, v in NAMES.items()}
+# formats in the planar layout (every layout test runs over these); F32
+# weights keep their rows as they are and have tests of their own
 WEIGHT_TYPES = [Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F16]
 
 ABI_VERSION = 3
@@ -242,6 +244,8 @@ class Device:
         x = np.ascontiguousarray(x, dtype=np.float32)
         be, bb = GEOM[pair]
         out = np.zeros(x.size // be * bb, dtype=np.uint8)
+        if pair == F32:
+            return x.view(np.uint8).copy()
         fn = {Q8_K: self.L.sihip_quantize_q8_K, Q8_0: self.L.sihip_quantize_q8_0,
               F16: self.L.sihip_convert_f16}[pair]
         self._check(fn(self.ctx, _ptr(x), _ptr(out), x.size))

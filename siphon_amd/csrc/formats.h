@@ -42,6 +42,7 @@ enum : uint32_t {
 // GGUF geometry (reference quant.h:92-100).
 SIHD inline bool geometry(uint32_t t, uint32_t *be, uint32_t *bb) {
     switch (t) {
+        case T_F32:  *be = 1;   *bb = 4;   return true;
         case T_F16:  *be = 1;   *bb = 2;   return true;
         case T_Q4_0: *be = 32;  *bb = 18;  return true;
         case T_Q5_0: *be = 32;  *bb = 22;  return true;
@@ -59,6 +60,7 @@ SIHD inline bool geometry(uint32_t t, uint32_t *be, uint32_t *bb) {
 // Activation pair format (reference kernels.c:946-960).
 SIHD constexpr inline uint32_t pair_of(uint32_t t) {
     switch (t) {
+        case T_F32: return T_F32;
         case T_F16: return T_F16;
         case T_Q4_0: case T_Q5_0: case T_Q8_0: return T_Q8_0;
         default: return T_Q8_K;
@@ -129,7 +131,7 @@ SIHD inline int64_t plane_records(const Layout &L, int p) {
 
 inline bool make_layout(uint32_t type, int64_t n_out, int64_t n_in, int G, Layout *L) {
     uint32_t be, bb;
-    if (!geometry(type, &be, &bb) || type == T_Q8_K) return false;
+    if (!geometry(type, &be, &bb) || type == T_Q8_K || type == T_F32) return false;  // F32: no planes
     if (n_in <= 0 || n_out <= 0 || n_in % 32 != 0 || n_in % be != 0) return false;
     if (G < 1 || G > 64 || (G & (G - 1))) return false;
     L->type = type;

@@ -688,14 +688,21 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
     }
+    // Ordering: each wave's partial-sum stores have completed (vmcnt 0) before
+    // the barrier and hence before the arrival is counted; the last
+    // workgroup's sc1 loads are issued after the barrier that follows the
+    // count's return. The signal fences keep the compiler from moving memory
+    // operations across these points (they emit no instruction).
     __shared__ uint32_t last_flag;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     uint32_t *cnt = A.cnt + (int64_t)mblk * A.NB + nblk;
     if (threadIdx.x == 0)
         last_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                     (uint32_t)A.S - 1;
     __syncthreads();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (!last_flag) return;
     // this thread's outputs: rows m0 + idx / BN, columns nblk * BN + idx % BN
     // for idx = tid + 256 q; all loads of one slice are issued together

@@ -291,12 +291,17 @@ struct Buf {
 // and cost occupancy where the activations fill it exactly).
 template <int NC>
 __device__ inline void split_reduce(const MVSeg &sg, uint32_t grp, uint32_t ldp, uint32_t *last) {
+    // The signal fences keep the compiler from moving memory operations
+    // across the completion wait, the count and the loads after it (they
+    // emit no instruction); the hardware order is the wait and the barriers.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (threadIdx.x == 0)
         *last = __hip_atomic_fetch_add(sg.cnt + grp, 1u, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT) == sg.split - 1;
     __syncthreads();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (!*last) return;
     const uint32_t rows = kWaves * sg.R;
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(

@@ -19,6 +19,7 @@
 #include "attn.h"
 #include "formats.h"
 #include "gemm.h"
+#include "f32w.h"
 #include "gemm2.h"
 #include "matvec.h"
 #include "quant.h"
@@ -327,10 +328,43 @@ static int q4k_min_exponent(const uint8_t *blocks, uint64_t nblocks) {
     return e;
 }
 
+// F32 weights: the rows as they are (f32w.h). Layout fields other than
+// type and shape stay zero; no plane, slice or GEMM copy exists.
+static int upload_f32(sihip_ctx *ctx, uint64_t n_out, uint64_t n_in, const void *host,
+                      uint64_t bytes, sihip_weight **out) {
+    if (n_out == 0 || n_in == 0)
+        return set_err(ctx, SIHIP_EINVAL, "weight_upload: empty F32 tensor");
+    if (n_in > (1ull << 30) || n_out > (1ull << 31))
+        return set_err(ctx, SIHIP_ERANGE, "weight_upload: shape too large");
+    if (bytes != n_out * n_in * 4)
+        return set_err(ctx, SIHIP_EINVAL, "weight_upload: %llu bytes given, %llu expected",
+                       (unsigned long long)bytes, (unsigned long long)(n_out * n_in * 4));
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    uint8_t *dev = nullptr;
+    if (hipMalloc((void **)&dev, (size_t)bytes) != hipSuccess)
+        return set_err(ctx, SIHIP_ENOMEM, "weight_upload: %llu device bytes", (unsigned long long)bytes);
+    hipError_t e = hipMemcpyAsync(dev, host, (size_t)bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return set_err(ctx, SIHIP_EDEVICE, "weight_upload: %s", hipGetErrorString(e));
+    }
+    sihip_weight *w = new sihip_weight();
+    memset(&w->L, 0, sizeof w->L);
+    w->L.type = T_F32;
+    w->L.n_out = (int64_t)n_out;
+    w->L.n_in = (int64_t)n_in;
+    w->L.total_bytes = (int64_t)bytes;
+    w->dev = dev;
+    *out = w;
+    return SIHIP_OK;
+}
+
 extern "C" int sihip_weight_upload(sihip_ctx *ctx, uint32_t type, uint64_t n_out,
                                    uint64_t n_in, const void *host_blocks, uint64_t bytes,
                                    sihip_weight **out) {
     if (!ctx || !out || !host_blocks) return set_err(ctx, SIHIP_EINVAL, "weight_upload: NULL argument");
+    if (type == T_F32) return upload_f32(ctx, n_out, n_in, host_blocks, bytes, out);
     uint32_t be, bb;
     if (!geometry(type, &be, &bb) || type == T_Q8_K)
         return set_err(ctx, SIHIP_ENOTSUP, "weight_upload: unsupported ggml type %u", type);
@@ -521,10 +555,35 @@ static int max_cols(const sihip_ctx *ctx, uint32_t pair, int64_t n_in) {
 // rows [0, n_out[i]) of y[i] (column stride ldy[i]). The caller checks that
 // the matrices share n_in and that mix_supported() holds for their formats.
 // M is split into launches of 8/4/2/1 columns.
+// F32 weights (f32w.h): launches of up to kF32Cols columns of x (f32;
+// the pair format of F32 is f32 itself).
+static int run_f32(sihip_ctx *ctx, const sihip_weight *w, int64_t n_out, float *y, int64_t ldy,
+                   const float *x, int64_t ldx, int64_t M, hipStream_t st) {
+    const dim3 grid((unsigned)((n_out + kF32Threads / 64 - 1) / (kF32Threads / 64)));
+    const float *W = (const float *)w->dev;
+    for (int64_t m = 0; m < M;) {
+        const int64_t nc = M - m >= kF32Cols ? kF32Cols : M - m;
+        switch (nc) {
+            case 4: hipLaunchKernelGGL(f32_matvec_kernel<4>, grid, dim3(kF32Threads), 0, st, W, w->L.n_in, n_out, x + m * ldx, ldx, y + m * ldy, ldy); break;
+            case 3: hipLaunchKernelGGL(f32_matvec_kernel<3>, grid, dim3(kF32Threads), 0, st, W, w->L.n_in, n_out, x + m * ldx, ldx, y + m * ldy, ldy); break;
+            case 2: hipLaunchKernelGGL(f32_matvec_kernel<2>, grid, dim3(kF32Threads), 0, st, W, w->L.n_in, n_out, x + m * ldx, ldx, y + m * ldy, ldy); break;
+            default: hipLaunchKernelGGL(f32_matvec_kernel<1>, grid, dim3(kF32Threads), 0, st, W, w->L.n_in, n_out, x + m * ldx, ldx, y + m * ldy, ldy); break;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "f32 matvec launch: %s", hipGetErrorString(e));
+        m += nc;
+    }
+    return SIHIP_OK;
+}
+
 static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const *w,
                             const int64_t *n_out, float *const *y, const int64_t *ldy,
                             const float *x, int64_t ldx, const uint8_t *xq, int64_t ldxq,
                             int64_t M, hipStream_t st) {
+    if (w[0]->L.type == T_F32) {  // callers pass F32 weights one at a time
+        const float *xf = x ? x : (const float *)xq;
+        return run_f32(ctx, w[0], n_out[0], y[0], ldy[0], xf, x ? ldx : ldxq / 4, M, st);
+    }
     const int64_t n_in = w[0]->L.n_in;
     const uint32_t pair = pair_of(w[0]->L.type);
     uint32_t f0 = w[0]->L.type, f1 = w[0]->L.type;
@@ -935,6 +994,11 @@ static int run_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64
 
 static hipError_t launch_dequant(const Layout &L, const uint8_t *w, int64_t row0, int64_t nrows,
                                  float *out, int64_t ldo, hipStream_t st) {
+    if (L.type == T_F32) {
+        hipLaunchKernelGGL(f32_rows_kernel, dim3((unsigned)((nrows * L.n_in + kF32Threads - 1) / kF32Threads)),
+                           dim3(kF32Threads), 0, st, (const float *)w, L.n_in, row0, nrows, out, ldo);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((nrows * L.ncols + kThreads - 1) / kThreads)), block(kThreads);
     switch (L.type) {
         case T_F16: hipLaunchKernelGGL(dequant_rows_kernel<T_F16>, grid, block, 0, st, L, w, row0, nrows, out, ldo); break;
@@ -1123,7 +1187,7 @@ extern "C" int sihip_gemv_multi_dev(sihip_ctx *ctx, int count, const sihip_weigh
         if (w[i]->L.type < f0) f0 = w[i]->L.type;
         if (w[i]->L.type > f1) f1 = w[i]->L.type;
     }
-    bool fused = mix_supported(f0, f1);
+    bool fused = mix_supported(f0, f1) && f0 != T_F32;
     for (int i = 0; i < count && fused; i++)
         fused = w[i]->L.type == f0 || w[i]->L.type == f1;
     int64_t n_out[kMaxSegs], ldy[kMaxSegs];
@@ -1286,7 +1350,7 @@ extern "C" int sihip_gemv_pair(sihip_ctx *ctx, uint32_t wtype, int64_t n_rows, i
     uint32_t be, bb;
     if (!geometry(wtype, &be, &bb) || wtype == T_Q8_K)
         return set_err(ctx, SIHIP_ENOTSUP, "gemv_pair: unsupported type %u", wtype);
-    if (n_rows <= 0 || n_in <= 0 || n_in % be || n_in % 32)
+    if (n_rows <= 0 || n_in <= 0 || (wtype != T_F32 && (n_in % be || n_in % 32)))
         return set_err(ctx, SIHIP_EINVAL, "gemv_pair: bad shape");
     const uint32_t pair = pair_of(wtype);
     uint32_t pe, pb;

@@ -29,8 +29,22 @@ typedef struct {
     const void *data;
     uint32_t type;
     uint64_t n_out, n_in, bytes;
+    uint64_t print;   /* content fingerprint (fingerprint()) */
     sihip_weight *w;
 } slot;
+
+/* FNV-1a over the first and last 64 bytes of a tensor: a tensor of the
+ * same type and shape mapped at a reused address (a model closed and
+ * another opened while the backend stays open) almost surely differs in
+ * them, so it gets a fresh upload. */
+static uint64_t fingerprint(const void *data, uint64_t bytes) {
+    const unsigned char *p = data;
+    const uint64_t k = bytes < 64 ? bytes : 64;
+    uint64_t h = 0xcbf29ce484222325ULL;
+    for (uint64_t i = 0; i < k; i++) h = (h ^ p[i]) * 0x100000001b3ULL;
+    for (uint64_t i = bytes - k; i < bytes; i++) h = (h ^ p[i]) * 0x100000001b3ULL;
+    return h;
+}
 
 typedef struct {
     si_backend base;  /* first member: the engine sees a plain si_backend */
@@ -85,13 +99,15 @@ static int slot_insert(hip_backend *hb, const slot *ins) {
 static int si_code(int rc) { return rc == SIHIP_EDEVICE ? SI_EIO : rc; }
 
 /* The device copy of w, uploaded on first use. A cached copy whose key
- * pointer now belongs to a tensor of another type or shape is stale (its
- * memory was reused): it is replaced. */
+ * pointer now belongs to a tensor of another type, shape or content (its
+ * memory was reused) is stale: it is replaced. */
 static int device_weight(hip_backend *hb, const si_tensor *w, sihip_weight **out) {
     const uint64_t n_in = w->ne[0], n_out = w->ne[1] ? w->ne[1] : 1;
+    const uint64_t print = fingerprint(w->data, w->n_bytes);
     slot *s = slot_find(hb, w->data);
     if (s) {
-        if (s->type == w->type && s->n_out == n_out && s->n_in == n_in && s->bytes == w->n_bytes) {
+        if (s->type == w->type && s->n_out == n_out && s->n_in == n_in && s->bytes == w->n_bytes &&
+            s->print == print) {
             *out = s->w;
             return SI_OK;
         }
@@ -108,6 +124,7 @@ static int device_weight(hip_backend *hb, const si_tensor *w, sihip_weight **out
         s->n_out = n_out;
         s->n_in = n_in;
         s->bytes = w->n_bytes;
+        s->print = print;
         s->w = dw;
         *out = dw;
         return SI_OK;
@@ -120,7 +137,7 @@ static int device_weight(hip_backend *hb, const si_tensor *w, sihip_weight **out
                    hb->f.last_error(hb->ctx));
         return si_code(rc);
     }
-    const slot ins = {w->data, w->type, n_out, n_in, w->n_bytes, dw};
+    const slot ins = {w->data, w->type, n_out, n_in, w->n_bytes, print, dw};
     const int irc = slot_insert(hb, &ins);
     if (irc) {
         hb->f.weight_free(hb->ctx, dw);

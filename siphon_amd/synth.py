@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import F16, GEOM, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
+from . import F16, F32, GEOM, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
 
 # byte offsets of the f16 scale fields inside each block
 F16_FIELDS = {Q4_0: (0,), Q5_0: (0,), Q8_0: (0,), Q2_K: (80, 82), Q3_K: (108,),
@@ -26,10 +26,13 @@ def make_weights(wtype: int, n_out: int, n_in: int, rng: np.random.Generator,
 
     Q6_K block scales are int8 uniform in [-32, 31] and Q8_0 quants uniform in
     [-127, 127] (the benchmark's stated distributions); all other quant and
-    sub-scale bytes are uniform random. F16 weights are uniform in
+    sub-scale bytes are uniform random. F16 and F32 weights are uniform in
     [-0.05, 0.05].
     """
     be, bb = GEOM[wtype]
+    if wtype == F32:
+        w = rng.uniform(-0.05, 0.05, n_out * n_in).astype(np.float32)
+        return w.view(np.uint8).reshape(n_out, n_in * 4)
     if wtype == F16:
         w = rng.uniform(-0.05, 0.05, n_out * n_in).astype(np.float16)
         return w.view(np.uint8).reshape(n_out, n_in * 2)

@@ -48,7 +48,7 @@ def test_vtable_gemv_gemm_row_to_f32(harness, oracle):
     try:
         rng = np.random.default_rng(17)
         for wt, n_out, n_in in ((sa.Q4_K, 300, 2048), (sa.Q6_K, 129, 1024), (sa.Q8_0, 77, 896),
-                                (sa.F16, 64, 512)):
+                                (sa.F16, 64, 512), (sa.F32, 65, 501)):
             W = synth.make_weights(wt, n_out, n_in, rng)
             keep.append(W)
             x = rng.standard_normal(n_in).astype(np.float32)
@@ -74,7 +74,7 @@ def test_vtable_gemv_gemm_row_to_f32(harness, oracle):
             assert np.array_equal(out.view(np.uint32),
                                   oracle.dequant(wt, W[3], n_in).view(np.uint32))
         n, nbytes = harness.weights(be)
-        assert n == 4 and nbytes > 0
+        assert n == 5 and nbytes > 0
     finally:
         harness.close(be)
 
@@ -104,7 +104,9 @@ def test_vtable_error_contract(harness):
 @pytest.mark.gpu
 def test_reused_address_is_not_served_stale(harness, oracle):
     """A host buffer that is freed and reused for a different tensor (a
-    different type or shape at the same address) gets a fresh upload."""
+    different type or shape at the same address, or the same type and
+    shape with other contents, told apart by a fingerprint of the first
+    and last 64 bytes) gets a fresh upload."""
     rc, be = harness.open(HIP_SO)
     assert rc == 0, harness.errstr()
     try:
@@ -125,6 +127,13 @@ def test_reused_address_is_not_served_stale(harness, oracle):
         ref2, l2 = oracle.gemv(sa.F16, W2, 64, 512, x2)
         assert np.all(np.abs(y2.astype(np.float64) - ref2) <= 1e-5 * l2 + 1e-6)
         assert harness.weights(be)[0] == 1  # the stale copy was replaced, not kept
+        W3 = synth.make_weights(sa.F16, 64, 512, rng)  # same type and shape, new contents
+        buf[:W3.nbytes] = W3.reshape(-1)
+        y3 = np.zeros(64, np.float32)
+        assert harness.gemv(be, sa.F16, 64, 512, buf[:W3.nbytes], x2, y3, 64) == 0
+        ref3, l3 = oracle.gemv(sa.F16, W3, 64, 512, x2)
+        assert np.all(np.abs(y3.astype(np.float64) - ref3) <= 1e-5 * l3 + 1e-6)
+        assert harness.weights(be)[0] == 1
     finally:
         harness.close(be)
 

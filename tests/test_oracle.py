@@ -198,3 +198,28 @@ def test_against_compiled_reference(oracle, ref):
             d, l1 = oracle.vec_dot(wt, N, W[r], xq)
             for simd in (True, False):
                 assert abs(ref.dot(wt, N, W[r], xq, simd=simd) - d) <= 1e-6 * l1
+
+
+def test_f32_dot_exact_and_vs_reference(oracle):
+    """F32 weights (reference pair F32: x passes through, si_dot_f32 sums
+    float products in double, kernels.c:180-187): the oracle's dot is the
+    exact sum of exact products, so it equals numpy's float64 dot of the
+    same values to double rounding; against the compiled reference's own
+    gemv (where oracle/_ref is built) each row is within the reference's
+    float-product rounding, at most 2^-24 of the terms' L1."""
+    rng = np.random.default_rng(32)
+    n_out, n_in = 37, 1001  # odd length: no vector assumption
+    W = rng.uniform(-0.05, 0.05, (n_out, n_in)).astype(np.float32)
+    x = rng.standard_normal(n_in).astype(np.float32)
+    Wb = W.view(np.uint8)
+    y, l1 = oracle.gemv(siq.F32, Wb, n_out, n_in, x)
+    exact = W.astype(np.float64) @ x.astype(np.float64)
+    assert np.all(np.abs(y.astype(np.float64) - exact) <= 2.0 ** -24 * np.abs(exact) + 1e-30)
+    assert np.allclose(l1, np.abs(W.astype(np.float64) * x.astype(np.float64)).sum(axis=1))
+    d, m = oracle.vec_dot(siq.F32, n_in, Wb[5], x.view(np.uint8))
+    assert abs(d - exact[5]) <= 1e-12 * m
+    assert np.array_equal(oracle.dequant(siq.F32, Wb[3], n_in), W[3])
+    r = siq.Reference.load()
+    if r is not None:
+        yr, _ = r.gemv_timed(siq.F32, Wb, n_out, n_in, x, 1, 1)
+        assert np.all(np.abs(yr.astype(np.float64) - exact) <= 2.0 ** -24 * l1 + 2.0 ** -24 * np.abs(exact))
