@@ -315,17 +315,20 @@ def bench_attention(dev, torch, stream, positions=(511, 4095)):
     return res
 
 
-def bench_gemm(dev, torch, stream, rng):
+def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
     """Config 3: Q4_K W[14336 x 4096] x X[M x 4096] -> Y[M x 14336], M = 512
     headline and the sweep {64, 128, 512, 2048}. Each call quantizes X to Q8_K
-    rows and runs the MFMA GEMM; ten weight copies rotate so the 256 MB
-    Infinity Cache cannot serve the weights. The first call per copy builds
-    its GEMM-ordered copy and is excluded (warm-up)."""
+    rows and runs the MFMA GEMM; enough weight copies rotate that more than
+    `rotate_bytes` of GGUF bytes (fewer than any GEMM-ordered copy holds)
+    stream between two reads of one copy, so the 256 MB Infinity Cache cannot
+    serve them. The first call per copy builds its GEMM-ordered copy and is
+    excluded (warm-up)."""
     import siphon_amd as sa
     from siphon_amd import synth
     n_out, n_in = 14336, 4096
     W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
-    ws = [dev.upload(sa.Q4_K, n_out, n_in, W) for _ in range(10)]
+    copies = -(-rotate_bytes // W.nbytes) + 1
+    ws = [dev.upload(sa.Q4_K, n_out, n_in, W) for _ in range(copies)]
     sp = stream.cuda_stream
     sweep = {}
     for M in (64, 128, 512, 2048):
@@ -335,7 +338,7 @@ def bench_gemm(dev, torch, stream, rng):
             for w in ws:
                 dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
         torch.cuda.synchronize()
-        reps = 20
+        reps = 2 * len(ws)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         with torch.cuda.stream(stream):
@@ -358,12 +361,12 @@ def bench_gemm(dev, torch, stream, rng):
     Y = torch.empty(M, n_out, device="cuda")
     for wt in (sa.Q5_K, sa.Q2_K, sa.Q3_K):
         Wf = synth.make_weights(wt, n_out, n_in, rng)
-        wf = [dev.upload(wt, n_out, n_in, Wf) for _ in range(6)]
+        wf = [dev.upload(wt, n_out, n_in, Wf) for _ in range(-(-rotate_bytes // Wf.nbytes) + 1)]
         with torch.cuda.stream(stream):
             for w in wf:
                 dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
         torch.cuda.synchronize()
-        reps = 12
+        reps = 2 * len(wf)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         with torch.cuda.stream(stream):
@@ -380,6 +383,7 @@ def bench_gemm(dev, torch, stream, rng):
     del X, Y
     head = sweep["512"]
     return {"value": head["TOPS"], "unit": "TOPS", "M": 512, "shape": [n_out, n_in],
+            "copies": copies,
             "us_per_call": head["us_per_call"], "sweep": sweep, "other_formats_m512": formats,
             "roofline": {"bound": "mfma", "achieved": head["TOPS"], "peak": INT8_PEAK_TOPS,
                          "unit": "TOP/s", "frac": head["frac_int8_peak"]}}
@@ -391,6 +395,7 @@ def _config_shapes():
     256; the 896-wide head of that model cannot be Q6_K)."""
     import siphon_amd as sa
     shapes = [("cfg0 Q4_K 5632x2048", sa.Q4_K, 5632, 2048, (1,)),
+              ("cfg0 Q4_0 5632x2048", sa.Q4_0, 5632, 2048, (1, 8)),
               ("cfg1 Q8_0 4864x896", sa.Q8_0, 4864, 896, (1,)),
               ("cfg1 Q6_K head 151936x1024", sa.Q6_K, 151936, 1024, (1,)),
               ("cfg1 Q8_0 head 151936x896", sa.Q8_0, 151936, 896, (1,))]

@@ -28,6 +28,10 @@ NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K:
          Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_K: "Q8_K"}
 WEIGHT_TYPES = [Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F16]
 
+# worker threads of the oracle's row loop: the CPUs this process may run on,
+# at most 16 (the share of one GPU box)
+LANES = max(1, min(16, len(os.sched_getaffinity(0))))
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _u32 = ctypes.c_uint32
@@ -119,7 +123,7 @@ class Oracle:
         assert fn(wtype, n, _ptr(w), _ptr(a), ctypes.byref(d), ctypes.byref(m))
         return d.value, m.value
 
-    def gemv(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, x: np.ndarray, lanes: int = 8):
+    def gemv(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, x: np.ndarray, lanes: int = LANES):
         W = np.ascontiguousarray(W, dtype=np.uint8)
         x = np.ascontiguousarray(x, dtype=np.float32)
         y = np.zeros(n_out, dtype=np.float32)
@@ -127,7 +131,7 @@ class Oracle:
         assert self.L.siq_gemv(wtype, _ptr(W), n_out, n_in, _ptr(x), _ptr(y), _ptr(l1), lanes)
         return y, l1
 
-    def gemm(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, X: np.ndarray, lanes: int = 8):
+    def gemm(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, X: np.ndarray, lanes: int = LANES):
         W = np.ascontiguousarray(W, dtype=np.uint8)
         X = np.ascontiguousarray(X, dtype=np.float32)
         M = X.shape[0]

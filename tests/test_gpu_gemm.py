@@ -103,12 +103,15 @@ def test_gemm_mfma_every_tile_width(dev, oracle, option, wt, G):
                  f"mfma gemm {sa.NAMES[wt]} G={G}")
 
 
-def test_gemm_config3_sampled_rows(dev, oracle):
-    """Config 3 at full size (Q4_K 14336 x 4096, M = 512) on the default
-    path; 160 weight rows spread over every workgroup tile are checked
-    against the oracle for all 512 activation rows."""
-    rng = np.random.default_rng(3)
-    n_out, n_in, M = 14336, 4096, 512
+@pytest.mark.parametrize("M", [64, 128, 512, 2048])
+def test_gemm_config3_full_size(dev, oracle, M):
+    """Config 3 at full size (Q4_K 14336 x 4096) over its M sweep on the
+    default dispatch. Up to M = 512 every output is checked against the
+    oracle; above that, 160 weight rows spread over every workgroup tile for
+    all M activation rows, and every weight row for four activation rows
+    (first, last and two inside)."""
+    rng = np.random.default_rng(3 + M)
+    n_out, n_in = 14336, 4096
     W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
     X = rng.standard_normal((M, n_in)).astype(np.float32)
     w = dev.upload(sa.Q4_K, n_out, n_in, W)
@@ -116,11 +119,20 @@ def test_gemm_config3_sampled_rows(dev, oracle):
         Y = dev.gemm(w, X)
     finally:
         w.free()
+    if M <= 512:
+        ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
+        assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
+                     f"config 3 M={M}, every output")
+        return
     rows = np.unique(np.concatenate([rng.choice(n_out, 128, replace=False),
                                      np.arange(0, n_out, 509), [0, n_out - 1]]))
     ref, L1 = oracle.gemm(sa.Q4_K, W[rows], len(rows), n_in, X)
     assert_close(Y[:, rows].reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
-                 "config 3 sampled rows")
+                 f"config 3 M={M} sampled rows")
+    cols = np.array([0, 37, M // 2 + 5, M - 1])
+    ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X[cols])
+    assert_close(Y[cols].reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
+                 f"config 3 M={M} every row of activation rows {cols.tolist()}")
 
 
 @pytest.mark.parametrize("wt", [sa.Q2_K, sa.Q3_K, sa.Q5_K], ids=lambda t: sa.NAMES[t])

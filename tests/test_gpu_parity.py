@@ -138,8 +138,8 @@ def test_gemv_f32_vs_oracle(dev, oracle, wt):
         w.free()
 
 
-@pytest.mark.parametrize("wt", [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.Q8_0, sa.Q5_0, sa.F16],
-                         ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("wt", [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.Q8_0, sa.Q5_0, sa.Q4_0,
+                                sa.F16, sa.F32], ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("M", [1, 3, 8, 13])
 def test_gemm_small_M_vs_oracle(dev, oracle, wt, M):
     rng = np.random.default_rng(2000 + wt * 31 + M)
