@@ -197,6 +197,17 @@ class Reference:
                 f.restype = None
         L.ref_shim_gemv.argtypes = [_u32, _vp, _i64, _i64, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp]
         L.ref_shim_gemv.restype = ctypes.c_int
+        L.ref_shim_gguf_open.argtypes = [ctypes.c_char_p]
+        L.ref_shim_gguf_open.restype = _vp
+        L.ref_shim_gguf_close.argtypes = [_vp]
+        L.ref_shim_errstr.restype = ctypes.c_char_p
+        L.ref_shim_gguf_tensor.argtypes = [_vp, ctypes.c_char_p, _vp, _vp]
+        L.ref_shim_gguf_map_offset.argtypes = [_vp, _vp]
+        L.ref_shim_gguf_map_offset.restype = _i64
+        L.ref_shim_gguf_alignment.argtypes = [_vp]
+        L.ref_shim_gguf_alignment.restype = ctypes.c_uint64
+        L.ref_shim_tensor_gemv.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int]
+        L.ref_shim_tensor_row.argtypes = [_vp, ctypes.c_uint64, _vp]
         L.si_expf.argtypes = [ctypes.c_float]
         L.si_expf.restype = ctypes.c_float
         L.si_softmax.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_float]
@@ -290,6 +301,40 @@ class Reference:
             sc_all[h, :n] = sc
             pr_all[h, :n] = pr16
         return out, sc_all, pr_all
+
+    # GGUF container through the reference parser; tensor views are
+    # si_tensor structs at caller-owned addresses (t_addr)
+    def gguf_open(self, path: str) -> int:
+        g = self.L.ref_shim_gguf_open(path.encode())
+        if not g:
+            raise OSError(f"reference si_gguf_open({path}): {self.L.ref_shim_errstr().decode()}")
+        return g
+
+    def gguf_close(self, g: int) -> None:
+        self.L.ref_shim_gguf_close(g)
+
+    def gguf_tensor(self, g: int, name: str, be: int | None, t_addr: int) -> int:
+        return self.L.ref_shim_gguf_tensor(g, name.encode(), be, t_addr)
+
+    def gguf_map_offset(self, g: int, p: int) -> int:
+        return self.L.ref_shim_gguf_map_offset(g, p)
+
+    def gguf_alignment(self, g: int) -> int:
+        return self.L.ref_shim_gguf_alignment(g)
+
+    def tensor_size(self) -> int:
+        return self.L.ref_shim_tensor_size()
+
+    def tensor_gemv(self, t_addr: int, x: np.ndarray, n_out: int, lanes: int = LANES):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(n_out, dtype=np.float32)
+        self.L.ref_shim_tensor_gemv(t_addr, _ptr(x), _ptr(y), n_out, lanes)
+        return y
+
+    def tensor_row(self, t_addr: int, row: int, n: int):
+        out = np.zeros(n, dtype=np.float32)
+        self.L.ref_shim_tensor_row(t_addr, row, _ptr(out))
+        return out
 
     def gemv_timed(self, wtype: int, W: np.ndarray, n_out: int, n_in: int, x: np.ndarray,
                    lanes: int, reps: int):

@@ -200,6 +200,14 @@ int si_backend_hip_upload(si_backend *be, const si_tensor *w) {
     return SI_OK;
 }
 
+int si_backend_hip_place(si_backend *be, si_tensor *w) {
+    const int rc = si_backend_hip_upload(be, w);
+    if (rc) return rc;
+    w->loc = SI_LOC_DEVICE;
+    w->be = be;
+    return SI_OK;
+}
+
 int si_backend_hip_weights(const si_backend *be, uint64_t *device_bytes) {
     const hip_backend *hb = (const hip_backend *)be;
     uint64_t total = 0;

@@ -62,6 +62,17 @@ int si_backend_hip_gemm(si_backend *be, const si_tensor *w, const float *X, int6
  * si_errstr() set. */
 int si_backend_hip_upload(si_backend *be, const si_tensor *w);
 
+/* Make w resident on the device and assign it to this backend: uploads it
+ * as si_backend_hip_upload does, then sets w->loc = SI_LOC_DEVICE and
+ * w->be = be. w->data keeps the mmap pointer: it stays the key of the
+ * device copy and the source row_to_f32 reads (the model must keep its
+ * si_gguf open, as for the CPU backend). The model loader's hook for the
+ * tensors of layers assigned to this backend and for the output head
+ * (reference model.c:171; the engine then reaches them through
+ * m->layer_be[il] and m->output.be). On failure w is left untouched. SI_OK
+ * or a negative SI_* code with si_errstr() set. */
+int si_backend_hip_place(si_backend *be, si_tensor *w);
+
 /* Number of weight tensors uploaded so far and their device bytes. */
 int si_backend_hip_weights(const si_backend *be, uint64_t *device_bytes);
 

@@ -8,10 +8,12 @@
  *   si_set_err, si_errstr           reference include/siphon/common.h:36-38
  *   si_tp (opaque lane pool)        reference include/siphon/threadpool.h:19
  *   si_backend_cpu                  reference include/siphon/tensor.h:58
- * The reference has no device location yet (tensor.h:25-29 leaves
- * SI_LOC_DEVICE for a later backend); the adapter needs none: weights stay
- * SI_LOC_HOST (the mmap remains the source of every upload) and its
- * backend is tagged SI_LOC_HOST because gemv takes and returns host
+ * plus the one line a Siphon tree adds to support this backend:
+ *   SI_LOC_DEVICE = 2               the device location the reference leaves
+ *                                   for a later backend (tensor.h:25-29);
+ *                                   si_backend_hip_place tags the tensors it
+ *                                   made resident with it.
+ * The backend itself stays tagged SI_LOC_HOST: gemv takes and returns host
  * arrays. */
 #ifndef SI_MIRROR_H
 #define SI_MIRROR_H
@@ -32,6 +34,7 @@ enum {
 typedef enum {
     SI_LOC_NONE = 0,
     SI_LOC_HOST = 1,
+    SI_LOC_DEVICE = 2,
 } si_loc;
 
 typedef struct si_tp si_tp;

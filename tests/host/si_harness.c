@@ -94,3 +94,32 @@ int th_upload(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, cons
     const si_tensor t = make_tensor(be, type, n_out, n_in, data, bytes);
     return si_backend_hip_upload(be, &t);
 }
+
+/* ---- tensor views made by the reference loader (GGUF end-to-end) ---- */
+
+int th_tensor_size(void) { return (int)sizeof(si_tensor); }
+
+int th_place(si_backend *be, si_tensor *t) {
+    g_err[0] = 0;
+    return si_backend_hip_place(be, t);
+}
+
+/* The routed engine's calls: through the backend the tensor is assigned to
+ * (t->be), as m->layer_be[il]->gemv, m->output.be->gemv and
+ * m->tok_embd.be->row_to_f32 would. Return 0, or -1 with th_errstr() set. */
+int th_tensor_gemv(const si_tensor *t, const float *x, float *y, int64_t n) {
+    g_err[0] = 0;
+    t->be->gemv(t->be, t, x, y, n, NULL);
+    return g_err[0] ? -1 : 0;
+}
+
+int th_tensor_row(const si_tensor *t, uint64_t row, float *out) {
+    g_err[0] = 0;
+    t->be->row_to_f32(t->be, t, row, out);
+    return g_err[0] ? -1 : 0;
+}
+
+int th_tensor_gemm(si_backend *be, const si_tensor *t, const float *X, int64_t M, float *Y) {
+    g_err[0] = 0;
+    return si_backend_hip_gemm(be, t, X, M, Y);
+}

@@ -10,6 +10,16 @@ HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "host")
 SO = os.path.join(HERE, "libsi_harness.so")
 
 
+SI_LOC_NONE, SI_LOC_HOST, SI_LOC_DEVICE = 0, 1, 2
+
+
+class SiTensor(ctypes.Structure):
+    """si_tensor (reference include/siphon/tensor.h:33-41)."""
+    _fields_ = [("type", ctypes.c_uint32), ("ne", ctypes.c_uint64 * 4),
+                ("n_elems", ctypes.c_uint64), ("n_bytes", ctypes.c_uint64),
+                ("data", ctypes.c_void_p), ("loc", ctypes.c_int), ("be", ctypes.c_void_p)]
+
+
 class Harness:
     def __init__(self):
         subprocess.run(["make", "-s", "-C", HERE], check=True)
@@ -25,6 +35,11 @@ class Harness:
         L.th_row_to_f32.argtypes = [vp, u32, u64, u64, vp, u64, u64, vp]
         L.th_weights.argtypes = [vp, ctypes.POINTER(u64)]
         L.th_upload.argtypes = [vp, u32, u64, u64, vp, u64]
+        tp = ctypes.POINTER(SiTensor)
+        L.th_place.argtypes = [vp, tp]
+        L.th_tensor_gemv.argtypes = [tp, vp, vp, i64]
+        L.th_tensor_row.argtypes = [tp, u64, vp]
+        L.th_tensor_gemm.argtypes = [vp, tp, vp, i64, vp]
         self.L = L
 
     def errstr(self) -> str:
@@ -60,3 +75,18 @@ class Harness:
         b = ctypes.c_uint64()
         n = self.L.th_weights(be, ctypes.byref(b))
         return n, b.value
+
+    def tensor_size(self) -> int:
+        return self.L.th_tensor_size()
+
+    def place(self, be, t: SiTensor) -> int:
+        return self.L.th_place(be, ctypes.byref(t))
+
+    def tensor_gemv(self, t: SiTensor, x, y, n) -> int:
+        return self.L.th_tensor_gemv(ctypes.byref(t), x.ctypes.data, y.ctypes.data, n)
+
+    def tensor_row(self, t: SiTensor, row, out) -> int:
+        return self.L.th_tensor_row(ctypes.byref(t), row, out.ctypes.data)
+
+    def tensor_gemm(self, be, t: SiTensor, X, Y) -> int:
+        return self.L.th_tensor_gemm(be, ctypes.byref(t), X.ctypes.data, X.shape[0], Y.ctypes.data)

@@ -47,7 +47,7 @@ def edge_vectors(rng, n):
 def assert_close(y, ref, l1, what):
     err = np.abs(y.astype(np.float64) - ref)
     bound = TOL_REL * l1 + TOL_ABS
-    bad = np.nonzero(err > bound)[0]
+    bad = np.nonzero(~(err <= bound))[0]  # NaN fails
     assert bad.size == 0, (f"{what}: {bad.size} outputs out of tolerance, first row {bad[0]}: "
                            f"gpu {y[bad[0]]} ref {ref[bad[0]]} l1 {l1[bad[0]]}")
 
