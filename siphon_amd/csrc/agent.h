@@ -13,4 +13,62 @@ __device__ inline float load_agent_f32(__amdgpu_buffer_rsrc_t r, uint32_t byte_o
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 16));
 }
 
+// End of a K-sliced GEMM tile, after each wave of the workgroup has issued
+// its agent-scope stores of the slice's partial sums into
+// part[(slice * Mp + m) * ldp + n]: count the workgroup's arrival on *cnt;
+// the last of the S workgroups of the tile adds the S partial tiles in
+// slice order (so the result does not depend on arrival order) into
+// y[m * ldy + n] for the tile's rows m0 .. m0 + BM - 1 below M and columns
+// n0 .. n0 + BN - 1 below n_out, and resets the counter to zero for the
+// next launch. Rows past M were not written and are not read.
+//
+// Ordering: each wave's partial-sum stores have completed (vmcnt 0) before
+// the barrier and hence before the arrival is counted; the last
+// workgroup's agent-scope loads are issued after the barrier that follows
+// the count's return. The signal fences keep the compiler from moving
+// memory operations across these points (they emit no instruction).
+template <int BM, int BN, int THREADS>
+__device__ inline void slices_finish(const float *part, uint32_t *cnt, int S, int64_t Mp,
+                                     int64_t ldp, int64_t m0, int64_t M, int64_t n0,
+                                     int64_t n_out, float *y, int64_t ldy) {
+    __shared__ uint32_t last_flag;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)S - 1;
+    __syncthreads();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (!last_flag) return;
+    // this thread's outputs: rows m0 + idx / BN, columns n0 + idx % BN for
+    // idx = tid + THREADS q; all loads of one slice are issued together
+    constexpr int kOut = BM * BN / THREADS;
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(part), (short)0, (int)((int64_t)S * Mp * ldp * 4), 0x00020000);
+    const int64_t nn = n0 + threadIdx.x % BN;
+    float v[kOut];
+#pragma unroll
+    for (int q = 0; q < kOut; q++) v[q] = 0.0f;
+    for (int sl = 0; sl < S; sl++) {
+        float pv[kOut];
+#pragma unroll
+        for (int q = 0; q < kOut; q++) {
+            const int64_t m = m0 + (threadIdx.x + THREADS * q) / BN;
+            // rows past M were not written: read row 0's value, unused
+            pv[q] = load_agent_f32(pr, (uint32_t)((((int64_t)sl * Mp + (m < M ? m : 0)) * ldp + nn) * 4));
+        }
+#pragma unroll
+        for (int q = 0; q < kOut; q++) v[q] += pv[q];
+    }
+    if (nn < n_out) {
+#pragma unroll
+        for (int q = 0; q < kOut; q++) {
+            const int64_t m = m0 + (threadIdx.x + THREADS * q) / BN;
+            if (m < M) y[m * ldy + nn] = v[q];
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace sihip

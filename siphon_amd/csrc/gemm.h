@@ -688,50 +688,9 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kq_kernel(GemmArgs A) {
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
     }
-    // Ordering: each wave's partial-sum stores have completed (vmcnt 0) before
-    // the barrier and hence before the arrival is counted; the last
-    // workgroup's sc1 loads are issued after the barrier that follows the
-    // count's return. The signal fences keep the compiler from moving memory
-    // operations across these points (they emit no instruction).
-    __shared__ uint32_t last_flag;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    uint32_t *cnt = A.cnt + (int64_t)mblk * A.NB + nblk;
-    if (threadIdx.x == 0)
-        last_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (uint32_t)A.S - 1;
-    __syncthreads();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (!last_flag) return;
-    // this thread's outputs: rows m0 + idx / BN, columns nblk * BN + idx % BN
-    // for idx = tid + 256 q; all loads of one slice are issued together
-    constexpr int kOut = kGemmBM * kGemmBN / kGemmThreads;
-    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-        A.part, (short)0, (int)((int64_t)A.S * A.Mp * ldp * 4), 0x00020000);
-    const int64_t nn = (int64_t)nblk * kGemmBN + threadIdx.x % kGemmBN;
-    float v[kOut];
-#pragma unroll
-    for (int q = 0; q < kOut; q++) v[q] = 0.0f;
-    for (int sl = 0; sl < A.S; sl++) {
-        float pv[kOut];
-#pragma unroll
-        for (int q = 0; q < kOut; q++) {
-            const int64_t m = m0 + (threadIdx.x + kGemmThreads * q) / kGemmBN;
-            // rows past M were not written: read row 0's value, unused
-            pv[q] = load_agent_f32(pr, (uint32_t)((((int64_t)sl * A.Mp + (m < A.M ? m : 0)) * ldp + nn) * 4));
-        }
-#pragma unroll
-        for (int q = 0; q < kOut; q++) v[q] += pv[q];
-    }
-    if (nn < A.n_out) {
-#pragma unroll
-        for (int q = 0; q < kOut; q++) {
-            const int64_t m = m0 + (threadIdx.x + kGemmThreads * q) / kGemmBN;
-            if (m < A.M) A.y[m * A.ldy + nn] = v[q];
-        }
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    slices_finish<kGemmBM, kGemmBN, kGemmThreads>(A.part, A.cnt + (int64_t)mblk * A.NB + nblk, A.S,
+                                                 A.Mp, ldp, m0, A.M, (int64_t)nblk * kGemmBN,
+                                                 A.n_out, A.y, A.ldy);
 }
 
 }  // namespace sihip

@@ -21,6 +21,7 @@
 #include "gemm.h"
 #include "f32w.h"
 #include "gemm2.h"
+#include "gemm6.h"
 #include "matvec.h"
 #include "quant.h"
 
@@ -38,7 +39,8 @@ struct Options {
     int64_t gemm_mt = -1;      // GEMM m-tile rows / 32 (rule: by M)
     int64_t gemm_sbk = -1;     // GEMM K-slice length in super-blocks, 0: none (rule: by tiles)
     int64_t gemm2_min_m = -1;  // smallest M on the 16x16 Q4_K GEMM (rule: kGemm2MinM)
-    int64_t gemm2_waves = -1;  // waves per SIMD of the 16x16 Q4_K GEMM, 1 or 2 (rule: 2)
+    int64_t gemm2_waves = -1;  // waves per SIMD of the 16x16 GEMMs, 1 or 2 (rule: 2)
+    int64_t gemm6_min_m = -1;  // smallest M on the Q6_K GEMM (rule: kGemm6MinM)
 };
 
 struct OptionName {
@@ -51,7 +53,7 @@ static const OptionName kOptionNames[] = {
     {"SPLIT_ELEMS", &Options::split_elems}, {"TILE_COLS", &Options::tile_cols},
     {"GEMM_MIN_M", &Options::gemm_min_m}, {"GEMM_MT", &Options::gemm_mt},
     {"GEMM_SBK", &Options::gemm_sbk},     {"GEMM2_MIN_M", &Options::gemm2_min_m},
-    {"GEMM2_WAVES", &Options::gemm2_waves},
+    {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
 };
 
 struct sihip_ctx {
@@ -90,8 +92,9 @@ struct sihip_weight {
     uint8_t *dev;
     uint8_t *gemm = nullptr;  // GEMM-ordered copy, built on the first prefill call
     int64_t gemm_bytes = 0;
-    // Q4_K: the copy of the 16x16 matrix-core GEMM (gemm2.h) and its
-    // exponent E (the min operand holds -dmin * mn * 2^E)
+    // Q4_K and Q6_K: the copy of the 16x16 matrix-core GEMM of the type
+    // (gemm2.h, gemm6.h); Q4_K: its exponent E (the min operand holds
+    // -dmin * mn * 2^E)
     uint8_t *gemm2 = nullptr;
     int64_t gemm2_bytes = 0;
     int gexp = 0;
@@ -698,8 +701,12 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 static int64_t gemm_min_m(const Options &o) { return o.gemm_min_m > 0 ? o.gemm_min_m : 5; }
 
 static bool gemm_mfma_supported(uint32_t type) {
-    return type == T_Q4_K || type == T_Q5_K || type == T_Q2_K || type == T_Q3_K;
+    return type == T_Q4_K || type == T_Q5_K || type == T_Q2_K || type == T_Q3_K || type == T_Q6_K;
 }
+
+// Types whose 32x32 GEMM copy exists (gemm.h); Q6_K runs only on its 16x16
+// kernel (gemm6.h).
+static bool gemm32_supported(uint32_t type) { return gemm_mfma_supported(type) && type != T_Q6_K; }
 
 // The weight's copy in the GEMM's order (gemm_layout_kernel), built from
 // its matvec copy on stream st.
@@ -730,24 +737,30 @@ static int build_gemm_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     return SIHIP_OK;
 }
 
-// Q4_K: the weight's copy in the order of the 16x16 GEMM (gemm2.h).
+// Q4_K and Q6_K: the weight's copy in the order of the type's 16x16 GEMM
+// (gemm2.h, gemm6.h).
 static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     if (capturing(st))
         return set_err(ctx, SIHIP_EINVAL,
                        "the weight's GEMM copy would be built during graph capture: call "
                        "sihip_weight_prepare_gemm before capturing");
     const Layout &L = w->L;
+    const bool q6 = L.type == T_Q6_K;
     const int64_t nb = L.n_in / 256;
     const int64_t nblk32 = (L.n_out + kG2BN - 1) / kG2BN * (kG2BN / 32);
-    const int64_t bytes = gemm2_layout_bytes(nblk32, nb);
+    const int64_t bytes = q6 ? gemm6_layout_bytes(nblk32, nb) : gemm2_layout_bytes(nblk32, nb);
     uint8_t *g = nullptr;
     hipError_t e = hipMalloc(&g, (size_t)bytes);
     if (e != hipSuccess)
         return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
                        hipGetErrorString(e));
-    const int64_t threads = nblk32 * nb * (kG2ChunkQ4K / 16);
-    hipLaunchKernelGGL(gemm2_layout_q4k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
-                       L, (const uint8_t *)w->dev, g, nblk32, std::ldexp(1.0f, w->gexp));
+    const int64_t threads = nblk32 * nb * ((q6 ? kG6Chunk : kG2ChunkQ4K) / 16);
+    if (q6)
+        hipLaunchKernelGGL(gemm6_layout_q6k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           st, L, (const uint8_t *)w->dev, g, nblk32);
+    else
+        hipLaunchKernelGGL(gemm2_layout_q4k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           st, L, (const uint8_t *)w->dev, g, nblk32, std::ldexp(1.0f, w->gexp));
     e = hipGetLastError();
     if (e != hipSuccess) {
         (void)hipFree(g);
@@ -762,11 +775,11 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
     if (!ctx || !w) return set_err(ctx, SIHIP_EINVAL, "weight_prepare_gemm: NULL argument");
     if (!gemm_mfma_supported(w->L.type)) return SIHIP_OK;
     HIP_OK(ctx, hipSetDevice(ctx->device));
-    if (!w->gemm) {
+    if (gemm32_supported(w->L.type) && !w->gemm) {
         const int rc = build_gemm_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
-    if (w->L.type == T_Q4_K && !w->gemm2) {
+    if ((w->L.type == T_Q4_K || w->L.type == T_Q6_K) && !w->gemm2) {
         const int rc = build_gemm2_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
@@ -781,10 +794,18 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
 constexpr int64_t kGemm2MinM = 384;
 static int64_t gemm2_min_m(const Options &o) { return o.gemm2_min_m > 0 ? o.gemm2_min_m : kGemm2MinM; }
 
+// Smallest M that takes the Q6_K GEMM (gemm6.h); option GEMM6_MIN_M. Up to
+// 4 columns the matvec kernel streams the 6.56-bit GGUF bytes once, less
+// traffic than the GEMM's 2-byte digit copy; from 5 it would stream them
+// twice or more (ffn_down 4096 x 14336 at M = 8: 44.8 us on the matvec
+// kernel, 34.4 us on the GEMM).
+constexpr int64_t kGemm6MinM = 5;
+static int64_t gemm6_min_m(const Options &o) { return o.gemm6_min_m > 0 ? o.gemm6_min_m : kGemm6MinM; }
+
 // Shape of one matrix-core GEMM call: tile height, padded rows, workspace
 // sizes and K slices.
 struct GemmPlan {
-    bool v2;           // the 16x16 Q4_K kernel (gemm2.h); mt then counts its 16-row m tiles
+    bool v2;           // a 16x16 kernel (Q4_K: gemm2.h, Q6_K: gemm6.h); mt counts 16-row m tiles
     int mt;            // 32-row MFMA tiles per wave along m
     int64_t Mp;        // M rounded up to the workgroup's rows
     int64_t ws_bytes;  // quantized activation planes
@@ -796,6 +817,37 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     GemmPlan p;
     const int64_t K = L.n_in, nb = K / 256;
     const int64_t NB = (L.n_out + kGemmBN - 1) / kGemmBN;
+    if (L.type == T_Q6_K) {
+        // m blocks of 16, 32 or 64 rows (the GEMM_MT option, 1, 2 or 4,
+        // overrides); K slices when the output tiles give fewer than two
+        // workgroups per CU, at least 2 super-blocks per slice (the GEMM_SBK
+        // option overrides, 0: none)
+        p.v2 = true;
+        p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+        if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4)
+            p.mt = (int)ctx->opt.gemm_mt;
+        const int64_t BM = 16 * p.mt;
+        p.Mp = (M + BM - 1) / BM * BM;
+        p.ws_bytes = p.Mp / BM * nb * g2_rec_bytes((int)BM);
+        const int64_t tiles = (p.Mp / BM) * NB;
+        const int64_t want = 2 * ctx->n_cu;
+        int64_t sbk = 0;
+        if (tiles < want) {
+            int64_t S = (want + tiles - 1) / tiles;
+            if (S > nb / 2) S = nb / 2;
+            if (S > 1) sbk = (nb + S - 1) / S;
+        }
+        if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
+        p.S = 1;
+        p.SBK = (int)nb;
+        p.part_bytes = 0;
+        if (sbk > 0 && sbk < nb && tiles <= kGemmCounters) {
+            p.S = (int)((nb + sbk - 1) / sbk);
+            p.SBK = (int)sbk;
+            p.part_bytes = (int64_t)p.S * p.Mp * NB * kG2BN * (int64_t)sizeof(float);
+        }
+        return p;
+    }
     if (L.type == T_Q4_K && M >= gemm2_min_m(ctx->opt)) {
         // 128-row m blocks; the GEMM_MT option (2, 4 or 8) overrides
         p.v2 = true;
@@ -883,10 +935,50 @@ static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, uint8_t
     return hipGetLastError();
 }
 
+template <int MT>
+static hipError_t launch_gemm6(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
+                               const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
+                               hipStream_t st) {
+    constexpr int BM = 16 * MT;
+    const Layout &L = w->L;
+    const int64_t nb = L.n_in / 256;
+    const int64_t blocks = p.Mp * nb;
+    hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)), dim3(kG2Threads),
+                       0, st, X, ldx, M, p.Mp, nb, B.ws);
+    G6Args A;
+    A.w = w->gemm2;
+    A.x = B.ws;
+    A.y = Y;
+    A.ldy = ldy;
+    A.n_out = L.n_out;
+    A.M = M;
+    A.Mp = p.Mp;
+    A.nb = (int)nb;
+    A.MB = (int)(p.Mp / BM);
+    A.NB = (int)((L.n_out + kG2BN - 1) / kG2BN);
+    A.S = p.S;
+    A.SBK = p.SBK;
+    A.part = p.S > 1 ? B.part : nullptr;
+    A.cnt = p.S > 1 ? B.cnt : nullptr;
+    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
+    hipLaunchKernelGGL((gemm6_q6k_kernel<MT>), grid, dim3(kG2Threads), 0, st, A);
+    return hipGetLastError();
+}
+
 static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPlan &p,
                             const GemmBufs &B, const float *X, int64_t ldx, int64_t M, float *Y,
                             int64_t ldy, hipStream_t st) {
     const Layout &L = w->L;
+    if (p.v2 && L.type == T_Q6_K) {
+        hipError_t e;
+        switch (p.mt) {
+            case 1: e = launch_gemm6<1>(w, p, B, X, ldx, M, Y, ldy, st); break;
+            case 2: e = launch_gemm6<2>(w, p, B, X, ldx, M, Y, ldy, st); break;
+            default: e = launch_gemm6<4>(w, p, B, X, ldx, M, Y, ldy, st); break;
+        }
+        if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+        return SIHIP_OK;
+    }
     if (p.v2) {
         hipError_t e;
         const bool w1 = ctx->opt.gemm2_waves == 1;
@@ -981,6 +1073,7 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
 // Prefill dispatch: MFMA GEMM where supported and M is large enough,
 // otherwise the matvec kernel over column groups.
 static bool gemm_on_mfma(const sihip_ctx *ctx, const sihip_weight *w, int64_t M) {
+    if (w->L.type == T_Q6_K) return M >= gemm6_min_m(ctx->opt);
     return gemm_mfma_supported(w->L.type) && M >= gemm_min_m(ctx->opt);
 }
 

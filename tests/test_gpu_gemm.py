@@ -1,6 +1,6 @@
-"""GPU parity of the prefill GEMM on the matrix cores (Q4_K, Q5_K, Q2_K and
-Q3_K weights x Q8_K rows) against the oracle, to the same tolerance as the matvec:
-|gpu - ref| <= 1e-5 * sum|terms| + 1e-6 per output."""
+"""GPU parity of the prefill GEMM on the matrix cores (Q4_K, Q5_K, Q2_K, Q3_K
+and Q6_K weights x Q8_K rows) against the oracle, to the same tolerance as the
+matvec: |gpu - ref| <= 1e-5 * sum|terms| + 1e-6 per output."""
 import numpy as np
 import pytest
 
@@ -20,7 +20,13 @@ def _rows(rng, M, n_in):
     return X
 
 
-MFMA_TYPES = [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K]
+MFMA_TYPES = [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K]
+
+
+def _force_mfma(option):
+    """The matrix-core path at every M (Q6_K has a threshold of its own)."""
+    option("GEMM_MIN_M", "1")
+    option("GEMM6_MIN_M", "1")
 
 
 def _extreme_q2k(W, n_out, n_in):
@@ -45,6 +51,19 @@ def _extreme_q3k(W, n_out, n_in):
     return W
 
 
+def _extreme_q6k(W, n_out, n_in):
+    """Q6_K rows 0-3 at the ends of the digit operands: scales -128 and 127
+    against quants 0 and 63, so v = (q - 32) * sc takes 4096, 3937, -3968 and
+    -4064 (digits hi = 32, lo = 0 up to hi = -32, lo = 32)."""
+    blk = W.reshape(n_out, n_in // 256, 210)
+    for row, (scale_byte, quant_byte) in enumerate([(0x80, 0x00), (0x7F, 0xFF), (0x80, 0xFF),
+                                                    (0x7F, 0x00)]):
+        if row < n_out:
+            blk[row, :, 0:192] = quant_byte  # ql and qh
+            blk[row, :, 192:208] = scale_byte
+    return W
+
+
 def _extreme_q5k(W, n_out, n_in):
     """Q5_K rows 0-1 with every 6-bit scale and min 63 (sh = sl = 7) and
     every quant 31 or 0: operand bytes sh * q - 128 = 89 and -128."""
@@ -62,7 +81,7 @@ def _extreme_q5k(W, n_out, n_in):
     (129, 768, 65),
 ])
 def test_gemm_mfma_vs_oracle(dev, oracle, option, wt, n_out, n_in, M):
-    option("GEMM_MIN_M", "1")  # the MFMA path even for tiny M
+    _force_mfma(option)  # the MFMA path even for tiny M
     rng = np.random.default_rng(n_out * 7 + n_in + M + wt)
     W = synth.make_weights(wt, n_out, n_in, rng)
     if wt == sa.Q2_K:
@@ -71,6 +90,8 @@ def test_gemm_mfma_vs_oracle(dev, oracle, option, wt, n_out, n_in, M):
         W = _extreme_q3k(W, n_out, n_in)
     if wt == sa.Q5_K:
         W = _extreme_q5k(W, n_out, n_in)
+    if wt == sa.Q6_K:
+        W = _extreme_q6k(W, n_out, n_in)
     X = _rows(rng, M, n_in)
     w = dev.upload(wt, n_out, n_in, W)
     try:
@@ -86,7 +107,7 @@ def test_gemm_mfma_vs_oracle(dev, oracle, option, wt, n_out, n_in, M):
 @pytest.mark.parametrize("G", [1, 4, 16, 64])
 def test_gemm_mfma_every_tile_width(dev, oracle, option, wt, G):
     """The GEMM reads the matvec layout of any tile width."""
-    option("GEMM_MIN_M", "1")
+    _force_mfma(option)
     option("TILE_COLS", str(G))
     rng = np.random.default_rng(900 + G + wt)
     n_out, n_in, M = 300, 1792, 40
@@ -164,7 +185,7 @@ def test_gemm_k_slices(dev, oracle, option, wt, mt, sbk):
     several m tiles, a ragged last n tile): every slicing and tile height
     within tolerance of the oracle, and a repeated call gives the same bits
     (the last slice of each tile resets its arrival counter)."""
-    option("GEMM_MIN_M", "1")
+    _force_mfma(option)
     option("GEMM_MT", str(mt))
     option("GEMM_SBK", str(sbk))
     rng = np.random.default_rng(1100 + 10 * mt + sbk + 1000 * wt)
@@ -189,9 +210,9 @@ def test_gemm_k_slices(dev, oracle, option, wt, mt, sbk):
 def test_prepare_gemm_matches_lazy_copy(dev, oracle):
     """sihip_weight_prepare_gemm builds the GEMM copies at once (device bytes
     grow by them, a second call adds nothing; Q4_K has two, one per GEMM
-    kernel, and a lazy call builds only the one it uses); a later gemm gives
-    the bits of a weight whose copy its first gemm built. Other types: a
-    no-op."""
+    kernel, and a lazy call builds only the one it uses; Q6_K has one); a
+    later gemm gives the bits of a weight whose copy its first gemm built.
+    Types without a matrix-core GEMM: a no-op."""
     rng = np.random.default_rng(4242)
     n_out, n_in, M = 700, 2048, 40
     W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
@@ -199,6 +220,8 @@ def test_prepare_gemm_matches_lazy_copy(dev, oracle):
     eager, lazy = dev.upload(sa.Q4_K, n_out, n_in, W), dev.upload(sa.Q4_K, n_out, n_in, W)
     W6 = synth.make_weights(sa.Q6_K, 64, 512, rng)
     w6 = dev.upload(sa.Q6_K, 64, 512, W6)
+    W8 = synth.make_weights(sa.Q8_0, 64, 512, rng)
+    w8 = dev.upload(sa.Q8_0, 64, 512, W8)
     try:
         before = eager.device_bytes
         eager.prepare_gemm()
@@ -214,9 +237,12 @@ def test_prepare_gemm_matches_lazy_copy(dev, oracle):
                      f"prepared gemm {n_out}x{n_in} M={M}")
         b6 = w6.device_bytes
         w6.prepare_gemm()
-        assert w6.device_bytes == b6
+        assert w6.device_bytes > b6
+        b8 = w8.device_bytes
+        w8.prepare_gemm()
+        assert w8.device_bytes == b8
     finally:
-        for w in (eager, lazy, w6):
+        for w in (eager, lazy, w6, w8):
             w.free()
 
 
@@ -259,3 +285,50 @@ def test_gemm2_q4k_vs_oracle(dev, oracle, option, n_out, n_in, M, mt, huge):
     what = f"gemm2 Q4_K {n_out}x{n_in} M={M} MT={mt}"
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
     assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
+
+
+@pytest.mark.parametrize("n_out,n_in,M", [(4096, 14336, 512), (1024, 4096, 512), (4096, 14336, 8),
+                                          (1024, 4096, 8), (4096, 14336, 64)])
+def test_gemm6_q6k_bench_shapes(dev, oracle, option, n_out, n_in, M):
+    """The Q6_K GEMM (gemm6.h) at the 8B layer's Q6_K shapes (ffn_down and
+    wv), M = 512, 64 and 8 (below its default threshold, forced): every
+    output against the oracle, and a repeat gives the same bits (K slices
+    reset their counters)."""
+    option("GEMM6_MIN_M", "1")
+    rng = np.random.default_rng(n_out + n_in + M)
+    W = _extreme_q6k(synth.make_weights(sa.Q6_K, n_out, n_in, rng), n_out, n_in)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(sa.Q6_K, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+        Y2 = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(sa.Q6_K, W, n_out, n_in, X)
+    what = f"gemm6 Q6_K {n_out}x{n_in} M={M}"
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
+    assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
+
+
+@pytest.mark.parametrize("n_out,n_in,M,mt,sbk", [
+    (333, 2816, 70, 4, -1), (4096, 1280, 384, 4, -1), (129, 768, 65, 2, 0),
+    (200, 1024, 16, 1, 1), (1000, 512, 130, 4, 0), (130, 4096, 257, 4, 3), (300, 3072, 40, 2, 5),
+])
+def test_gemm6_q6k_tiles(dev, oracle, option, n_out, n_in, M, mt, sbk):
+    """The Q6_K GEMM at every m-tile count (1, 2, 4), with and without K
+    slices (ragged last slice), ragged M and n_out, rows at the ends of its
+    operand range."""
+    option("GEMM6_MIN_M", "1")
+    option("GEMM_MT", str(mt))
+    option("GEMM_SBK", str(sbk))
+    rng = np.random.default_rng(7 * n_out + n_in + M + mt)
+    W = _extreme_q6k(synth.make_weights(sa.Q6_K, n_out, n_in, rng), n_out, n_in)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(sa.Q6_K, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(sa.Q6_K, W, n_out, n_in, X)
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
+                 f"gemm6 Q6_K {n_out}x{n_in} M={M} MT={mt} SBK={sbk}")

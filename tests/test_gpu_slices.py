@@ -57,6 +57,7 @@ def test_sliced_calls_repeat_bit_exact(dev, oracle, option, wt):
     and batched columns, each against the oracle, and the first activation
     again at the end gives the same bits."""
     option("GEMM_MIN_M", "1000")  # batches take the matvec kernel
+    option("GEMM6_MIN_M", "1000")
     option("TILE_COLS", "4")  # several rounds per tile (the default is 1 here)
     rng = np.random.default_rng(950 + wt)
     n_out, n_in = 300, 9216

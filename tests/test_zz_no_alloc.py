@@ -1,7 +1,10 @@
 """sihip_gemm_dev_noalloc: the GEMM entry point that allocates nothing (its
 workspaces are a static device scratch). It runs the kernels of
-sihip_gemm_dev, so its outputs must equal that entry point's bit for bit;
-each case makes two calls in a row, the second with fewer rows, so a
+sihip_gemm_dev, so its outputs must equal that entry point's bit for bit,
+except where the K-slice partial sums of sihip_gemm_dev would not fit the
+scratch: then it runs the tile unsliced, which adds the same terms in
+another f32 order, and both are checked against the oracle to the path's
+bar. Each case makes two calls in a row, the second with fewer rows, so a
 leftover of the first call in the shared scratch (activation planes,
 partial sums, arrival counters) would show in the second."""
 import ctypes
@@ -12,6 +15,7 @@ import pytest
 import siphon_amd as sa
 from siphon_amd import synth
 
+from .test_gpu_parity import assert_close
 from .test_gpu_slices import _HipGraph, bits
 
 pytestmark = pytest.mark.gpu
@@ -35,19 +39,23 @@ def _gemm_both(dev, w, X):
 
 # (type, n_out, n_in, first M, second M): the config-3 shape on the matrix
 # cores, K-sliced small batches, the matvec path (M below the matrix-core
-# threshold) and a format without a matrix-core path
+# threshold), a format without a matrix-core path and the Q6_K GEMM with K
+# slices; the last case's slices do not fit the scratch at M = 512
 CASES = [
     (sa.Q4_K, 14336, 4096, 512, 96),
     (sa.Q2_K, 3072, 5120, 16, 8),
     (sa.Q5_K, 1000, 2048, 70, 33),
     (sa.Q4_K, 2048, 4096, 4, 2),
     (sa.Q6_K, 1024, 4096, 8, 3),
+    (sa.Q6_K, 1024, 4096, 64, 20),
+    (sa.Q6_K, 4096, 14336, 512, 40),
 ]
+UNSLICED = {(sa.Q6_K, 4096, 14336, 512)}  # (type, n_out, n_in, M) run unsliced
 
 
 @pytest.mark.parametrize("wt,n_out,n_in,M1,M2", CASES,
                          ids=[f"{sa.NAMES[c[0]]}-{c[1]}x{c[2]}-M{c[3]}-{c[4]}" for c in CASES])
-def test_noalloc_matches_gemm_dev(dev, wt, n_out, n_in, M1, M2):
+def test_noalloc_matches_gemm_dev(dev, oracle, wt, n_out, n_in, M1, M2):
     print(f"noalloc {sa.NAMES[wt]} {n_out}x{n_in} M={M1} then {M2}", flush=True)
     rng = np.random.default_rng(n_out + n_in + M1)
     W = synth.make_weights(wt, n_out, n_in, rng)
@@ -58,6 +66,12 @@ def test_noalloc_matches_gemm_dev(dev, wt, n_out, n_in, M1, M2):
             X = rng.standard_normal((M, n_in)).astype(np.float32)
             ya, yb = _gemm_both(dev, w, X)
             assert not np.isnan(ya).any()
+            if (wt, n_out, n_in, M) in UNSLICED:
+                ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+                for y, what in ((ya, "gemm_dev"), (yb, "noalloc")):
+                    assert_close(y.reshape(-1), ref.reshape(-1).astype(np.float64),
+                                 L1.reshape(-1), f"{sa.NAMES[wt]} M={M} {what}")
+                continue
             assert np.array_equal(bits(ya), bits(yb)), \
                 f"{sa.NAMES[wt]} M={M}: noalloc differs from gemm_dev"
     finally:
