@@ -58,16 +58,19 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemm", action="store_true", help="skip the M=512 GEMM")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the M=512 prefill pass over the 32 layers")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--unfused", action="store_true",
                     help="one launch per matrix instead of fused q/k/v and gate/up launches")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-format matvec measurements (configs 0, 1, 4)")
     ap.add_argument("--no-attn", action="store_true", help="skip the decode attention")
-    ap.add_argument("--profile", choices=("gemm", "traffic", "configs", "attn"),
+    ap.add_argument("--profile", choices=("gemm", "traffic", "configs", "attn", "prefill"),
                     help="run one workload for a profiler and exit: the GEMM M sweep, "
                          "a 64 MiB copy plus 12 gate/up launches (HBM counter runs), "
-                         "the per-format matvec measurements, or the decode attention")
+                         "the per-format matvec measurements, the decode attention, or "
+                         "the M=512 prefill pass over 32 layers")
     return ap.parse_args()
 
 
@@ -109,6 +112,9 @@ def main():
         stream = torch.cuda.Stream()
         if args.profile == "gemm":
             out = bench_gemm(dev, torch, stream, rng)
+        elif args.profile == "prefill":
+            layers, _ = build_layers(dev, rng, 0)
+            out = bench_prefill_pass(dev, torch, stream, layers)
         elif args.profile == "configs":
             out = bench_configs(dev, torch, stream, rng)
         elif args.profile == "attn":
@@ -245,6 +251,8 @@ def main():
 
     if not args.no_gemm:
         result["gemm_m512"] = bench_gemm(dev, torch, stream, rng)
+    if not args.no_prefill:
+        result["prefill_pass"] = bench_prefill_pass(dev, torch, stream, layers)
     if not args.no_attn:
         result["attention"] = bench_attention(dev, torch, stream)
     if not args.no_configs:
@@ -359,7 +367,7 @@ def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
     M = 512
     X = torch.randn(M, n_in, device="cuda")
     Y = torch.empty(M, n_out, device="cuda")
-    for wt in (sa.Q5_K, sa.Q2_K, sa.Q3_K):
+    for wt in (sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K):
         Wf = synth.make_weights(wt, n_out, n_in, rng)
         wf = [dev.upload(wt, n_out, n_in, Wf) for _ in range(-(-rotate_bytes // Wf.nbytes) + 1)]
         with torch.cuda.stream(stream):
@@ -387,6 +395,88 @@ def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
             "us_per_call": head["us_per_call"], "sweep": sweep, "other_formats_m512": formats,
             "roofline": {"bound": "mfma", "achieved": head["TOPS"], "peak": INT8_PEAK_TOPS,
                          "unit": "TOP/s", "frac": head["frac_int8_peak"]}}
+
+
+def bench_prefill_pass(dev, torch, stream, layers, M=512, reps=5):
+    """Prefill of a 512-token prompt through the 32 decode-pass layers: the
+    7 matrices of each layer in engine order, each one gemm_dev call on
+    M = 512 activation rows (N(0,1), resident in HBM), 224 calls in one HIP
+    graph. The GEMM copies are built first, as load-time placement builds
+    them. TOPS = 2 M x (weights' n_out x n_in summed) / pass time; per
+    matrix kind, its 32 calls in a graph of their own give the average call
+    time (activation quantization included)."""
+    import siphon_amd as sa
+    from siphon_amd import synth
+    sp = stream.cuda_stream
+    for l in layers:
+        for w in l.values():
+            w.prepare_gemm()
+    names = [n for (n, _, _, _) in synth.LLAMA3_8B_LAYER]
+    X = {n_in: torch.randn(M, n_in, device="cuda") for n_in in (4096, 14336)}
+    Y = {n: torch.empty(M, layers[0][n].n_out, device="cuda") for n in names}
+
+    def calls(il, name):
+        w = layers[il][name]
+        dev.gemm_dev(w, X[w.n_in].data_ptr(), M, Y[name].data_ptr(), sp)
+
+    def run_pass():
+        for il in range(N_LAYERS):
+            for n in names:
+                calls(il, n)
+
+    with torch.cuda.stream(stream):
+        run_pass()
+    torch.cuda.synchronize()
+    eager = {n: y.clone() for n, y in Y.items()}
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run_pass()
+    for _ in range(2):  # replays must reproduce the eager results exactly
+        g.replay()
+        torch.cuda.synchronize()
+        for n in names:
+            assert torch.equal(Y[n], eager[n]), f"prefill graph replay differs on {n}"
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        with torch.cuda.stream(stream):
+            g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pass_ms = e0.elapsed_time(e1) / reps
+    ops = sum(2.0 * M * w.n_out * w.n_in for l in layers for w in l.values())
+    tops = ops / (pass_ms * 1e-3) / 1e12
+    del g
+    per = {}
+    for n in names:
+        gn = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gn, stream=stream):
+            for il in range(N_LAYERS):
+                calls(il, n)
+        gn.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            with torch.cuda.stream(stream):
+                gn.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * N_LAYERS)
+        w = layers[0][n]
+        t = 2.0 * M * w.n_out * w.n_in / (us * 1e-6) / 1e12
+        per[n] = {"type": sa.NAMES[w.type],
+                  "shape": [w.n_out, w.n_in], "us_per_call": round(us, 1), "TOPS": round(t, 1),
+                  "frac_int8_peak": round(t / INT8_PEAK_TOPS, 4)}
+        del gn
+    dom = max(per, key=lambda k: per[k]["us_per_call"])
+    return {"M": M, "layers": N_LAYERS, "calls_per_pass": N_LAYERS * len(names),
+            "ms_per_pass": round(pass_ms, 3), "TOPS": round(tops, 1),
+            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+            "tokens_per_s": round(M / (pass_ms * 1e-3), 1),
+            "per_matrix": per,
+            "roofline": {"kernel": f"{dom} GEMM ({per[dom]['type']})", "bound": "mfma",
+                         "achieved": per[dom]["TOPS"], "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                         "frac": per[dom]["frac_int8_peak"]}}
 
 
 def _config_shapes():

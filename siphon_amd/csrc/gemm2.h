@@ -37,6 +37,7 @@
 // which is unit 2 ks + g / 2, elements 16 (g % 2) + slot of the unit.
 #pragma once
 
+#include "agent.h"
 #include "formats.h"
 #include "quant.h"
 #include "unit.h"
@@ -198,9 +199,16 @@ struct G2Args {
     const uint8_t *x;     // activation records [MB][nb]
     float *y;             // Y[m * ldy + n]
     int64_t ldy;
-    int64_t n_out, M;
+    int64_t n_out, M, Mp;
     int nb, MB, NB;       // super-blocks; m blocks of BM rows; n blocks of 128 rows
     float yscale;         // 2^-E
+    // K slices: S == 1, one workgroup per output tile; S > 1, slice s covers
+    // super-blocks [s SBK, (s + 1) SBK) and its partial sums (already scaled
+    // by 2^-E) go to part[(s Mp + m) * NB * 128 + n], the tile's arrivals to
+    // cnt[mblk * NB + nblk] (zero between launches)
+    int S, SBK;
+    float *part;
+    uint32_t *cnt;
 };
 
 // q * f bytewise for bytes and products below 256 (no carries between
@@ -221,12 +229,16 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     constexpr int kPieces = kRec / 1024;
     __shared__ __attribute__((aligned(16))) uint8_t sx[2][kRec];
     // XCD-aware order: workgroups go round-robin over the 8 XCDs, so the m
-    // blocks of one n block (which read the same weights) are consecutive
-    // workgroups of one XCD and share its L2
+    // blocks and slices of one n block (which read the same weights) are
+    // consecutive workgroups of one XCD and share its L2
     const int b = blockIdx.x;
     const int xcd = b & 7, t = b >> 3;
-    const int nblk = (t / A.MB) * 8 + xcd, mblk = t % A.MB;
+    const int per = A.MB * A.S;
+    const int nblk = (t / per) * 8 + xcd, rest = t % per;
+    const int slice = rest / A.MB, mblk = rest % A.MB;
     if (nblk >= A.NB) return;
+    const int c0 = slice * A.SBK;
+    const int c1 = c0 + A.SBK < A.nb ? c0 + A.SBK : A.nb;  // this slice's super-blocks
     // wave index as a scalar: the buffer resources below derive from it
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -288,10 +300,10 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
         for (int nt = 0; nt < 2; nt++) y[mt][nt] = (v4f2_t){0.0f, 0.0f, 0.0f, 0.0f};
 
     Raw raw;
-    dma(0, 0);
-    load_w(0, raw);
-    for (int c = 0; c < A.nb; c++) {
-        const int buf = c & 1;
+    dma(c0, 0);
+    load_w(c0, raw);
+    for (int c = c0; c < c1; c++) {
+        const int buf = (c - c0) & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         // decode this super-block's operands
@@ -316,7 +328,7 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
         // the next super-block's record and weights, a whole super-block
         // ahead; unconditional (the last super-block loads itself again), so
         // the registers of the prefetch are the ones decoded next
-        const int cn = c + 1 < A.nb ? c + 1 : c;
+        const int cn = c + 1 < c1 ? c + 1 : c;
         dma(cn, buf ^ 1);
         load_w(cn, raw);
         const uint8_t *X = sx[buf];
@@ -362,7 +374,25 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     // without per-element tests
     const int64_t n0 = (int64_t)nblk * kG2BN + 32 * wave;
     const int64_t m0 = (int64_t)mblk * BM;
-    const bool full = n0 + 32 <= A.n_out && m0 + BM <= A.M;
+    if (A.S == 1) {
+        const bool full = n0 + 32 <= A.n_out && m0 + BM <= A.M;
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int64_t n = n0 + 16 * nt + r16;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int64_t m = m0 + 16 * mt + 4 * g + i;
+                    if (full || (m < A.M && n < A.n_out)) A.y[m * A.ldy + n] = y[mt][nt][i] * A.yscale;
+                }
+        }
+        return;
+    }
+    // K slices: partial sums through agent-scope stores (they write through
+    // and are read past the per-XCD L2s), then the tile's arrival and the
+    // last workgroup's slice-order sum
+    const int64_t ldp = (int64_t)A.NB * kG2BN;
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
         const int64_t n = n0 + 16 * nt + r16;
@@ -371,9 +401,14 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int64_t m = m0 + 16 * mt + 4 * g + i;
-                if (full || (m < A.M && n < A.n_out)) A.y[m * A.ldy + n] = y[mt][nt][i] * A.yscale;
+                if (m < A.M)
+                    __hip_atomic_store(A.part + ((int64_t)slice * A.Mp + m) * ldp + n,
+                                       y[mt][nt][i] * A.yscale, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
             }
     }
+    slices_finish<BM, kG2BN, kG2Threads>(A.part, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, A.Mp,
+                                         ldp, m0, A.M, (int64_t)nblk * kG2BN, A.n_out, A.y, A.ldy);
 }
 
 }  // namespace sihip

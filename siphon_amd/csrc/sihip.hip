@@ -813,53 +813,67 @@ struct GemmPlan {
     int64_t part_bytes;
 };
 
+// K slices of the 16x16 GEMMs: when the output tiles would fill at most
+// half of the workgroup slots (each kernel runs two workgroups per CU), the
+// super-blocks of a tile are split over S workgroups, enough for two per
+// CU, at least 2 super-blocks each; the GEMM_SBK option overrides (0:
+// none). Above half the slots, the partial sums' extra traffic costs more
+// than the idle slots.
+static void plan_slices(const sihip_ctx *ctx, GemmPlan &p, int64_t tiles, int64_t nb, int64_t NB) {
+    const int64_t want = 2 * ctx->n_cu;
+    int64_t sbk = 0;
+    if (2 * tiles <= want) {
+        int64_t S = (want + tiles - 1) / tiles;
+        if (S > nb / 2) S = nb / 2;
+        if (S > 1) sbk = (nb + S - 1) / S;
+    }
+    if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
+    p.S = 1;
+    p.SBK = (int)nb;
+    p.part_bytes = 0;
+    if (sbk > 0 && sbk < nb && tiles <= kGemmCounters) {
+        p.S = (int)((nb + sbk - 1) / sbk);
+        p.SBK = (int)sbk;
+        p.part_bytes = (int64_t)p.S * p.Mp * NB * kG2BN * (int64_t)sizeof(float);
+    }
+}
+
 static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     GemmPlan p;
     const int64_t K = L.n_in, nb = K / 256;
     const int64_t NB = (L.n_out + kGemmBN - 1) / kGemmBN;
     if (L.type == T_Q6_K) {
         // m blocks of 16, 32 or 64 rows (the GEMM_MT option, 1, 2 or 4,
-        // overrides); K slices when the output tiles give fewer than two
-        // workgroups per CU, at least 2 super-blocks per slice (the GEMM_SBK
-        // option overrides, 0: none)
+        // overrides); K slices as plan_slices decides
+        // (shorter m blocks while the output tiles would not reach half the
+        // CUs: Q6_K wv 1024 x 4096 at M = 512, 24.5 us in 32-row blocks
+        // against 28.1 us in 64-row blocks with more K slices)
         p.v2 = true;
         p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+        while (p.mt > 1 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu / 2) p.mt /= 2;
         if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4)
             p.mt = (int)ctx->opt.gemm_mt;
         const int64_t BM = 16 * p.mt;
         p.Mp = (M + BM - 1) / BM * BM;
         p.ws_bytes = p.Mp / BM * nb * g2_rec_bytes((int)BM);
-        const int64_t tiles = (p.Mp / BM) * NB;
-        const int64_t want = 2 * ctx->n_cu;
-        int64_t sbk = 0;
-        if (tiles < want) {
-            int64_t S = (want + tiles - 1) / tiles;
-            if (S > nb / 2) S = nb / 2;
-            if (S > 1) sbk = (nb + S - 1) / S;
-        }
-        if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
-        p.S = 1;
-        p.SBK = (int)nb;
-        p.part_bytes = 0;
-        if (sbk > 0 && sbk < nb && tiles <= kGemmCounters) {
-            p.S = (int)((nb + sbk - 1) / sbk);
-            p.SBK = (int)sbk;
-            p.part_bytes = (int64_t)p.S * p.Mp * NB * kG2BN * (int64_t)sizeof(float);
-        }
+        plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB);
         return p;
     }
     if (L.type == T_Q4_K && M >= gemm2_min_m(ctx->opt)) {
-        // 128-row m blocks; the GEMM_MT option (2, 4 or 8) overrides
+        // 128-row m blocks, shorter ones (64, 32 rows) while the output
+        // tiles would not reach one per CU, then K slices (plan_slices); the
+        // GEMM_MT option (2, 4 or 8) overrides. At M = 512: 4096 x 4096 in
+        // 64-row blocks 35.0 us (128-row: 55.4), 1024 x 4096 in 32-row
+        // blocks 21.2 us (128-row: 46.5).
         p.v2 = true;
         p.mt = 8;
-        if (ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4)
+        while (p.mt > 2 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu) p.mt /= 2;
+        if (ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4 || ctx->opt.gemm_mt == 8)
             p.mt = (int)ctx->opt.gemm_mt;
         const int64_t BM = 16 * p.mt;
         p.Mp = (M + BM - 1) / BM * BM;
         p.ws_bytes = p.Mp / BM * nb * g2_rec_bytes((int)BM);
-        p.S = 1;
-        p.SBK = (int)nb;
-        p.part_bytes = 0;
+        plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB);
         return p;
     }
     p.v2 = false;
@@ -910,9 +924,10 @@ struct GemmBufs {
 // Y[m, :] = W x[m, :] for m < M on the matrix cores, with the workspaces
 // in B (sized by plan_gemm); the weight's GEMM copy must exist.
 template <int MT, int W>
-static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, uint8_t *ws,
+static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
                                const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
                                hipStream_t st) {
+    uint8_t *ws = B.ws;
     constexpr int BM = 16 * MT;
     const Layout &L = w->L;
     const int64_t nb = L.n_in / 256;
@@ -926,11 +941,16 @@ static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, uint8_t
     A.ldy = ldy;
     A.n_out = L.n_out;
     A.M = M;
+    A.Mp = p.Mp;
     A.nb = (int)nb;
     A.MB = (int)(p.Mp / BM);
     A.NB = (int)((L.n_out + kG2BN - 1) / kG2BN);
     A.yscale = std::ldexp(1.0f, -w->gexp);
-    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB));
+    A.S = p.S;
+    A.SBK = p.SBK;
+    A.part = p.S > 1 ? B.part : nullptr;
+    A.cnt = p.S > 1 ? B.cnt : nullptr;
+    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
     hipLaunchKernelGGL((gemm2_q4k_kernel<MT, W>), grid, dim3(kG2Threads), 0, st, A);
     return hipGetLastError();
 }
@@ -983,11 +1003,11 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
         hipError_t e;
         const bool w1 = ctx->opt.gemm2_waves == 1;
         switch (p.mt) {
-            case 2: e = launch_gemm2<2, 2>(w, p, B.ws, X, ldx, M, Y, ldy, st); break;
-            case 4: e = w1 ? launch_gemm2<4, 1>(w, p, B.ws, X, ldx, M, Y, ldy, st)
-                           : launch_gemm2<4, 2>(w, p, B.ws, X, ldx, M, Y, ldy, st); break;
-            default: e = w1 ? launch_gemm2<8, 1>(w, p, B.ws, X, ldx, M, Y, ldy, st)
-                            : launch_gemm2<8, 2>(w, p, B.ws, X, ldx, M, Y, ldy, st); break;
+            case 2: e = launch_gemm2<2, 2>(w, p, B, X, ldx, M, Y, ldy, st); break;
+            case 4: e = w1 ? launch_gemm2<4, 1>(w, p, B, X, ldx, M, Y, ldy, st)
+                           : launch_gemm2<4, 2>(w, p, B, X, ldx, M, Y, ldy, st); break;
+            default: e = w1 ? launch_gemm2<8, 1>(w, p, B, X, ldx, M, Y, ldy, st)
+                            : launch_gemm2<8, 2>(w, p, B, X, ldx, M, Y, ldy, st); break;
         }
         if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
         return SIHIP_OK;

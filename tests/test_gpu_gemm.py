@@ -262,16 +262,19 @@ def _extreme_q4k(W, n_out, n_in, huge_dmin):
     return W
 
 
-@pytest.mark.parametrize("n_out,n_in,M,mt,huge", [
-    (200, 1024, 16, 8, False), (333, 2048, 130, 8, True), (1000, 256, 100, 4, False),
-    (129, 768, 65, 2, True), (130, 4096, 257, 8, False), (4096, 1280, 384, 8, True),
+@pytest.mark.parametrize("n_out,n_in,M,mt,huge,sbk", [
+    (200, 1024, 16, 8, False, -1), (333, 2048, 130, 8, True, -1), (1000, 256, 100, 4, False, -1),
+    (129, 768, 65, 2, True, -1), (130, 4096, 257, 8, False, -1), (4096, 1280, 384, 8, True, -1),
+    (4096, 1280, 384, 8, False, 0), (333, 2816, 130, 4, True, 3), (1024, 4096, 512, 8, False, -1),
 ])
-def test_gemm2_q4k_vs_oracle(dev, oracle, option, n_out, n_in, M, mt, huge):
+def test_gemm2_q4k_vs_oracle(dev, oracle, option, n_out, n_in, M, mt, huge, sbk):
     """The 16x16 Q4_K GEMM (gemm2.h) forced at every M, m-tile count 2, 4
-    and 8, ragged M and n_out, one super-block per row, and rows at the ends
-    of its operand ranges, against the oracle."""
+    and 8, with K slices as planned, none, and 3 super-blocks per slice
+    (ragged last slice), ragged M and n_out, one super-block per row, and
+    rows at the ends of its operand ranges, against the oracle."""
     option("GEMM2_MIN_M", "1")
     option("GEMM_MT", str(mt))
+    option("GEMM_SBK", str(sbk))
     rng = np.random.default_rng(n_out + 3 * n_in + M + mt)
     W = _extreme_q4k(synth.make_weights(sa.Q4_K, n_out, n_in, rng), n_out, n_in, huge)
     X = _rows(rng, M, n_in)
@@ -282,7 +285,7 @@ def test_gemm2_q4k_vs_oracle(dev, oracle, option, n_out, n_in, M, mt, huge):
     finally:
         w.free()
     ref, L1 = oracle.gemm(sa.Q4_K, W, n_out, n_in, X)
-    what = f"gemm2 Q4_K {n_out}x{n_in} M={M} MT={mt}"
+    what = f"gemm2 Q4_K {n_out}x{n_in} M={M} MT={mt} SBK={sbk}"
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
     assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
 
