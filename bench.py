@@ -66,11 +66,12 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-format matvec measurements (configs 0, 1, 4)")
     ap.add_argument("--no-attn", action="store_true", help="skip the decode attention")
-    ap.add_argument("--profile", choices=("gemm", "traffic", "configs", "attn", "prefill"),
+    ap.add_argument("--profile", choices=("gemm", "traffic", "configs", "attn", "prefill", "calib"),
                     help="run one workload for a profiler and exit: the GEMM M sweep, "
                          "a 64 MiB copy plus 12 gate/up launches (HBM counter runs), "
-                         "the per-format matvec measurements, the decode attention, or "
-                         "the M=512 prefill pass over 32 layers")
+                         "the per-format matvec measurements, the decode attention, "
+                         "the M=512 prefill pass over 32 layers, or the HBM calibration "
+                         "(a 4 GiB streaming read and the decode pass's launches read-only)")
     return ap.parse_args()
 
 
@@ -112,6 +113,8 @@ def main():
         stream = torch.cuda.Stream()
         if args.profile == "gemm":
             out = bench_gemm(dev, torch, stream, rng)
+        elif args.profile == "calib":
+            out = profile_calibration(dev, torch, stream)
         elif args.profile == "prefill":
             layers, _ = build_layers(dev, rng, 0)
             out = bench_prefill_pass(dev, torch, stream, layers)
@@ -548,6 +551,75 @@ def bench_configs(dev, torch, stream, rng, rotate_bytes=512 << 20):
             w.free()
         out[label] = entry
     return out
+
+
+def profile_calibration(dev, torch, stream, reps=10):
+    """HBM ceilings the decode pass is measured against, with the library's
+    read-only probe kernel (sihip_probe_read_dev):
+    - one streaming read of 4 GiB per launch: the rate HBM gives a long
+      read;
+    - the decode pass's launch structure with nothing but reads: per layer
+      four launches of the q/k/v, wo, gate/up and down weight bytes of the
+      Llama-3-8B Q4_K_M layer, 32 layers over consecutive slices of one
+      4.44 GB buffer (past the 256 MB MALL), 128 launches in one HIP graph.
+    Each time is the average over `reps` launches or graph replays, with
+    HIP events on the launch stream."""
+    import siphon_amd as sa
+    from siphon_amd import synth
+    sp = stream.cuda_stream
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    big = 4 << 30
+    buf = torch.ones(big // 4, dtype=torch.int32, device="cuda")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    dev.probe_read_dev(buf.data_ptr(), big, sink.data_ptr(), sp)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        dev.probe_read_dev(buf.data_ptr(), big, sink.data_ptr(), sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / reps
+    stream_gbs = big / t / 1e9
+    del buf
+    shapes = {n: (wt, o, i) for (n, wt, o, i) in synth.LLAMA3_8B_LAYER}
+    wb = {n: sa.row_bytes(wt, i) * o for n, (wt, o, i) in shapes.items()}
+    groups = [("qkv", ("wq", "wk", "wv")), ("wo", ("wo",)), ("gate_up", ("ffn_gate", "ffn_up")),
+              ("down", ("ffn_down",))]
+    sizes = [sum(wb[n] for n in names) for _, names in groups]
+    layer_bytes = sum(sizes)
+    buf = torch.ones((N_LAYERS * layer_bytes + 4095) // 4, dtype=torch.int32, device="cuda")
+    base = buf.data_ptr()
+
+    def run_pass():
+        off = 0
+        for _ in range(N_LAYERS):
+            for nb in sizes:
+                dev.probe_read_dev(base + off, nb, sink.data_ptr(), sp)
+                off += nb
+
+    with torch.cuda.stream(stream):
+        run_pass()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run_pass()
+    g.replay()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        with torch.cuda.stream(stream):
+            g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pass_ms = e0.elapsed_time(e1) / reps
+    pass_gbs = N_LAYERS * layer_bytes / (pass_ms * 1e-3) / 1e9
+    del g, buf
+    return {"stream_read": {"bytes": big, "ms": round(t * 1e3, 3), "GB/s": round(stream_gbs, 1),
+                            "hbm_frac": round(stream_gbs / HBM_PEAK_GBS, 4)},
+            "pass_read_only": {"launches": N_LAYERS * len(sizes), "bytes": N_LAYERS * layer_bytes,
+                               "launch_bytes": dict(zip([g[0] for g in groups], sizes)),
+                               "ms": round(pass_ms, 4), "GB/s": round(pass_gbs, 1),
+                               "hbm_frac": round(pass_gbs / HBM_PEAK_GBS, 4)}}
 
 
 def profile_traffic(dev, torch, stream, rng):

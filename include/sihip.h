@@ -223,6 +223,16 @@ int sihip_convert_f16(sihip_ctx *ctx, const float *x, void *out, int64_t n);
 int sihip_vec_dot(sihip_ctx *ctx, uint32_t wtype, int n, float *s,
                   const void *x, const void *y);
 
+/* Calibration, with no counterpart in the reference: one streaming read
+ * of `bytes` bytes at p (device memory, 16-byte aligned, bytes a multiple
+ * of 16) in one launch, nothing written unless a folded checksum of the
+ * data hits a fixed 32-bit value (then one word per workgroup goes to
+ * sink, which must hold 4096 words). It measures the HBM rate a launch
+ * that only reads that many bytes reaches, the ceiling the matvec
+ * launches are compared with. */
+int sihip_probe_read_dev(sihip_ctx *ctx, const void *p, uint64_t bytes, uint32_t *sink,
+                         void *stream);
+
 /* Matvec over n_rows consecutive weight rows (host bytes) against a
  * pair-format activation (host bytes): the per-row dot of many rows in one
  * launch, used by parity tests with the reference's own quantized input. */

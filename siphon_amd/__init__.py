@@ -77,6 +77,7 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_gemv_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
     L.sihip_dequant_row.argtypes = [_vp, _vp, _u64, _vp]
     L.sihip_dequant_rows_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _i64, _vp]
+    L.sihip_probe_read_dev.argtypes = [_vp, _vp, _u64, _vp, _vp]
     L.sihip_attn_decode_dev.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                         ctypes.c_float, _vp, _vp, _vp, _vp]
     L.sihip_gemm_dev.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
@@ -196,6 +197,9 @@ class Device:
         out = np.zeros(w.n_in, dtype=np.float32)
         self._check(self.L.sihip_dequant_row(self.ctx, w.handle, row, _ptr(out)))
         return out
+
+    def probe_read_dev(self, p: int, nbytes: int, sink_ptr: int, stream: int | None = None):
+        self._check(self.L.sihip_probe_read_dev(self.ctx, p, nbytes, sink_ptr, stream))
 
     def dequant_rows_dev(self, w: Weight, row0: int, nrows: int, out_ptr: int, ldo: int,
                          stream: int | None = None):

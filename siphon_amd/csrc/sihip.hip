@@ -1128,6 +1128,47 @@ static hipError_t launch_dequant(const Layout &L, const uint8_t *w, int64_t row0
     return hipGetLastError();
 }
 
+// ---- calibration -------------------------------------------------------------------
+
+// Streaming read: a grid-stride loop over 16-byte words, four loads in
+// flight per thread, the words folded by xor; the fold is stored only when
+// it hits a fixed value, so the reads cannot be dropped and nothing else is
+// written.
+__global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *p, int64_t n16,
+                                                         uint32_t *sink) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^
+               d.z ^ d.w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (acc == 0x5eed1e55u) sink[blockIdx.x] = acc;
+}
+
+extern "C" int sihip_probe_read_dev(sihip_ctx *ctx, const void *p, uint64_t bytes, uint32_t *sink,
+                                    void *stream) {
+    if (!ctx || !p || !sink) return set_err(ctx, SIHIP_EINVAL, "probe_read_dev: NULL argument");
+    if (bytes == 0 || bytes % 16 || !aligned16(p))
+        return set_err(ctx, SIHIP_EINVAL, "probe_read_dev: p and bytes must be 16-byte aligned");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const int64_t n16 = (int64_t)(bytes / 16);
+    // at least four words per thread, at most 8 workgroups per CU (and the
+    // 4096 words of sink)
+    int64_t wg = (n16 + 1023) / 1024;
+    const int64_t cap = std::min<int64_t>(8 * (int64_t)ctx->n_cu, 4096);
+    if (wg > cap) wg = cap;
+    hipLaunchKernelGGL(probe_read_kernel, dim3((unsigned)wg), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4 *)p, n16, sink);
+    HIP_OK(ctx, hipGetLastError());
+    return SIHIP_OK;
+}
+
 extern "C" int sihip_dequant_rows_dev(sihip_ctx *ctx, const sihip_weight *w, uint64_t row0,
                                       uint64_t nrows, float *out, int64_t ldo, void *stream) {
     if (!ctx || !w || !out) return set_err(ctx, SIHIP_EINVAL, "dequant_rows_dev: NULL argument");
