@@ -1130,25 +1130,27 @@ static hipError_t launch_dequant(const Layout &L, const uint8_t *w, int64_t row0
 
 // ---- calibration -------------------------------------------------------------------
 
-// Streaming read: a grid-stride loop over 16-byte words, four loads in
-// flight per thread, the words folded by xor; the fold is stored only when
-// it hits a fixed value, so the reads cannot be dropped and nothing else is
-// written.
+// Streaming read: a grid-stride loop over 16-byte words with the
+// nontemporal hint (as the matvec's weight loads), four loads in flight per
+// thread, the words folded by xor; the fold is stored only when it hits a
+// fixed value, so the reads cannot be dropped and nothing else is written.
 __global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *p, int64_t n16,
                                                          uint32_t *sink) {
+    typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+    const v4u_t *q = reinterpret_cast<const v4u_t *>(p);
     const int64_t stride = (int64_t)gridDim.x * 256;
     int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    uint32_t acc = 0;
+    v4u_t acc = {0, 0, 0, 0};
     for (; i + 3 * stride < n16; i += 4 * stride) {
-        const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
-        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^
-               d.z ^ d.w;
+        const v4u_t a = __builtin_nontemporal_load(q + i);
+        const v4u_t b = __builtin_nontemporal_load(q + i + stride);
+        const v4u_t c = __builtin_nontemporal_load(q + i + 2 * stride);
+        const v4u_t d = __builtin_nontemporal_load(q + i + 3 * stride);
+        acc ^= a ^ b ^ c ^ d;
     }
-    for (; i < n16; i += stride) {
-        const uint4 a = p[i];
-        acc ^= a.x ^ a.y ^ a.z ^ a.w;
-    }
-    if (acc == 0x5eed1e55u) sink[blockIdx.x] = acc;
+    for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(q + i);
+    const uint32_t f = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (f == 0x5eed1e55u) sink[blockIdx.x] = f;
 }
 
 extern "C" int sihip_probe_read_dev(sihip_ctx *ctx, const void *p, uint64_t bytes, uint32_t *sink,

@@ -114,9 +114,10 @@ SIHD inline T ldp(const uint8_t *p) {
 }
 
 // Load a T of weight-plane data from p with the nontemporal hint: weights
-// stream through once per launch, so they should not displace cached lines
-// (activations, LDS spill-free data). Measured on a plain 4 GiB read: 6.5
-// TB/s with the hint against 6.0 without, at two workgroups per CU.
+// stream through once per launch. Used where one load instruction of a wave
+// reads whole consecutive records (64 lanes x T bytes, full lines). Measured
+// on a plain 4 GiB read: 6.5 TB/s with the hint against 6.0 without, at
+// two workgroups per CU.
 template <typename T>
 SIHD inline T ldw(const uint8_t *p) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -203,12 +204,16 @@ SIHD inline void load_unit(const Planes &P, uint32_t rec, Raw &w) {
         w.f = ldw<uint32_t>(P.p[1] + rec * 4u);
         w.e = ldw<uint16_t>(P.p[2] + rec * 2u);
     } else if constexpr (FMT == T_Q8_0) {
-        w.a = ldw<U4>(P.p[0] + rec * 32u);
-        w.b = ldw<U4>(P.p[0] + rec * 32u + 16u);
+        // 32- and 64-byte records read 16 bytes at a time: each load covers
+        // part of every line, so the lines must stay cached for the next
+        // load (no nontemporal hint: F16 ffn_up 27648 x 5120 took 91 us
+        // with it, 56 without)
+        w.a = ldp<U4>(P.p[0] + rec * 32u);
+        w.b = ldp<U4>(P.p[0] + rec * 32u + 16u);
         w.e = ldw<uint16_t>(P.p[1] + rec * 2u);
     } else {  // F16
         const uint8_t *p = P.p[0] + rec * 64u;
-        w.a = ldw<U4>(p); w.b = ldw<U4>(p + 16); w.c = ldw<U4>(p + 32); w.d = ldw<U4>(p + 48);
+        w.a = ldp<U4>(p); w.b = ldp<U4>(p + 16); w.c = ldp<U4>(p + 32); w.d = ldp<U4>(p + 48);
     }
 }
 
@@ -302,10 +307,10 @@ SIHD inline void load_kblock(const Planes &P, uint32_t urec, uint32_t brec, KRaw
         w.e = ldw<uint16_t>(P.p[3] + brec * 2u);
     }
     if constexpr (FMT == T_Q3_K) {
-        const uint8_t *sc = P.p[2] + brec * 12u;
-        w.m.x = ldw<uint32_t>(sc);
-        w.m.y = ldw<uint32_t>(sc + 4);
-        w.m.z = ldw<uint32_t>(sc + 8);
+        const uint8_t *sc = P.p[2] + brec * 12u;  // 12-byte records: as Q8_0's
+        w.m.x = ldp<uint32_t>(sc);
+        w.m.y = ldp<uint32_t>(sc + 4);
+        w.m.z = ldp<uint32_t>(sc + 8);
         w.e = ldw<uint16_t>(P.p[3] + brec * 2u);
     }
     if constexpr (FMT == T_Q2_K) {
