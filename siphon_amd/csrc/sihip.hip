@@ -56,6 +56,24 @@ static const OptionName kOptionNames[] = {
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
 };
 
+// Order of launches that share mutable device state across streams: a
+// context's GEMM and attention workspaces, a column-sliced weight's partial
+// sums and arrival counters. While all of them come on one stream nothing
+// is added. The first launch on a second stream waits for the device to
+// drain (hipDeviceSynchronize; no stream handle of an earlier call is
+// touched, since the caller may have destroyed it); from then on the state
+// carries an event recorded after each of its launches, and a launch on
+// another stream than the last one waits for that event. Launches made
+// during a graph capture are neither recorded nor made to wait: a captured
+// sequence is ordered by its graph, and its replays must not overlap eager
+// use of the same state on another stream.
+struct StreamOrder {
+    hipStream_t last = nullptr;
+    bool used = false;
+    bool multi = false;
+    hipEvent_t ev = nullptr;
+};
+
 struct sihip_ctx {
     int device;
     int n_cu;
@@ -81,6 +99,7 @@ struct sihip_ctx {
     std::vector<void *> retired;
     // this device's copy of the static scratch of sihip_gemm_dev_noalloc
     uint8_t *scratch = nullptr;
+    StreamOrder order;  // of the launches using the workspaces above
 };
 
 // Arrival counters of K-sliced GEMM tiles, allocated (and zeroed) at
@@ -104,6 +123,7 @@ struct sihip_weight {
     float *part = nullptr;
     uint32_t *cnt = nullptr;
     int64_t split_bytes = 0;
+    mutable StreamOrder order;  // of the launches using part and cnt (split > 1)
 };
 
 static char g_init_err[512];
@@ -130,6 +150,33 @@ static bool capturing(hipStream_t st) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess) return false;
     return cs != hipStreamCaptureStatusNone;
+}
+
+// Before a launch on stream st that uses the state ordered by o.
+static int order_before(sihip_ctx *ctx, StreamOrder &o, hipStream_t st) {
+    if (!o.used || o.last == st || capturing(st)) return SIHIP_OK;
+    if (!o.multi) {
+        HIP_OK(ctx, hipDeviceSynchronize());
+        HIP_OK(ctx, hipEventCreateWithFlags(&o.ev, hipEventDisableTiming));
+        o.multi = true;
+        return SIHIP_OK;
+    }
+    HIP_OK(ctx, hipStreamWaitEvent(st, o.ev, 0));
+    return SIHIP_OK;
+}
+
+// After that launch was enqueued.
+static int order_after(sihip_ctx *ctx, StreamOrder &o, hipStream_t st) {
+    if (capturing(st)) return SIHIP_OK;
+    o.used = true;
+    o.last = st;
+    if (o.multi) HIP_OK(ctx, hipEventRecord(o.ev, st));
+    return SIHIP_OK;
+}
+
+static void order_free(StreamOrder &o) {
+    if (o.ev) (void)hipEventDestroy(o.ev);
+    o = StreamOrder();
 }
 
 // A context workspace of at least `bytes`. Growing it allocates a new
@@ -230,6 +277,7 @@ extern "C" void sihip_shutdown(sihip_ctx *ctx) {
                     (void *)ctx->d_gcnt, ctx->d_attn})
         if (p) (void)hipFree(p);
     for (void *p : ctx->retired) (void)hipFree(p);
+    order_free(ctx->order);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -441,6 +489,7 @@ extern "C" int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w) {
     (void)hipFree(w->dev);
     if (w->gemm) (void)hipFree(w->gemm);
     if (w->gemm2) (void)hipFree(w->gemm2);
+    order_free(w->order);
     delete w;
     return SIHIP_OK;
 }
@@ -635,6 +684,12 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
             nwg[i] = share < 1 ? 1 : (share < want[i] ? share : want[i]);
         }
     }
+    for (int i = 0; i < count; i++) {
+        if (w[i]->split > 1) {
+            const int rc = order_before(ctx, w[i]->order, st);
+            if (rc) return rc;
+        }
+    }
     int64_t m = 0;
     while (m < M) {
         int nc = ncmax;
@@ -677,6 +732,12 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         if (e != hipSuccess)
             return set_err(ctx, SIHIP_EDEVICE, "matvec launch: %s", hipGetErrorString(e));
         m += nc;
+    }
+    for (int i = 0; i < count; i++) {
+        if (w[i]->split > 1) {
+            const int rc = order_after(ctx, w[i]->order, st);
+            if (rc) return rc;
+        }
     }
     return SIHIP_OK;
 }
@@ -1086,8 +1147,12 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
         rc = ensure(ctx, &ctx->d_gpart, &ctx->d_gpart_cap, (size_t)p.part_bytes, st);
         if (rc) return rc;
     }
+    rc = order_before(ctx, ctx->order, st);
+    if (rc) return rc;
     const GemmBufs B{(uint8_t *)ctx->d_ws, (float *)ctx->d_gpart, ctx->d_gcnt};
-    return launch_gemm_mfma(ctx, w, p, B, X, ldx, M, Y, ldy, st);
+    rc = launch_gemm_mfma(ctx, w, p, B, X, ldx, M, Y, ldy, st);
+    if (rc) return rc;
+    return order_after(ctx, ctx->order, st);
 }
 
 // Prefill dispatch: MFMA GEMM where supported and M is large enough,
@@ -1308,6 +1373,8 @@ extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint1
                   (unsigned)(n_head_kv * chunks));
     if (gs.y > 65535) return set_err(ctx, SIHIP_EINVAL, "attn_decode_dev: too many KV heads");
     const hipStream_t st = (hipStream_t)stream;
+    const int orc = order_before(ctx, ctx->order, st);
+    if (orc) return orc;
     // wide loads where rows stay aligned: keys 8 bytes, value rows 16
     const bool kvec = head_dim % 4 == 0 && (uintptr_t)k_cache % 8 == 0;
     const bool vvec = n_ctx % 8 == 0 && (uintptr_t)v_cache % 16 == 0;
@@ -1322,7 +1389,7 @@ extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint1
         hipLaunchKernelGGL(attn_pv_kernel<false>, gv, dim3(kAttnThreads), 0, st, A);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "attention launch: %s", hipGetErrorString(e));
-    return SIHIP_OK;
+    return order_after(ctx, ctx->order, st);
 }
 
 extern "C" int sihip_gemv_multi_dev(sihip_ctx *ctx, int count, const sihip_weight *const *w,
