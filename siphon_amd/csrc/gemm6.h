@@ -23,7 +23,8 @@
 // weight rows, wave w owning rows 32 w .. 32 w + 31 (two 16-column n
 // tiles); the activation record of a super-block is copied to LDS by DMA,
 // double buffered. A wave's digit operands of a super-block (64 VGPRs) are
-// loaded a whole super-block ahead into a second register set. K slices
+// reloaded K-step by K-step for the next super-block as soon as each
+// K-step's MFMAs are issued. K slices
 // (S > 1) split the super-blocks of a tile over S workgroups whose partial
 // sums are added in slice order (slices_finish), for shapes whose output
 // tiles alone would leave CUs idle.
@@ -199,62 +200,70 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm6_q6k_kernel(G6Args A) {
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) y[mt][nt] = (v4f2_t){0.0f, 0.0f, 0.0f, 0.0f};
 
-    // one super-block on the operands in cur and the record in X while the
-    // next one's are loaded into nxt and xn (unconditionally: the last
-    // super-block of the slice loads itself again, so the memory counters
-    // always hold the same loads)
-    auto step = [&](int c, const Ops &cur, Ops &nxt, const uint8_t *X, uint8_t *xn) {
+    // One super-block c on the operands in o and the record in X. K-step ks
+    // of every m tile runs before K-step ks + 1, and the next super-block's
+    // operands of K-step ks are loaded into o as soon as its MFMAs have been
+    // issued, three quarters of a step ahead of their use (all m tiles'
+    // accumulators stay live instead of a second operand set; loading a
+    // whole second set a step ahead spills at MT = 4, and MT = 4 ffn_down
+    // 4096 x 14336 at M = 512 took 114 us that way, 101 us this way). The
+    // next record is loaded at the start and written to xn at the end;
+    // loads are unconditional (the last super-block of the slice loads
+    // itself again).
+    auto step = [&](int c, Ops &o, const uint8_t *X, uint8_t *xn) {
         __syncthreads();
         const int cn = c + 1 < c1 ? c + 1 : c;
         load_x(cn);
-        // MT <= 2: the next operands load here, a whole step ahead (the
-        // barrier keeps the scheduler from sinking the loads behind the
-        // compute they overlap). MT = 4 cannot hold both operand sets in 256
-        // registers: its loads are issued at the end of the step.
-        if constexpr (MT <= 2) {
-            load_w(cn, nxt);
+        v4i2_t h[MT][2], l[MT][2];
+        const int so = cn * kG6Chunk;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const v4i2_t a = *reinterpret_cast<const v4i2_t *>(X + (4 * mt + ks) * 1024 + lane * 16);
+                const v4i2_t z = {0, 0, 0, 0};
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    h[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, o.b[ks][nt][0], ks ? h[mt][nt] : z, 0, 0, 0);
+                    l[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, o.b[ks][nt][1], ks ? l[mt][nt] : z, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int dg = 0; dg < 2; dg++)
+                    o.b[ks][nt][dg] = __builtin_bit_cast(
+                        v4i2_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                    wr, v_op, so + ((2 * ks + nt) * 2 + dg) * 1024, 0));
             __builtin_amdgcn_sched_barrier(0);
         }
-        v4i2_t a[2][4];
-        auto lds_q = [&](int mt, v4i2_t (&aa)[4]) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-                aa[ks] = *reinterpret_cast<const v4i2_t *>(X + (4 * mt + ks) * 1024 + lane * 16);
-        };
-        lds_q(0, a[0]);
+        const float d0 = o.d[0], d1 = o.d[1];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            if (mt + 1 < MT) lds_q(mt + 1, a[(mt + 1) & 1]);
             const float4 dx = *reinterpret_cast<const float4 *>(X + g2_rec_dx(BM) + (16 * mt + 4 * g) * 4);
-            const v4i2_t(&am)[4] = a[mt & 1];
-            v4i2_t h0 = {0, 0, 0, 0}, h1 = {0, 0, 0, 0}, l0 = {0, 0, 0, 0}, l1 = {0, 0, 0, 0};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                h0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], cur.b[ks][0][0], h0, 0, 0, 0);
-                l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], cur.b[ks][0][1], l0, 0, 0, 0);
-                h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], cur.b[ks][1][0], h1, 0, 0, 0);
-                l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[ks], cur.b[ks][1][1], l1, 0, 0, 0);
-            }
             const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float u0 = cur.d[0] * (float)(128 * h0[i] + l0[i]);
-                const float u1 = cur.d[1] * (float)(128 * h1[i] + l1[i]);
+                const float u0 = d0 * (float)(128 * h[mt][0][i] + l[mt][0][i]);
+                const float u1 = d1 * (float)(128 * h[mt][1][i] + l[mt][1][i]);
                 y[mt][0][i] = fma_f32(dxv[i], u0, y[mt][0][i]);
                 y[mt][1][i] = fma_f32(dxv[i], u1, y[mt][1][i]);
             }
         }
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+            o.d[nt] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(wr, v_d, so + nt * 64, 0));
         store_x(xn);
-        if constexpr (MT > 2) load_w(cn, nxt);
     };
 
-    Ops o0, o1;
+    Ops o;
     load_x(c0);
-    load_w(c0, o0);
+    load_w(c0, o);
     store_x(sx0);
     for (int c = c0; c < c1; c += 2) {
-        step(c, o0, o1, sx0, sx1);
-        if (c + 1 < c1) step(c + 1, o1, o0, sx1, sx0);
+        step(c, o, sx0, sx1);
+        if (c + 1 < c1) step(c + 1, o, sx1, sx0);
     }
 
     // result register i of lane l: row 4 (l / 16) + i of the m tile,

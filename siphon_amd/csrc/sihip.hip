@@ -906,12 +906,13 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     if (L.type == T_Q6_K) {
         // m blocks of 16, 32 or 64 rows (the GEMM_MT option, 1, 2 or 4,
         // overrides); K slices as plan_slices decides
-        // (shorter m blocks while the output tiles would not reach half the
-        // CUs: Q6_K wv 1024 x 4096 at M = 512, 24.5 us in 32-row blocks
-        // against 28.1 us in 64-row blocks with more K slices)
+        // (shorter m blocks while the output tiles would not reach a quarter
+        // of the CUs: ffn_down 4096 x 14336 at M = 64 takes 41 us in 32-row
+        // blocks against 48 us in 16-row ones, and 1024 x 4096 at M = 512
+        // the same 24 us in 64- or 32-row blocks)
         p.v2 = true;
         p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-        while (p.mt > 1 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu / 2) p.mt /= 2;
+        while (p.mt > 1 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu / 4) p.mt /= 2;
         if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4)
             p.mt = (int)ctx->opt.gemm_mt;
         const int64_t BM = 16 * p.mt;
