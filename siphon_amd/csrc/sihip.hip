@@ -22,6 +22,7 @@
 #include "f32w.h"
 #include "gemm2.h"
 #include "gemm6.h"
+#include "gemmh.h"
 #include "matvec.h"
 #include "quant.h"
 
@@ -41,6 +42,7 @@ struct Options {
     int64_t gemm2_min_m = -1;  // smallest M on the 16x16 Q4_K GEMM (rule: kGemm2MinM)
     int64_t gemm2_waves = -1;  // waves per SIMD of the 16x16 GEMMs, 1 or 2 (rule: 2)
     int64_t gemm6_min_m = -1;  // smallest M on the Q6_K GEMM (rule: kGemm6MinM)
+    int64_t gemmh_min_m = -1;  // smallest M on the F16 GEMM (rule: kGemmhMinM)
 };
 
 struct OptionName {
@@ -54,6 +56,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM_MIN_M", &Options::gemm_min_m}, {"GEMM_MT", &Options::gemm_mt},
     {"GEMM_SBK", &Options::gemm_sbk},     {"GEMM2_MIN_M", &Options::gemm2_min_m},
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
+    {"GEMMH_MIN_M", &Options::gemmh_min_m},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -761,13 +764,22 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 // force both paths).
 static int64_t gemm_min_m(const Options &o) { return o.gemm_min_m > 0 ? o.gemm_min_m : 5; }
 
-static bool gemm_mfma_supported(uint32_t type) {
-    return type == T_Q4_K || type == T_Q5_K || type == T_Q2_K || type == T_Q3_K || type == T_Q6_K;
+static bool gemm_mfma_supported(const Layout &L) {
+    const uint32_t t = L.type;
+    if (t == T_F16) return L.n_in % 128 == 0;  // steps of 128 elements
+    return t == T_Q4_K || t == T_Q5_K || t == T_Q2_K || t == T_Q3_K || t == T_Q6_K;
 }
 
-// Types whose 32x32 GEMM copy exists (gemm.h); Q6_K runs only on its 16x16
-// kernel (gemm6.h).
-static bool gemm32_supported(uint32_t type) { return gemm_mfma_supported(type) && type != T_Q6_K; }
+// Types whose 32x32 GEMM copy exists (gemm.h); Q6_K and F16 run only on
+// their 16x16 kernels (gemm6.h, gemmh.h).
+static bool gemm32_supported(const Layout &L) {
+    return gemm_mfma_supported(L) && L.type != T_Q6_K && L.type != T_F16;
+}
+
+// Types with a 16x16 GEMM copy (w->gemm2).
+static bool gemm16_supported(const Layout &L) {
+    return gemm_mfma_supported(L) && (L.type == T_Q4_K || L.type == T_Q6_K || L.type == T_F16);
+}
 
 // The weight's copy in the GEMM's order (gemm_layout_kernel), built from
 // its matvec copy on stream st.
@@ -798,30 +810,41 @@ static int build_gemm_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     return SIHIP_OK;
 }
 
-// Q4_K and Q6_K: the weight's copy in the order of the type's 16x16 GEMM
-// (gemm2.h, gemm6.h).
+// Q4_K, Q6_K and F16: the weight's copy in the order of the type's 16x16
+// GEMM (gemm2.h, gemm6.h, gemmh.h).
 static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     if (capturing(st))
         return set_err(ctx, SIHIP_EINVAL,
                        "the weight's GEMM copy would be built during graph capture: call "
                        "sihip_weight_prepare_gemm before capturing");
     const Layout &L = w->L;
-    const bool q6 = L.type == T_Q6_K;
-    const int64_t nb = L.n_in / 256;
     const int64_t nblk32 = (L.n_out + kG2BN - 1) / kG2BN * (kG2BN / 32);
-    const int64_t bytes = q6 ? gemm6_layout_bytes(nblk32, nb) : gemm2_layout_bytes(nblk32, nb);
+    int64_t bytes, threads;
+    if (L.type == T_F16) {
+        bytes = gemmh_layout_bytes(nblk32, L.n_in / 128);
+        threads = nblk32 * (L.n_in / 128) * (kGHChunk / 16);
+    } else if (L.type == T_Q6_K) {
+        bytes = gemm6_layout_bytes(nblk32, L.n_in / 256);
+        threads = nblk32 * (L.n_in / 256) * (kG6Chunk / 16);
+    } else {
+        bytes = gemm2_layout_bytes(nblk32, L.n_in / 256);
+        threads = nblk32 * (L.n_in / 256) * (kG2ChunkQ4K / 16);
+    }
     uint8_t *g = nullptr;
     hipError_t e = hipMalloc(&g, (size_t)bytes);
     if (e != hipSuccess)
         return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
                        hipGetErrorString(e));
-    const int64_t threads = nblk32 * nb * ((q6 ? kG6Chunk : kG2ChunkQ4K) / 16);
-    if (q6)
-        hipLaunchKernelGGL(gemm6_layout_q6k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                           st, L, (const uint8_t *)w->dev, g, nblk32);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (L.type == T_F16)
+        hipLaunchKernelGGL(gemmh_layout_f16, grid, dim3(256), 0, st, L, (const uint8_t *)w->dev, g,
+                           nblk32);
+    else if (L.type == T_Q6_K)
+        hipLaunchKernelGGL(gemm6_layout_q6k, grid, dim3(256), 0, st, L, (const uint8_t *)w->dev, g,
+                           nblk32);
     else
-        hipLaunchKernelGGL(gemm2_layout_q4k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                           st, L, (const uint8_t *)w->dev, g, nblk32, std::ldexp(1.0f, w->gexp));
+        hipLaunchKernelGGL(gemm2_layout_q4k, grid, dim3(256), 0, st, L, (const uint8_t *)w->dev, g,
+                           nblk32, std::ldexp(1.0f, w->gexp));
     e = hipGetLastError();
     if (e != hipSuccess) {
         (void)hipFree(g);
@@ -834,13 +857,13 @@ static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
 
 extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
     if (!ctx || !w) return set_err(ctx, SIHIP_EINVAL, "weight_prepare_gemm: NULL argument");
-    if (!gemm_mfma_supported(w->L.type)) return SIHIP_OK;
+    if (!gemm_mfma_supported(w->L)) return SIHIP_OK;
     HIP_OK(ctx, hipSetDevice(ctx->device));
-    if (gemm32_supported(w->L.type) && !w->gemm) {
+    if (gemm32_supported(w->L) && !w->gemm) {
         const int rc = build_gemm_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
-    if ((w->L.type == T_Q4_K || w->L.type == T_Q6_K) && !w->gemm2) {
+    if (gemm16_supported(w->L) && !w->gemm2) {
         const int rc = build_gemm2_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
@@ -862,6 +885,15 @@ static int64_t gemm2_min_m(const Options &o) { return o.gemm2_min_m > 0 ? o.gemm
 // kernel, 34.4 us on the GEMM).
 constexpr int64_t kGemm6MinM = 5;
 static int64_t gemm6_min_m(const Options &o) { return o.gemm6_min_m > 0 ? o.gemm6_min_m : kGemm6MinM; }
+
+// Smallest M that takes the F16 GEMM (gemmh.h); option GEMMH_MIN_M. Its copy
+// holds the same bytes as the weights and streams them once for up to 128
+// rows per m block, where the matvec kernel's time grows with the columns
+// (config 4 at M = 8: ffn_up 27648 x 5120 61 us against 103, ffn_down 67
+// against 153, attn 20 against 66); at M = 1 and 2 the matvec kernel is as
+// fast or faster (kv 1024 x 5120 at M = 2: 10.2 us against 15.8).
+constexpr int64_t kGemmhMinM = 3;
+static int64_t gemmh_min_m(const Options &o) { return o.gemmh_min_m > 0 ? o.gemmh_min_m : kGemmhMinM; }
 
 // Shape of one matrix-core GEMM call: tile height, padded rows, workspace
 // sizes and K slices.
@@ -903,6 +935,22 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     GemmPlan p;
     const int64_t K = L.n_in, nb = K / 256;
     const int64_t NB = (L.n_out + kGemmBN - 1) / kGemmBN;
+    if (L.type == T_F16) {
+        // m blocks of 16 to 128 rows by M, shorter while the output tiles
+        // reach fewer than a quarter of the CUs (the GEMM_MT option, 1, 2,
+        // 4 or 8, overrides); K slices over steps of 128 elements
+        const int64_t nk = K / 128;
+        p.v2 = true;
+        p.mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+        while (p.mt > 1 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu / 4) p.mt /= 2;
+        if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4 || ctx->opt.gemm_mt == 8)
+            p.mt = (int)ctx->opt.gemm_mt;
+        const int64_t BM = 16 * p.mt;
+        p.Mp = (M + BM - 1) / BM * BM;
+        p.ws_bytes = p.Mp / BM * nk * gh_rec_bytes((int)BM);
+        plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB);
+        return p;
+    }
     if (L.type == T_Q6_K) {
         // m blocks of 16, 32 or 64 rows (the GEMM_MT option, 1, 2 or 4,
         // overrides); K slices as plan_slices decides
@@ -1018,6 +1066,36 @@ static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const G
 }
 
 template <int MT>
+static hipError_t launch_gemmh(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
+                               const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
+                               hipStream_t st) {
+    constexpr int BM = 16 * MT;
+    const Layout &L = w->L;
+    const int64_t nk = L.n_in / 128;
+    const int64_t threads = p.Mp * L.n_in / 8;
+    hipLaunchKernelGGL(gemmh_convert_x<BM>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       st, X, ldx, M, p.Mp, L.n_in, B.ws);
+    GHArgs A;
+    A.w = w->gemm2;
+    A.x = B.ws;
+    A.y = Y;
+    A.ldy = ldy;
+    A.n_out = L.n_out;
+    A.M = M;
+    A.Mp = p.Mp;
+    A.nk = (int)nk;
+    A.MB = (int)(p.Mp / BM);
+    A.NB = (int)((L.n_out + kG2BN - 1) / kG2BN);
+    A.S = p.S;
+    A.SBK = p.SBK;
+    A.part = p.S > 1 ? B.part : nullptr;
+    A.cnt = p.S > 1 ? B.cnt : nullptr;
+    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
+    hipLaunchKernelGGL((gemmh_f16_kernel<MT>), grid, dim3(kG2Threads), 0, st, A);
+    return hipGetLastError();
+}
+
+template <int MT>
 static hipError_t launch_gemm6(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
                                const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
                                hipStream_t st) {
@@ -1051,6 +1129,17 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
                             const GemmBufs &B, const float *X, int64_t ldx, int64_t M, float *Y,
                             int64_t ldy, hipStream_t st) {
     const Layout &L = w->L;
+    if (p.v2 && L.type == T_F16) {
+        hipError_t e;
+        switch (p.mt) {
+            case 1: e = launch_gemmh<1>(w, p, B, X, ldx, M, Y, ldy, st); break;
+            case 2: e = launch_gemmh<2>(w, p, B, X, ldx, M, Y, ldy, st); break;
+            case 4: e = launch_gemmh<4>(w, p, B, X, ldx, M, Y, ldy, st); break;
+            default: e = launch_gemmh<8>(w, p, B, X, ldx, M, Y, ldy, st); break;
+        }
+        if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+        return SIHIP_OK;
+    }
     if (p.v2 && L.type == T_Q6_K) {
         hipError_t e;
         switch (p.mt) {
@@ -1159,8 +1248,10 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
 // Prefill dispatch: MFMA GEMM where supported and M is large enough,
 // otherwise the matvec kernel over column groups.
 static bool gemm_on_mfma(const sihip_ctx *ctx, const sihip_weight *w, int64_t M) {
+    if (!gemm_mfma_supported(w->L)) return false;
     if (w->L.type == T_Q6_K) return M >= gemm6_min_m(ctx->opt);
-    return gemm_mfma_supported(w->L.type) && M >= gemm_min_m(ctx->opt);
+    if (w->L.type == T_F16) return M >= gemmh_min_m(ctx->opt);
+    return M >= gemm_min_m(ctx->opt);
 }
 
 static int run_gemm(sihip_ctx *ctx, const sihip_weight *w, const float *X, int64_t M, float *Y,

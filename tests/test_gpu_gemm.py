@@ -20,13 +20,15 @@ def _rows(rng, M, n_in):
     return X
 
 
-MFMA_TYPES = [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K]
+MFMA_TYPES = [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.F16]
 
 
 def _force_mfma(option):
-    """The matrix-core path at every M (Q6_K has a threshold of its own)."""
+    """The matrix-core path at every M (Q6_K and F16 have thresholds of
+    their own)."""
     option("GEMM_MIN_M", "1")
     option("GEMM6_MIN_M", "1")
+    option("GEMMH_MIN_M", "1")
 
 
 def _extreme_q2k(W, n_out, n_in):
@@ -335,3 +337,49 @@ def test_gemm6_q6k_tiles(dev, oracle, option, n_out, n_in, M, mt, sbk):
     ref, L1 = oracle.gemm(sa.Q6_K, W, n_out, n_in, X)
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
                  f"gemm6 Q6_K {n_out}x{n_in} M={M} MT={mt} SBK={sbk}")
+
+
+@pytest.mark.parametrize("n_out,n_in,M,mt,sbk", [
+    (27648, 5120, 8, -1, -1), (5120, 27648, 8, -1, -1), (300, 1280, 70, 4, 0), (129, 384, 33, 2, 1),
+    (1000, 2048, 130, 8, -1), (64, 896, 3, 1, -1),
+])
+def test_gemmh_f16_vs_oracle(dev, oracle, option, n_out, n_in, M, mt, sbk):
+    """The F16 GEMM (gemmh.h) at the config-4 batch-8 shapes and at every
+    m-tile height, with and without K slices, ragged M and n_out, against
+    the oracle; a repeat gives the same bits."""
+    option("GEMMH_MIN_M", "1")
+    option("GEMM_MT", str(mt))
+    option("GEMM_SBK", str(sbk))
+    rng = np.random.default_rng(n_out + n_in + M + mt)
+    W = synth.make_weights(sa.F16, n_out, n_in, rng)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(sa.F16, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+        Y2 = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(sa.F16, W, n_out, n_in, X)
+    what = f"gemmh F16 {n_out}x{n_in} M={M} MT={mt} SBK={sbk}"
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
+    assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
+
+
+def test_f16_rows_not_multiple_of_128_take_the_matvec(dev, oracle):
+    """F16 rows whose length is not a multiple of 128 elements (288 = 9 x
+    32) have no GEMM copy: batches run on the matvec kernel, within the
+    bar."""
+    rng = np.random.default_rng(77)
+    n_out, n_in, M = 200, 288, 12
+    W = synth.make_weights(sa.F16, n_out, n_in, rng)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(sa.F16, n_out, n_in, W)
+    try:
+        before = w.device_bytes
+        w.prepare_gemm()
+        assert w.device_bytes == before
+        Y = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(sa.F16, W, n_out, n_in, X)
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), "F16 288-wide rows")
