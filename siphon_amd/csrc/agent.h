@@ -42,24 +42,44 @@ __device__ inline void slices_finish(const float *part, uint32_t *cnt, int S, in
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (!last_flag) return;
     // this thread's outputs: rows m0 + idx / BN, columns n0 + idx % BN for
-    // idx = tid + THREADS q; all loads of one slice are issued together
+    // idx = tid + THREADS q; the loads of kU slices (32 per thread, or
+    // kOut if more) are issued together, since each group of loads costs a
+    // round trip to memory (agent-scope loads miss the XCD's L2), and are
+    // added in slice order
     constexpr int kOut = BM * BN / THREADS;
+    constexpr int kU = kOut >= 32 ? 1 : 32 / kOut;
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(part), (short)0, (int)((int64_t)S * Mp * ldp * 4), 0x00020000);
     const int64_t nn = n0 + threadIdx.x % BN;
+    // byte offset of output q in slice sl; rows past M were not written:
+    // read row 0's value, unused
+    auto off = [&](int sl, int q) -> uint32_t {
+        const int64_t m = m0 + (threadIdx.x + THREADS * q) / BN;
+        return (uint32_t)((((int64_t)sl * Mp + (m < M ? m : 0)) * ldp + nn) * 4);
+    };
     float v[kOut];
 #pragma unroll
     for (int q = 0; q < kOut; q++) v[q] = 0.0f;
-    for (int sl = 0; sl < S; sl++) {
-        float pv[kOut];
+    int sl = 0;
+    for (; sl + kU <= S; sl += kU) {
+        float pv[kU][kOut];
 #pragma unroll
-        for (int q = 0; q < kOut; q++) {
-            const int64_t m = m0 + (threadIdx.x + THREADS * q) / BN;
-            // rows past M were not written: read row 0's value, unused
-            pv[q] = load_agent_f32(pr, (uint32_t)((((int64_t)sl * Mp + (m < M ? m : 0)) * ldp + nn) * 4));
+        for (int u = 0; u < kU; u++)
+#pragma unroll
+            for (int q = 0; q < kOut; q++) pv[u][q] = load_agent_f32(pr, off(sl + u, q));
+#pragma unroll
+        for (int u = 0; u < kU; u++)
+#pragma unroll
+            for (int q = 0; q < kOut; q++) v[q] += pv[u][q];
+    }
+    if constexpr (kU > 1) {
+        for (; sl < S; sl++) {
+            float pv[kOut];
+#pragma unroll
+            for (int q = 0; q < kOut; q++) pv[q] = load_agent_f32(pr, off(sl, q));
+#pragma unroll
+            for (int q = 0; q < kOut; q++) v[q] += pv[q];
         }
-#pragma unroll
-        for (int q = 0; q < kOut; q++) v[q] += pv[q];
     }
     if (nn < n_out) {
 #pragma unroll

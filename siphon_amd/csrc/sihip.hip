@@ -23,6 +23,7 @@
 #include "gemm2.h"
 #include "gemm6.h"
 #include "gemmh.h"
+#include "gemmq.h"
 #include "matvec.h"
 #include "quant.h"
 
@@ -43,6 +44,7 @@ struct Options {
     int64_t gemm2_waves = -1;  // waves per SIMD of the 16x16 GEMMs, 1 or 2 (rule: 2)
     int64_t gemm6_min_m = -1;  // smallest M on the Q6_K GEMM (rule: kGemm6MinM)
     int64_t gemmh_min_m = -1;  // smallest M on the F16 GEMM (rule: kGemmhMinM)
+    int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
 };
 
 struct OptionName {
@@ -56,7 +58,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM_MIN_M", &Options::gemm_min_m}, {"GEMM_MT", &Options::gemm_mt},
     {"GEMM_SBK", &Options::gemm_sbk},     {"GEMM2_MIN_M", &Options::gemm2_min_m},
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
-    {"GEMMH_MIN_M", &Options::gemmh_min_m},
+    {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -764,21 +766,25 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 // force both paths).
 static int64_t gemm_min_m(const Options &o) { return o.gemm_min_m > 0 ? o.gemm_min_m : 5; }
 
+static bool is_q80_pair(uint32_t t) { return t == T_Q4_0 || t == T_Q5_0 || t == T_Q8_0; }
+
 static bool gemm_mfma_supported(const Layout &L) {
     const uint32_t t = L.type;
-    if (t == T_F16) return L.n_in % 128 == 0;  // steps of 128 elements
+    if (t == T_F16 || is_q80_pair(t)) return L.n_in % 128 == 0;  // steps of 128 elements
     return t == T_Q4_K || t == T_Q5_K || t == T_Q2_K || t == T_Q3_K || t == T_Q6_K;
 }
 
-// Types whose 32x32 GEMM copy exists (gemm.h); Q6_K and F16 run only on
-// their 16x16 kernels (gemm6.h, gemmh.h).
+// Types whose 32x32 GEMM copy exists (gemm.h): the K-quants but Q6_K.
 static bool gemm32_supported(const Layout &L) {
-    return gemm_mfma_supported(L) && L.type != T_Q6_K && L.type != T_F16;
+    return gemm_mfma_supported(L) && (L.type == T_Q4_K || L.type == T_Q5_K || L.type == T_Q2_K ||
+                                      L.type == T_Q3_K);
 }
 
-// Types with a 16x16 GEMM copy (w->gemm2).
+// Types with a 16x16 GEMM copy (w->gemm2): Q4_K (gemm2.h), Q6_K (gemm6.h),
+// F16 (gemmh.h), Q4_0 / Q5_0 / Q8_0 (gemmq.h).
 static bool gemm16_supported(const Layout &L) {
-    return gemm_mfma_supported(L) && (L.type == T_Q4_K || L.type == T_Q6_K || L.type == T_F16);
+    return gemm_mfma_supported(L) && (L.type == T_Q4_K || L.type == T_Q6_K || L.type == T_F16 ||
+                                      is_q80_pair(L.type));
 }
 
 // The weight's copy in the GEMM's order (gemm_layout_kernel), built from
@@ -820,7 +826,17 @@ static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     const Layout &L = w->L;
     const int64_t nblk32 = (L.n_out + kG2BN - 1) / kG2BN * (kG2BN / 32);
     int64_t bytes, threads;
-    if (L.type == T_F16) {
+    const int64_t nk = L.n_in / 128;
+    if (L.type == T_Q8_0) {
+        bytes = gemmq_layout_bytes<T_Q8_0>(nblk32, nk);
+        threads = nblk32 * nk * (gq_chunk<T_Q8_0>() / 16);
+    } else if (L.type == T_Q4_0) {
+        bytes = gemmq_layout_bytes<T_Q4_0>(nblk32, nk);
+        threads = nblk32 * nk * (gq_chunk<T_Q4_0>() / 16);
+    } else if (L.type == T_Q5_0) {
+        bytes = gemmq_layout_bytes<T_Q5_0>(nblk32, nk);
+        threads = nblk32 * nk * (gq_chunk<T_Q5_0>() / 16);
+    } else if (L.type == T_F16) {
         bytes = gemmh_layout_bytes(nblk32, L.n_in / 128);
         threads = nblk32 * (L.n_in / 128) * (kGHChunk / 16);
     } else if (L.type == T_Q6_K) {
@@ -836,7 +852,16 @@ static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
         return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
                        hipGetErrorString(e));
     const dim3 grid((unsigned)((threads + 255) / 256));
-    if (L.type == T_F16)
+    if (L.type == T_Q8_0)
+        hipLaunchKernelGGL(gemmq_layout<T_Q8_0>, grid, dim3(256), 0, st, L, (const uint8_t *)w->dev,
+                           g, nblk32);
+    else if (L.type == T_Q4_0)
+        hipLaunchKernelGGL(gemmq_layout<T_Q4_0>, grid, dim3(256), 0, st, L, (const uint8_t *)w->dev,
+                           g, nblk32);
+    else if (L.type == T_Q5_0)
+        hipLaunchKernelGGL(gemmq_layout<T_Q5_0>, grid, dim3(256), 0, st, L, (const uint8_t *)w->dev,
+                           g, nblk32);
+    else if (L.type == T_F16)
         hipLaunchKernelGGL(gemmh_layout_f16, grid, dim3(256), 0, st, L, (const uint8_t *)w->dev, g,
                            nblk32);
     else if (L.type == T_Q6_K)
@@ -895,6 +920,15 @@ static int64_t gemm6_min_m(const Options &o) { return o.gemm6_min_m > 0 ? o.gemm
 constexpr int64_t kGemmhMinM = 3;
 static int64_t gemmh_min_m(const Options &o) { return o.gemmh_min_m > 0 ? o.gemmh_min_m : kGemmhMinM; }
 
+// Smallest M that takes the Q4_0 / Q5_0 / Q8_0 GEMM (gemmq.h); option
+// GEMMQ_MIN_M. At M = 4 the GEMM is the faster on the large matrices
+// (config 4 ffn_up 27648 x 5120: 30.6 us against 49.3 on the matvec kernel,
+// ffn_down 33.4 against 40.7) and up to 2 us slower on the small ones (kv
+// 1024 x 5120: 13.3 against 11.3); at M = 2 the matvec kernel wins all but
+// ffn_up.
+constexpr int64_t kGemmqMinM = 4;
+static int64_t gemmq_min_m(const Options &o) { return o.gemmq_min_m > 0 ? o.gemmq_min_m : kGemmqMinM; }
+
 // Shape of one matrix-core GEMM call: tile height, padded rows, workspace
 // sizes and K slices.
 struct GemmPlan {
@@ -908,16 +942,20 @@ struct GemmPlan {
 
 // K slices of the 16x16 GEMMs: when the output tiles would fill at most
 // half of the workgroup slots (each kernel runs two workgroups per CU), the
-// super-blocks of a tile are split over S workgroups, enough for two per
-// CU, at least 2 super-blocks each; the GEMM_SBK option overrides (0:
-// none). Above half the slots, the partial sums' extra traffic costs more
-// than the idle slots.
-static void plan_slices(const sihip_ctx *ctx, GemmPlan &p, int64_t tiles, int64_t nb, int64_t NB) {
+// K steps of a tile (super-blocks, or 128-element steps) are split over S
+// workgroups, as many as keep to two per CU (a third workgroup on a CU
+// waits for a whole round: Q5_0 27648 x 5120 at M = 8 takes 25 us in 432
+// workgroups against 31 us in 648), at least min_sbk steps each (a slice's
+// fixed cost, its partial sums and the last workgroup's sum, outweighs a
+// few steps); the GEMM_SBK option overrides (0: none). Above half the
+// slots, the partial sums' extra traffic costs more than the idle slots.
+static void plan_slices(const sihip_ctx *ctx, GemmPlan &p, int64_t tiles, int64_t nb, int64_t NB,
+                        int64_t min_sbk = 2) {
     const int64_t want = 2 * ctx->n_cu;
     int64_t sbk = 0;
     if (2 * tiles <= want) {
-        int64_t S = (want + tiles - 1) / tiles;
-        if (S > nb / 2) S = nb / 2;
+        int64_t S = want / tiles;
+        if (S > nb / min_sbk) S = nb / min_sbk;
         if (S > 1) sbk = (nb + S - 1) / S;
     }
     if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
@@ -935,20 +973,24 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     GemmPlan p;
     const int64_t K = L.n_in, nb = K / 256;
     const int64_t NB = (L.n_out + kGemmBN - 1) / kGemmBN;
-    if (L.type == T_F16) {
-        // m blocks of 16 to 128 rows by M, shorter while the output tiles
-        // reach fewer than a quarter of the CUs (the GEMM_MT option, 1, 2,
-        // 4 or 8, overrides); K slices over steps of 128 elements
+    if (L.type == T_F16 || is_q80_pair(L.type)) {
+        // m blocks of 16 to 128 rows by M (Q4_0/Q5_0/Q8_0: to 64), shorter
+        // while the output tiles reach fewer than a quarter of the CUs (the
+        // GEMM_MT option, 1, 2, 4 or 8, overrides); K slices over steps of
+        // 128 elements
         const int64_t nk = K / 128;
         p.v2 = true;
         p.mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+        if (L.type != T_F16 && p.mt > 4) p.mt = 4;
         while (p.mt > 1 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu / 4) p.mt /= 2;
-        if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4 || ctx->opt.gemm_mt == 8)
+        if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4 ||
+            (ctx->opt.gemm_mt == 8 && L.type == T_F16))
             p.mt = (int)ctx->opt.gemm_mt;
         const int64_t BM = 16 * p.mt;
         p.Mp = (M + BM - 1) / BM * BM;
-        p.ws_bytes = p.Mp / BM * nk * gh_rec_bytes((int)BM);
-        plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB);
+        p.ws_bytes = p.Mp / BM * nk *
+                     (L.type == T_F16 ? gh_rec_bytes((int)BM) : gq_rec_bytes((int)BM));
+        plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, L.type == T_F16 ? 2 : 5);
         return p;
     }
     if (L.type == T_Q6_K) {
@@ -1065,6 +1107,48 @@ static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const G
     return hipGetLastError();
 }
 
+template <uint32_t FMT, int MT>
+static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
+                               const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
+                               hipStream_t st) {
+    constexpr int BM = 16 * MT;
+    const Layout &L = w->L;
+    const int64_t nk = L.n_in / 128;
+    const int64_t threads = p.Mp * L.n_in / 32;
+    constexpr int bias = FMT == T_Q4_0 ? 8 : FMT == T_Q5_0 ? 16 : 0;
+    hipLaunchKernelGGL((gemmq_quantize_x<BM, bias>), dim3((unsigned)((threads + 255) / 256)),
+                       dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws);
+    GQArgs A;
+    A.w = w->gemm2;
+    A.x = B.ws;
+    A.y = Y;
+    A.ldy = ldy;
+    A.n_out = L.n_out;
+    A.M = M;
+    A.Mp = p.Mp;
+    A.nk = (int)nk;
+    A.MB = (int)(p.Mp / BM);
+    A.NB = (int)((L.n_out + kG2BN - 1) / kG2BN);
+    A.S = p.S;
+    A.SBK = p.SBK;
+    A.part = p.S > 1 ? B.part : nullptr;
+    A.cnt = p.S > 1 ? B.cnt : nullptr;
+    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
+    hipLaunchKernelGGL((gemmq_kernel<FMT, MT>), grid, dim3(kG2Threads), 0, st, A);
+    return hipGetLastError();
+}
+
+template <uint32_t FMT>
+static hipError_t launch_gemmq_mt(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
+                                  const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
+                                  hipStream_t st) {
+    switch (p.mt) {
+        case 1: return launch_gemmq<FMT, 1>(w, p, B, X, ldx, M, Y, ldy, st);
+        case 2: return launch_gemmq<FMT, 2>(w, p, B, X, ldx, M, Y, ldy, st);
+        default: return launch_gemmq<FMT, 4>(w, p, B, X, ldx, M, Y, ldy, st);
+    }
+}
+
 template <int MT>
 static hipError_t launch_gemmh(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
                                const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
@@ -1129,6 +1213,14 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
                             const GemmBufs &B, const float *X, int64_t ldx, int64_t M, float *Y,
                             int64_t ldy, hipStream_t st) {
     const Layout &L = w->L;
+    if (p.v2 && is_q80_pair(L.type)) {
+        const hipError_t e =
+            L.type == T_Q8_0   ? launch_gemmq_mt<T_Q8_0>(w, p, B, X, ldx, M, Y, ldy, st)
+            : L.type == T_Q4_0 ? launch_gemmq_mt<T_Q4_0>(w, p, B, X, ldx, M, Y, ldy, st)
+                               : launch_gemmq_mt<T_Q5_0>(w, p, B, X, ldx, M, Y, ldy, st);
+        if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+        return SIHIP_OK;
+    }
     if (p.v2 && L.type == T_F16) {
         hipError_t e;
         switch (p.mt) {
@@ -1251,6 +1343,7 @@ static bool gemm_on_mfma(const sihip_ctx *ctx, const sihip_weight *w, int64_t M)
     if (!gemm_mfma_supported(w->L)) return false;
     if (w->L.type == T_Q6_K) return M >= gemm6_min_m(ctx->opt);
     if (w->L.type == T_F16) return M >= gemmh_min_m(ctx->opt);
+    if (is_q80_pair(w->L.type)) return M >= gemmq_min_m(ctx->opt);
     return M >= gemm_min_m(ctx->opt);
 }
 

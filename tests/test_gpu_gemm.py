@@ -20,15 +20,16 @@ def _rows(rng, M, n_in):
     return X
 
 
-MFMA_TYPES = [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.F16]
+MFMA_TYPES = [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.F16, sa.Q4_0, sa.Q5_0, sa.Q8_0]
 
 
 def _force_mfma(option):
-    """The matrix-core path at every M (Q6_K and F16 have thresholds of
-    their own)."""
+    """The matrix-core path at every M (Q6_K, F16 and the Q8_0-pair formats
+    have thresholds of their own)."""
     option("GEMM_MIN_M", "1")
     option("GEMM6_MIN_M", "1")
     option("GEMMH_MIN_M", "1")
+    option("GEMMQ_MIN_M", "1")
 
 
 def _extreme_q2k(W, n_out, n_in):
@@ -66,6 +67,19 @@ def _extreme_q6k(W, n_out, n_in):
     return W
 
 
+def _extreme_q80(W, wt, n_out, n_in):
+    """Rows at the ends of the Q4_0 / Q5_0 / Q8_0 quant ranges: every quant
+    at its largest and at its smallest stored value (Q4_0 nibbles 15 and 0,
+    Q5_0 fifth bits and nibbles all set and all clear, Q8_0 bytes 127 and
+    -128), scales as drawn."""
+    bb = {sa.Q4_0: 18, sa.Q5_0: 22, sa.Q8_0: 34}[wt]
+    blk = W.reshape(n_out, n_in // 32, bb)
+    for row, byte in enumerate([0xFF, 0x00] if wt != sa.Q8_0 else [0x7F, 0x80]):
+        if row < n_out:
+            blk[row, :, 2:] = byte
+    return W
+
+
 def _extreme_q5k(W, n_out, n_in):
     """Q5_K rows 0-1 with every 6-bit scale and min 63 (sh = sl = 7) and
     every quant 31 or 0: operand bytes sh * q - 128 = 89 and -128."""
@@ -94,6 +108,8 @@ def test_gemm_mfma_vs_oracle(dev, oracle, option, wt, n_out, n_in, M):
         W = _extreme_q5k(W, n_out, n_in)
     if wt == sa.Q6_K:
         W = _extreme_q6k(W, n_out, n_in)
+    if wt in (sa.Q4_0, sa.Q5_0, sa.Q8_0):
+        W = _extreme_q80(W, wt, n_out, n_in)
     X = _rows(rng, M, n_in)
     w = dev.upload(wt, n_out, n_in, W)
     try:
@@ -212,9 +228,9 @@ def test_gemm_k_slices(dev, oracle, option, wt, mt, sbk):
 def test_prepare_gemm_matches_lazy_copy(dev, oracle):
     """sihip_weight_prepare_gemm builds the GEMM copies at once (device bytes
     grow by them, a second call adds nothing; Q4_K has two, one per GEMM
-    kernel, and a lazy call builds only the one it uses; Q6_K has one); a
-    later gemm gives the bits of a weight whose copy its first gemm built.
-    Types without a matrix-core GEMM: a no-op."""
+    kernel, and a lazy call builds only the one it uses; Q6_K and Q8_0 have
+    one); a later gemm gives the bits of a weight whose copy its first gemm
+    built. F32, with no matrix-core GEMM: a no-op."""
     rng = np.random.default_rng(4242)
     n_out, n_in, M = 700, 2048, 40
     W = synth.make_weights(sa.Q4_K, n_out, n_in, rng)
@@ -224,6 +240,8 @@ def test_prepare_gemm_matches_lazy_copy(dev, oracle):
     w6 = dev.upload(sa.Q6_K, 64, 512, W6)
     W8 = synth.make_weights(sa.Q8_0, 64, 512, rng)
     w8 = dev.upload(sa.Q8_0, 64, 512, W8)
+    W32 = synth.make_weights(sa.F32, 64, 512, rng)
+    w32 = dev.upload(sa.F32, 64, 512, W32)
     try:
         before = eager.device_bytes
         eager.prepare_gemm()
@@ -242,9 +260,12 @@ def test_prepare_gemm_matches_lazy_copy(dev, oracle):
         assert w6.device_bytes > b6
         b8 = w8.device_bytes
         w8.prepare_gemm()
-        assert w8.device_bytes == b8
+        assert w8.device_bytes > b8
+        b32 = w32.device_bytes
+        w32.prepare_gemm()
+        assert w32.device_bytes == b32
     finally:
-        for w in (eager, lazy, w6, w8):
+        for w in (eager, lazy, w6, w8, w32):
             w.free()
 
 
@@ -383,3 +404,31 @@ def test_f16_rows_not_multiple_of_128_take_the_matvec(dev, oracle):
         w.free()
     ref, L1 = oracle.gemm(sa.F16, W, n_out, n_in, X)
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), "F16 288-wide rows")
+
+
+@pytest.mark.parametrize("wt", [sa.Q4_0, sa.Q5_0, sa.Q8_0], ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("n_out,n_in,M,mt,sbk", [
+    (27648, 5120, 8, -1, -1), (5120, 27648, 8, -1, -1), (300, 1280, 70, 4, 0), (129, 384, 33, 2, 1),
+    (4864, 896, 16, -1, -1), (64, 896, 3, 1, -1),
+])
+def test_gemmq_vs_oracle(dev, oracle, option, wt, n_out, n_in, M, mt, sbk):
+    """The Q4_0 / Q5_0 / Q8_0 GEMM (gemmq.h) at the config-4 batch-8 shapes
+    and config 1's 4864 x 896, every m-tile height, with and without K
+    slices, rows at the ends of the quant ranges, against the oracle; a
+    repeat gives the same bits."""
+    option("GEMMQ_MIN_M", "1")
+    option("GEMM_MT", str(mt))
+    option("GEMM_SBK", str(sbk))
+    rng = np.random.default_rng(n_out + n_in + M + mt + wt)
+    W = _extreme_q80(synth.make_weights(wt, n_out, n_in, rng), wt, n_out, n_in)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(wt, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+        Y2 = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+    what = f"gemmq {sa.NAMES[wt]} {n_out}x{n_in} M={M} MT={mt} SBK={sbk}"
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
+    assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
