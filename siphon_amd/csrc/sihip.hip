@@ -936,7 +936,9 @@ struct GemmPlan {
     int mt;            // 32-row MFMA tiles per wave along m
     int64_t Mp;        // M rounded up to the workgroup's rows
     int64_t ws_bytes;  // quantized activation planes
-    int S, SBK;        // K slices (S == 1: none) and super-blocks per slice
+    int S, SBK;        // K slices (S == 1: none) and K steps per slice
+    int64_t steps;     // K steps of a tile: super-blocks, or 128-element
+                       // steps for the F16 and Q8_0-pair kernels
     int64_t part_bytes;
 };
 
@@ -961,6 +963,7 @@ static void plan_slices(const sihip_ctx *ctx, GemmPlan &p, int64_t tiles, int64_
     if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
     p.S = 1;
     p.SBK = (int)nb;
+    p.steps = nb;
     p.part_bytes = 0;
     if (sbk > 0 && sbk < nb && tiles <= kGemmCounters) {
         p.S = (int)((nb + sbk - 1) / sbk);
@@ -1056,6 +1059,7 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
     p.S = 1;
     p.SBK = (int)nb;
+    p.steps = nb;
     p.part_bytes = 0;
     if (sbk > 0 && sbk < nb && tiles <= kGemmCounters) {
         p.S = (int)((nb + sbk - 1) / sbk);
@@ -1505,7 +1509,7 @@ extern "C" int sihip_gemm_dev_noalloc(sihip_ctx *ctx, const sihip_weight *w, con
     const size_t part_off = ((size_t)p.ws_bytes + 255) & ~(size_t)255;
     if (p.S > 1 && part_off + (size_t)p.part_bytes > room) {
         p.S = 1;
-        p.SBK = (int)(w->L.n_in / 256);
+        p.SBK = (int)p.steps;
         p.part_bytes = 0;
     }
     const GemmBufs B{ctx->scratch, (float *)(ctx->scratch + part_off),

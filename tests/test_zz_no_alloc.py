@@ -39,8 +39,10 @@ def _gemm_both(dev, w, X):
 
 # (type, n_out, n_in, first M, second M): the config-3 shape on the matrix
 # cores, K-sliced small batches, the matvec path (M below the matrix-core
-# threshold), a format without a matrix-core path and the Q6_K GEMM with K
-# slices; the last case's slices do not fit the scratch at M = 512
+# threshold), the Q6_K, F16 and Q8_0-pair GEMMs with K slices; the slices
+# of the UNSLICED calls do not fit the scratch (the F16 and Q8_0-pair
+# kernels count K in 128-element steps, the others in super-blocks, and the
+# unsliced call must cover all of them)
 CASES = [
     (sa.Q4_K, 14336, 4096, 512, 96),
     (sa.Q2_K, 3072, 5120, 16, 8),
@@ -49,8 +51,13 @@ CASES = [
     (sa.Q6_K, 1024, 4096, 8, 3),
     (sa.Q6_K, 1024, 4096, 64, 20),
     (sa.Q6_K, 4096, 14336, 512, 40),
+    (sa.Q5_0, 4096, 14336, 256, 40),
+    (sa.F16, 4096, 14336, 256, 24),
+    (sa.Q8_0, 4864, 896, 16, 5),
+    (sa.Q4_0, 5632, 2048, 64, 9),
 ]
-UNSLICED = {(sa.Q6_K, 4096, 14336, 512)}  # (type, n_out, n_in, M) run unsliced
+UNSLICED = {(sa.Q6_K, 4096, 14336, 512), (sa.Q5_0, 4096, 14336, 256),
+            (sa.F16, 4096, 14336, 256)}  # (type, n_out, n_in, M) run unsliced
 
 
 @pytest.mark.parametrize("wt,n_out,n_in,M1,M2", CASES,
