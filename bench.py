@@ -44,6 +44,7 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
 # profiles/matvec_gate_up_traffic.md for the commands and raw values.
 GATE_UP_TRAFFIC_BYTES = 2.00 * 32454.0 * 1024 + 1.00 * 112.0 * 1024
 INT8_PEAK_TOPS = 5033.0         # MI355X dense int8 MFMA, TOPS (256 CU x 2.4 GHz x 8192)
+F16_PEAK_TFLOPS = 2516.5        # MI355X dense f16 MFMA, TFLOP/s (half the int8 rate)
 N_LAYERS = 32
 
 
@@ -365,12 +366,13 @@ def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
     for w in ws:
         w.free()
     # the other matrix-core formats at the same shape, M = 512 (not
-    # configured by the baseline: how far the Q4_K prefill path carries)
+    # configured by the baseline: how far the Q4_K prefill path carries;
+    # F16 runs on the f16 MFMAs, whose dense peak is half the int8 one)
     formats = {}
     M = 512
     X = torch.randn(M, n_in, device="cuda")
     Y = torch.empty(M, n_out, device="cuda")
-    for wt in (sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K):
+    for wt in (sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.Q4_0, sa.Q5_0, sa.Q8_0, sa.F16):
         Wf = synth.make_weights(wt, n_out, n_in, rng)
         wf = [dev.upload(wt, n_out, n_in, Wf) for _ in range(-(-rotate_bytes // Wf.nbytes) + 1)]
         with torch.cuda.stream(stream):
@@ -389,6 +391,8 @@ def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
         tops = 2.0 * M * n_out * n_in / t / 1e12
         formats[sa.NAMES[wt]] = {"us_per_call": round(t * 1e6, 1), "TOPS": round(tops, 1),
                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        if wt == sa.F16:  # f16 MFMAs: also against the dense f16 peak
+            formats[sa.NAMES[wt]]["frac_f16_peak"] = round(tops / F16_PEAK_TFLOPS, 4)
         for w in wf:
             w.free()
     del X, Y
