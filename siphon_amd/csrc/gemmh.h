@@ -105,9 +105,11 @@ struct GHArgs {
     uint32_t *cnt;        // cnt[mblk * NB + nblk], zero between launches
 };
 
+// At least two waves per SIMD, no upper bound: the register count (80
+// VGPRs at MT = 1 to 248 at MT = 8) sets the occupancy.
 template <int MT>
 __global__ __launch_bounds__(kG2Threads)
-__attribute__((amdgpu_waves_per_eu(2, 2))) void gemmh_f16_kernel(GHArgs A) {
+__attribute__((amdgpu_waves_per_eu(2))) void gemmh_f16_kernel(GHArgs A) {
     constexpr int BM = 16 * MT;
     constexpr int kRec = gh_rec_bytes(BM);
     constexpr int kXP = kRec / 16;

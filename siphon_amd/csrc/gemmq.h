@@ -232,9 +232,13 @@ struct GQArgs {
 // MT = 4, whose accumulators leave no room for four)
 __host__ __device__ constexpr int gq_depth(int MT) { return MT >= 4 ? 2 : 4; }
 
+// At least two waves per SIMD (256 registers each at most); no upper bound,
+// so the register count sets the occupancy: 124 VGPRs at MT = 1, 168 at
+// MT = 2, 134 at MT = 4 (three or four waves per SIMD), where an upper
+// bound of two would make the compiler reserve registers for two.
 template <uint32_t FMT, int MT>
 __global__ __launch_bounds__(kG2Threads)
-__attribute__((amdgpu_waves_per_eu(2, 2))) void gemmq_kernel(GQArgs A) {
+__attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
     constexpr int BM = 16 * MT;
     constexpr int kRec = gq_rec_bytes(BM);
     constexpr int kXP = kRec / 16;

@@ -943,17 +943,18 @@ struct GemmPlan {
 };
 
 // K slices of the 16x16 GEMMs: when the output tiles would fill at most
-// half of the workgroup slots (each kernel runs two workgroups per CU), the
-// K steps of a tile (super-blocks, or 128-element steps) are split over S
-// workgroups, as many as keep to two per CU (a third workgroup on a CU
-// waits for a whole round: Q5_0 27648 x 5120 at M = 8 takes 25 us in 432
+// half of `want` workgroups (by default two per CU, the slots of the
+// kernels built for two waves per SIMD), the K steps of a tile
+// (super-blocks, or 128-element steps) are split over S workgroups, as many
+// as keep within `want` (a workgroup past the slots waits for a whole
+// round: Q5_0 27648 x 5120 at M = 8 on two slots takes 25 us in 432
 // workgroups against 31 us in 648), at least min_sbk steps each (a slice's
 // fixed cost, its partial sums and the last workgroup's sum, outweighs a
-// few steps); the GEMM_SBK option overrides (0: none). Above half the
-// slots, the partial sums' extra traffic costs more than the idle slots.
+// few steps); the GEMM_SBK option overrides (0: none). Above half of
+// `want`, the partial sums' extra traffic costs more than the idle slots.
 static void plan_slices(const sihip_ctx *ctx, GemmPlan &p, int64_t tiles, int64_t nb, int64_t NB,
-                        int64_t min_sbk = 2) {
-    const int64_t want = 2 * ctx->n_cu;
+                        int64_t min_sbk = 2, int64_t want = 0) {
+    if (want <= 0) want = 2 * ctx->n_cu;
     int64_t sbk = 0;
     if (2 * tiles <= want) {
         int64_t S = want / tiles;
@@ -993,7 +994,20 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
         p.Mp = (M + BM - 1) / BM * BM;
         p.ws_bytes = p.Mp / BM * nk *
                      (L.type == T_F16 ? gh_rec_bytes((int)BM) : gq_rec_bytes((int)BM));
-        plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, L.type == T_F16 ? 2 : 5);
+        // The Q8_0-pair kernel holds three workgroups per CU from 32-row m
+        // blocks (at M = 8, 16-row blocks, two per CU are faster than three:
+        // 25.3 against 28.8 us for 27648 x 5120; at M = 512, 5120 x 27648 in
+        // 640 workgroups 313 us against 503 in 320). The F16 kernel streams
+        // 8 KB per wave and step with no epilogue: up to 64-row blocks it is
+        // fastest at about three workgroups per four CUs (M = 8: 27648 x
+        // 5120 unsliced, 216 workgroups, 47.6 us against 53.6 in 432;
+        // 5120 x 27648 in 160, 52.8 against 56.5 in 480; kv 1024 x 5120 in
+        // 64, 8.6 against 12.6 in 160), 128-row blocks at two per CU.
+        if (L.type == T_F16)
+            plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, p.mt <= 4 ? 5 : 2,
+                        p.mt <= 4 ? 3 * ctx->n_cu / 4 : 0);
+        else
+            plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, 5, (p.mt == 1 ? 2 : 3) * ctx->n_cu);
         return p;
     }
     if (L.type == T_Q6_K) {
