@@ -120,10 +120,12 @@ struct G6Args {
     uint32_t *cnt;
 };
 
-// Built for two waves per SIMD (256 registers each, two workgroups per CU).
+// At least two waves per SIMD (256 registers each at most), no upper
+// bound: 116 VGPRs at MT = 1 and 160 at MT = 2 leave room for three or
+// four waves per SIMD, 232 at MT = 4 for two.
 template <int MT>
 __global__ __launch_bounds__(kG2Threads)
-__attribute__((amdgpu_waves_per_eu(2, 2))) void gemm6_q6k_kernel(G6Args A) {
+__attribute__((amdgpu_waves_per_eu(2))) void gemm6_q6k_kernel(G6Args A) {
     constexpr int BM = 16 * MT;
     constexpr int kRec = g2_rec_bytes(BM);
     constexpr int kXP = kRec / 16;                           // 16-byte pieces of a record

@@ -1025,7 +1025,12 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
         const int64_t BM = 16 * p.mt;
         p.Mp = (M + BM - 1) / BM * BM;
         p.ws_bytes = p.Mp / BM * nb * g2_rec_bytes((int)BM);
-        plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB);
+        // K slices: with 16- and 32-row blocks (no operand decode, 2-byte
+        // digits streamed) about one workgroup per CU is fastest (M = 8:
+        // ffn_down 4096 x 14336 in 224 workgroups 25.6 us against 29.5 in
+        // 448; 27648 x 5120 unsliced 48.4 against 54.8), with 64-row blocks
+        // two (ffn_down at M = 512: 83.8 us in 512 against 107 in 256)
+        plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB, 2, p.mt <= 2 ? ctx->n_cu : 0);
         return p;
     }
     if (L.type == T_Q4_K && M >= gemm2_min_m(ctx->opt)) {
@@ -1056,30 +1061,16 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     const int64_t BM = 32 * p.mt;
     p.Mp = (M + BM - 1) / BM * BM;
     p.ws_bytes = gemm_x_bytes(p.Mp, K);
-    // K slices of SBK super-blocks when the output tiles alone would leave
-    // CUs idle (M <= 32 at the benchmark shapes: 112 tiles on 256 CUs):
-    // about one workgroup per CU, at least 4 super-blocks per slice. The
-    // partial sums cost a write and a read of S x M x N floats, which
-    // outweighs the extra parallelism once the tiles fill the chip
-    // (measured M = 64: 26.2 us unsliced, 32.3 us in 4 slices).
-    // The GEMM_SBK option overrides (0: no slices).
-    const int64_t tiles = (p.Mp / BM) * NB;
-    int64_t sbk = 0;
-    if (tiles < ctx->n_cu) {
-        int64_t S = (ctx->n_cu + tiles - 1) / tiles;
-        if (S > nb / 4) S = nb / 4;
-        if (S > 1) sbk = (nb + S - 1) / S;
-    }
-    if (ctx->opt.gemm_sbk >= 0) sbk = ctx->opt.gemm_sbk;
-    p.S = 1;
-    p.SBK = (int)nb;
-    p.steps = nb;
-    p.part_bytes = 0;
-    if (sbk > 0 && sbk < nb && tiles <= kGemmCounters) {
-        p.S = (int)((nb + sbk - 1) / sbk);
-        p.SBK = (int)sbk;
-        p.part_bytes = (int64_t)p.S * p.Mp * NB * kGemmBN * (int64_t)sizeof(float);
-    }
+    // K slices when the output tiles alone would leave CUs idle (M <= 32
+    // at the benchmark shapes: 112 tiles on 256 CUs), at least 4
+    // super-blocks per slice, as many as keep within two workgroups per CU
+    // (plan_slices; M = 8 ffn_down 5120 x 27648 in 480 workgroups: Q4_K
+    // 30.7 us, Q5_K 32.3, Q2_K 25.5, against 39.0 / 43.3 / 30.8 in 280 and
+    // 39.1 / 42.1 / 32.3 in 560). The partial sums cost a write and a read
+    // of S x M x N floats, which outweighs the extra parallelism once the
+    // tiles fill the chip (measured M = 64: 26.2 us unsliced, 32.3 us in 4
+    // slices).
+    plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB, 4);
     return p;
 }
 
