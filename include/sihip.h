@@ -165,6 +165,18 @@ int sihip_dequant_rows_dev(sihip_ctx *ctx, const sihip_weight *w,
 int sihip_gemv_multi_dev(sihip_ctx *ctx, int count,
                          const sihip_weight *const *w, const float *x,
                          float *const *y, void *stream);
+/* The M-row counterpart: Y[i] (M x n_out[i], row-major) receives
+ * sihip_gemm_dev(w[i], X), the weights sharing one X (M x n_in, 16-byte
+ * aligned): the q/k/v and gate/up matrices of the batched forward that
+ * replaces the reference's prompt loop (cmd_run.c:275-283; engine.c:317-319,
+ * 375-376, whose gemv calls each re-quantize x, backend.c:100-108). The
+ * activation is quantized once per record layout; weights of one kernel
+ * family run with one m-tile count, so their K slicing, and with it the f32
+ * summation order, may differ from a single sihip_gemm_dev call (same
+ * tolerance). All w[i] must have the same n_in; at most 4. */
+int sihip_gemm_multi_dev(sihip_ctx *ctx, int count,
+                         const sihip_weight *const *w, const float *X,
+                         int64_t M, float *const *Y, void *stream);
 
 /* Decode attention of one layer at position pos over an f16 KV cache, for
  * every query head h (reference attn_head, engine.c:90-147): the query

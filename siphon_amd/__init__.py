@@ -84,6 +84,8 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
     L.sihip_gemm_dev_noalloc.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
     L.sihip_gemv_multi_dev.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(_vp), _vp,
                                        ctypes.POINTER(_vp), _vp]
+    L.sihip_gemm_multi_dev.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(_vp), _vp, _i64,
+                                       ctypes.POINTER(_vp), _vp]
     for fn in ("sihip_quantize_q8_K", "sihip_quantize_q8_0", "sihip_convert_f16"):
         getattr(L, fn).argtypes = [_vp, _vp, _vp, _i64]
     L.sihip_vec_dot.argtypes = [_vp, _u32, ctypes.c_int, _vp, _vp, _vp]
@@ -228,6 +230,12 @@ class Device:
         wa = (_vp * n)(*[w.handle for w in ws])
         ya = (_vp * n)(*y_ptrs)
         self._check(self.L.sihip_gemv_multi_dev(self.ctx, n, wa, x_ptr, ya, stream))
+
+    def gemm_multi_dev(self, ws, X_ptr: int, M: int, Y_ptrs, stream: int | None = None):
+        n = len(ws)
+        wa = (_vp * n)(*[w.handle for w in ws])
+        ya = (_vp * n)(*Y_ptrs)
+        self._check(self.L.sihip_gemm_multi_dev(self.ctx, n, wa, X_ptr, M, ya, stream))
 
     # device memory through the library's own HIP runtime (no torch needed)
     def alloc(self, nbytes: int) -> "DevBuf":

@@ -973,7 +973,11 @@ static void plan_slices(const sihip_ctx *ctx, GemmPlan &p, int64_t tiles, int64_
     }
 }
 
-static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
+// force_mt > 0 sets the m tiles per wave where the kernel has that
+// instance (as the GEMM_MT option does; sihip_gemm_multi_dev uses it to
+// give weights that share X one activation record layout).
+static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int force_mt = 0) {
+    const int64_t opt_mt = force_mt > 0 ? force_mt : ctx->opt.gemm_mt;
     GemmPlan p;
     const int64_t K = L.n_in, nb = K / 256;
     const int64_t NB = (L.n_out + kGemmBN - 1) / kGemmBN;
@@ -987,9 +991,8 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
         p.mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
         if (L.type != T_F16 && p.mt > 4) p.mt = 4;
         while (p.mt > 1 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu / 4) p.mt /= 2;
-        if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4 ||
-            (ctx->opt.gemm_mt == 8 && L.type == T_F16))
-            p.mt = (int)ctx->opt.gemm_mt;
+        if (opt_mt == 1 || opt_mt == 2 || opt_mt == 4 || (opt_mt == 8 && L.type == T_F16))
+            p.mt = (int)opt_mt;
         const int64_t BM = 16 * p.mt;
         p.Mp = (M + BM - 1) / BM * BM;
         p.ws_bytes = p.Mp / BM * nk *
@@ -1020,8 +1023,7 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
         p.v2 = true;
         p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
         while (p.mt > 1 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu / 4) p.mt /= 2;
-        if (ctx->opt.gemm_mt == 1 || ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4)
-            p.mt = (int)ctx->opt.gemm_mt;
+        if (opt_mt == 1 || opt_mt == 2 || opt_mt == 4) p.mt = (int)opt_mt;
         const int64_t BM = 16 * p.mt;
         p.Mp = (M + BM - 1) / BM * BM;
         p.ws_bytes = p.Mp / BM * nb * g2_rec_bytes((int)BM);
@@ -1042,8 +1044,7 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
         p.v2 = true;
         p.mt = 8;
         while (p.mt > 2 && (M + 16 * p.mt - 1) / (16 * p.mt) * NB < ctx->n_cu) p.mt /= 2;
-        if (ctx->opt.gemm_mt == 2 || ctx->opt.gemm_mt == 4 || ctx->opt.gemm_mt == 8)
-            p.mt = (int)ctx->opt.gemm_mt;
+        if (opt_mt == 2 || opt_mt == 4 || opt_mt == 8) p.mt = (int)opt_mt;
         const int64_t BM = 16 * p.mt;
         p.Mp = (M + BM - 1) / BM * BM;
         p.ws_bytes = p.Mp / BM * nb * g2_rec_bytes((int)BM);
@@ -1054,7 +1055,7 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
     // small M: 32-row m tiles (twice the workgroups) with four super-blocks
     // of weights in flight per wave; the GEMM_MT option (1 or 2) overrides
     p.mt = M <= 128 ? 1 : 2;
-    if (ctx->opt.gemm_mt > 0) p.mt = ctx->opt.gemm_mt == 1 ? 1 : 2;
+    if (opt_mt > 0) p.mt = opt_mt == 1 ? 1 : 2;
     // Q5_K's fifth-bit words and bias term do not fit two 32-row tiles or
     // four super-blocks in flight in 256 VGPRs: 32-row tiles, two in flight
     if (L.type == T_Q5_K) p.mt = 1;
@@ -1075,11 +1076,15 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M) {
 }
 
 // Device buffers of one GEMM call: the activation planes, and for K slices
-// the partial sums and the arrival counters (zero between calls).
+// the partial sums and the arrival counters (zero between calls). quant:
+// the launch first writes the activation planes from X; false when an
+// earlier launch on the stream wrote the same planes (several weights
+// sharing one X and one record layout, sihip_gemm_multi_dev).
 struct GemmBufs {
     uint8_t *ws;
     float *part;
     uint32_t *cnt;
+    bool quant = true;
 };
 
 // Y[m, :] = W x[m, :] for m < M on the matrix cores, with the workspaces
@@ -1093,8 +1098,9 @@ static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const G
     const Layout &L = w->L;
     const int64_t nb = L.n_in / 256;
     const int64_t blocks = p.Mp * nb;
-    hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)), dim3(kG2Threads),
-                       0, st, X, ldx, M, p.Mp, nb, ws);
+    if (B.quant)
+        hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)),
+                           dim3(kG2Threads), 0, st, X, ldx, M, p.Mp, nb, ws);
     G2Args A;
     A.w = w->gemm2;
     A.x = ws;
@@ -1125,8 +1131,9 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     const int64_t nk = L.n_in / 128;
     const int64_t threads = p.Mp * L.n_in / 32;
     constexpr int bias = FMT == T_Q4_0 ? 8 : FMT == T_Q5_0 ? 16 : 0;
-    hipLaunchKernelGGL((gemmq_quantize_x<BM, bias>), dim3((unsigned)((threads + 255) / 256)),
-                       dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws);
+    if (B.quant)
+        hipLaunchKernelGGL((gemmq_quantize_x<BM, bias>), dim3((unsigned)((threads + 255) / 256)),
+                           dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws);
     GQArgs A;
     A.w = w->gemm2;
     A.x = B.ws;
@@ -1166,8 +1173,9 @@ static hipError_t launch_gemmh(const sihip_weight *w, const GemmPlan &p, const G
     const Layout &L = w->L;
     const int64_t nk = L.n_in / 128;
     const int64_t threads = p.Mp * L.n_in / 8;
-    hipLaunchKernelGGL(gemmh_convert_x<BM>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       st, X, ldx, M, p.Mp, L.n_in, B.ws);
+    if (B.quant)
+        hipLaunchKernelGGL(gemmh_convert_x<BM>, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                           0, st, X, ldx, M, p.Mp, L.n_in, B.ws);
     GHArgs A;
     A.w = w->gemm2;
     A.x = B.ws;
@@ -1196,8 +1204,9 @@ static hipError_t launch_gemm6(const sihip_weight *w, const GemmPlan &p, const G
     const Layout &L = w->L;
     const int64_t nb = L.n_in / 256;
     const int64_t blocks = p.Mp * nb;
-    hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)), dim3(kG2Threads),
-                       0, st, X, ldx, M, p.Mp, nb, B.ws);
+    if (B.quant)
+        hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)),
+                           dim3(kG2Threads), 0, st, X, ldx, M, p.Mp, nb, B.ws);
     G6Args A;
     A.w = w->gemm2;
     A.x = B.ws;
@@ -1272,8 +1281,9 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
     XP.d = (float *)(B.ws + Mp * K);
     XP.bs = (_Float16 *)(B.ws + Mp * K + nb * Mp * 4);
     const int64_t blocks = Mp * nb;
-    hipLaunchKernelGGL(gemm_quantize_x, dim3((unsigned)((blocks + 15) / 16)), dim3(kGemmThreads), 0,
-                       st, X, ldx, M, Mp, nb, XP);
+    if (B.quant)
+        hipLaunchKernelGGL(gemm_quantize_x, dim3((unsigned)((blocks + 15) / 16)), dim3(kGemmThreads),
+                           0, st, X, ldx, M, Mp, nb, XP);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm quantize: %s", hipGetErrorString(e));
     GemmArgs A;
@@ -1343,6 +1353,94 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
     const GemmBufs B{(uint8_t *)ctx->d_ws, (float *)ctx->d_gpart, ctx->d_gcnt};
     rc = launch_gemm_mfma(ctx, w, p, B, X, ldx, M, Y, ldy, st);
     if (rc) return rc;
+    return order_after(ctx, ctx->order, st);
+}
+
+// The activation records a plan's launch writes, as a key: launches with
+// equal keys over the same X write identical planes. Families: the 32-row
+// K-quant GEMM (Q8_K planes of Mp rows), the 16x16 Q4_K and Q6_K GEMMs (Q8_K
+// records of BM rows), the Q8_0-pair GEMM (Q8_0 records of BM rows with the
+// format's bias) and the F16 GEMM (f16 records of BM rows).
+struct XKey {
+    int fam;
+    int64_t bm;
+    int bias;
+    bool operator==(const XKey &o) const { return fam == o.fam && bm == o.bm && bias == o.bias; }
+};
+static XKey xkey(const Layout &L, const GemmPlan &p) {
+    if (!p.v2) return XKey{0, 32 * p.mt, 0};
+    if (L.type == T_F16) return XKey{3, 16 * p.mt, 0};
+    if (is_q80_pair(L.type))
+        return XKey{2, 16 * p.mt, L.type == T_Q4_0 ? 8 : L.type == T_Q5_0 ? 16 : 0};
+    return XKey{1, 16 * p.mt, 0};
+}
+
+// The MFMA GEMMs of several weights over one X: the weights of one record
+// family get one m-tile count (the largest of their own plans that each
+// kernel has), so X is quantized once per distinct record layout and the
+// launches after the first of a layout read its planes.
+static int run_gemm_multi(sihip_ctx *ctx, int count, const sihip_weight *const *wc,
+                          const float *X, int64_t M, float *const *Y, hipStream_t st) {
+    GemmPlan plan[kMaxSegs];
+    XKey key[kMaxSegs];
+    for (int i = 0; i < count; i++) {
+        plan[i] = plan_gemm(ctx, wc[i]->L, M);
+        key[i] = xkey(wc[i]->L, plan[i]);
+    }
+    for (int i = 0; i < count; i++) {
+        int mt = plan[i].mt;
+        for (int j = 0; j < count; j++)
+            if (key[j].fam == key[i].fam && plan[j].mt > mt) mt = plan[j].mt;
+        if (mt != plan[i].mt) {
+            const GemmPlan q = plan_gemm(ctx, wc[i]->L, M, mt);
+            if (q.mt == mt && q.v2 == plan[i].v2) {
+                plan[i] = q;
+                key[i] = xkey(wc[i]->L, q);
+            }
+        }
+    }
+    // one planes buffer per distinct key, 256-byte aligned, one after another
+    size_t off[kMaxSegs], total = 0, part = 0;
+    bool first[kMaxSegs];
+    for (int i = 0; i < count; i++) {
+        first[i] = true;
+        for (int j = 0; j < i; j++)
+            if (key[j] == key[i]) {
+                first[i] = false;
+                off[i] = off[j];
+                break;
+            }
+        if (first[i]) {
+            off[i] = total;
+            total += ((size_t)plan[i].ws_bytes + 255) & ~(size_t)255;
+        }
+        if (plan[i].S > 1 && (size_t)plan[i].part_bytes > part) part = (size_t)plan[i].part_bytes;
+    }
+    for (int i = 0; i < count; i++) {
+        sihip_weight *w = const_cast<sihip_weight *>(wc[i]);  // GEMM copies are caches of w
+        if (plan[i].v2 && !w->gemm2) {
+            const int rc = build_gemm2_copy(ctx, w, st);
+            if (rc) return rc;
+        }
+        if (!plan[i].v2 && !w->gemm) {
+            const int rc = build_gemm_copy(ctx, w, st);
+            if (rc) return rc;
+        }
+    }
+    int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, total, st);
+    if (rc) return rc;
+    if (part) {
+        rc = ensure(ctx, &ctx->d_gpart, &ctx->d_gpart_cap, part, st);
+        if (rc) return rc;
+    }
+    rc = order_before(ctx, ctx->order, st);
+    if (rc) return rc;
+    for (int i = 0; i < count; i++) {
+        GemmBufs B{(uint8_t *)ctx->d_ws + off[i], (float *)ctx->d_gpart, ctx->d_gcnt};
+        B.quant = first[i];
+        rc = launch_gemm_mfma(ctx, wc[i], plan[i], B, X, wc[i]->L.n_in, M, Y[i], wc[i]->L.n_out, st);
+        if (rc) return rc;
+    }
     return order_after(ctx, ctx->order, st);
 }
 
@@ -1584,6 +1682,36 @@ extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint1
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "attention launch: %s", hipGetErrorString(e));
     return order_after(ctx, ctx->order, st);
+}
+
+extern "C" int sihip_gemm_multi_dev(sihip_ctx *ctx, int count, const sihip_weight *const *w,
+                                    const float *X, int64_t M, float *const *Y, void *stream) {
+    if (!ctx || !w || !X || !Y || count < 1 || count > kMaxSegs)
+        return set_err(ctx, SIHIP_EINVAL, "gemm_multi_dev: bad arguments");
+    if (M <= 0) return set_err(ctx, SIHIP_EINVAL, "gemm_multi_dev: M must be positive");
+    if (!aligned16(X)) return set_err(ctx, SIHIP_EINVAL, "gemm_multi_dev: X must be 16-byte aligned");
+    for (int i = 0; i < count; i++) {
+        if (!w[i] || !Y[i]) return set_err(ctx, SIHIP_EINVAL, "gemm_multi_dev: NULL weight/output");
+        if (w[i]->L.n_in != w[0]->L.n_in)
+            return set_err(ctx, SIHIP_EINVAL, "gemm_multi_dev: n_in differs between weights");
+    }
+    const hipStream_t st = (hipStream_t)stream;
+    // weights below their matrix-core threshold run on their own; the others
+    // share the activation planes
+    const sihip_weight *mw[kMaxSegs];
+    float *my[kMaxSegs];
+    int nm = 0;
+    for (int i = 0; i < count; i++) {
+        if (gemm_on_mfma(ctx, w[i], M)) {
+            mw[nm] = w[i];
+            my[nm++] = Y[i];
+        } else {
+            const int rc = run_matvec(ctx, w[i], X, w[i]->L.n_in, nullptr, 0, M, Y[i],
+                                      w[i]->L.n_out, w[i]->L.n_out, st);
+            if (rc) return rc;
+        }
+    }
+    return nm ? run_gemm_multi(ctx, nm, mw, X, M, my, st) : SIHIP_OK;
 }
 
 extern "C" int sihip_gemv_multi_dev(sihip_ctx *ctx, int count, const sihip_weight *const *w,
