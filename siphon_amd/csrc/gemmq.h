@@ -21,9 +21,11 @@
 // ring rather than being loaded a step ahead: loads retire in issue order,
 // so waiting for a record loaded at the start of the previous step would
 // also wait for every weight load issued before it. A step's record is
-// copied from its ring slot into LDS at the end of the step before, and K
-// slices split a tile's steps over several workgroups when the output
-// tiles alone would leave the chip idle.
+// copied from its ring slot into LDS at the end of the step before; where a
+// K slice's records fit 64 KB (16- and 32-row m blocks), all of them are
+// copied into LDS before the first step instead, and the ring carries only
+// weights. K slices split a tile's steps over several workgroups when the
+// output tiles alone would leave the chip idle.
 #pragma once
 
 #include "agent.h"
@@ -49,13 +51,14 @@ __host__ __device__ constexpr int gq_rec_bytes(int BM) { return 160 * BM; }
 __host__ __device__ constexpr int gq_rec_dx(int BM) { return 128 * BM; }
 __host__ __device__ constexpr int gq_rec_bs(int BM) { return 144 * BM; }
 
-// One thread per Q8_0 block (row m, block kb); rows M..Mp-1 are zero.
-template <int BM, int BIAS>
-__global__ __launch_bounds__(256) void gemmq_quantize_x(const float *x, int64_t ldx, int64_t M,
-                                                        int64_t Mp, int64_t n_in, uint8_t *rec) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// Q8_0 block i (row m = i / (n_in / 32), block kb) of X into its record;
+// rows M..Mp-1 are zero. COHERENT: agent-scope stores, which the workgroups
+// of the same launch read back (the fused GEMM below); otherwise plain
+// stores for the GEMM launched after this one.
+template <int BM, int BIAS, bool COHERENT>
+__device__ inline void gq_quantize_one(const float *x, int64_t ldx, int64_t M, int64_t n_in,
+                                       uint8_t *rec, int64_t i) {
     const int64_t nbl = n_in / 32;
-    if (i >= Mp * nbl) return;
     const int64_t m = i / nbl, kb = i % nbl;
     const int64_t c = kb / 4;
     const int j = (int)(kb % 4);
@@ -72,11 +75,33 @@ __global__ __launch_bounds__(256) void gemmq_quantize_x(const float *x, int64_t 
     uint8_t *R = rec + (mb * (n_in / 128) + c) * gq_rec_bytes(BM);
     // lane group g of the fragment takes elements 8 g .. 8 g + 7 (words 2g, 2g+1)
     uint8_t *frag = R + (4 * (mr >> 4) + j) * 512;
+    float *dx = reinterpret_cast<float *>(R + gq_rec_dx(BM)) + j * BM + mr;
+    int *bs = reinterpret_cast<int *>(R + gq_rec_bs(BM)) + j * BM + mr;
 #pragma unroll
-    for (int g = 0; g < 4; g++)
-        *reinterpret_cast<uint2 *>(frag + (16 * g + (mr & 15)) * 8) = make_uint2(q.q[2 * g], q.q[2 * g + 1]);
-    reinterpret_cast<float *>(R + gq_rec_dx(BM))[j * BM + mr] = q.d;
-    reinterpret_cast<int *>(R + gq_rec_bs(BM))[j * BM + mr] = -BIAS * q.sum;
+    for (int g = 0; g < 4; g++) {
+        uint64_t *dst = reinterpret_cast<uint64_t *>(frag + (16 * g + (mr & 15)) * 8);
+        const uint64_t v = (uint64_t)q.q[2 * g] | ((uint64_t)q.q[2 * g + 1] << 32);
+        if constexpr (COHERENT)
+            __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            *dst = v;
+    }
+    if constexpr (COHERENT) {
+        __hip_atomic_store(dx, q.d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(bs, -BIAS * q.sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *dx = q.d;
+        *bs = -BIAS * q.sum;
+    }
+}
+
+// One thread per Q8_0 block (row m, block kb); rows M..Mp-1 are zero.
+template <int BM, int BIAS>
+__global__ __launch_bounds__(256) void gemmq_quantize_x(const float *x, int64_t ldx, int64_t M,
+                                                        int64_t Mp, int64_t n_in, uint8_t *rec) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= Mp * (n_in / 32)) return;
+    gq_quantize_one<BM, BIAS, false>(x, ldx, M, n_in, rec, i);
 }
 
 // ---- weight copy in the order of this kernel ----------------------------------
@@ -226,19 +251,52 @@ struct GQArgs {
     int S, SBK;           // K slices over steps
     float *part;
     uint32_t *cnt;
+    // fused activation quantization (gemmq_kernel<.., true>): the first
+    // nprod workgroups quantize X (M x n_in, row stride ldx) into the
+    // records and count their arrival on *flag; the other ncons wait for
+    // all of them before their first record read. The last of those to
+    // pass resets *flag and *done (its own count) to zero for the next
+    // launch.
+    const float *X;
+    int64_t ldx, n_in;
+    int nprod, ncons;
+    uint32_t *flag, *done;
 };
+
+// Bound of a consumer's wait on the producers, in polls of about 64 cycles
+// each (some 0.1 s): the producers run first whatever the grid, so the wait
+// ends long before; the bound keeps a fault elsewhere from hanging the GPU.
+constexpr uint32_t kGQSpin = 1u << 21;
 
 // steps in flight per wave: a ring of gq_depth(MT) register sets (two at
 // MT = 4, whose accumulators leave no room for four)
 __host__ __device__ constexpr int gq_depth(int MT) { return MT >= 4 ? 2 : 4; }
 
+// Dynamic LDS of gemmq_kernel<.., XM = 1 or 2>: the records of sbk steps in
+// whole KiBs. Those modes run where it is at most kGQSliceLds.
+__host__ __device__ constexpr int64_t gq_lds_bytes(int BM, int64_t sbk) {
+    return (sbk * gq_rec_bytes(BM) + 1023) / 1024 * 1024;
+}
+constexpr int64_t kGQSliceLds = 64 * 1024;
+
 // At least two waves per SIMD (256 registers each at most); no upper bound,
 // so the register count sets the occupancy: 124 VGPRs at MT = 1, 168 at
 // MT = 2, 134 at MT = 4 (three or four waves per SIMD), where an upper
 // bound of two would make the compiler reserve registers for two.
-template <uint32_t FMT, int MT>
+//
+// XM, where a workgroup's activation records come from:
+//   0: through the register ring into two LDS buffers, a step ahead;
+//   1: all records of its K slice copied into LDS (dynamic, gq_lds_bytes)
+//      before the first step, so the steps read LDS only, with no record
+//      loads, LDS stores or barriers between them;
+//   2: as 1, the records written by the launch's own first workgroups
+//      (agent-scope stores, read with agent-scope loads) instead of a
+//      quantization launch before it; the other workgroups request their
+//      first weights before they wait for them.
+template <uint32_t FMT, int MT, int XM>
 __global__ __launch_bounds__(kG2Threads)
 __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
+    constexpr bool FUSE = XM == 2;
     constexpr int BM = 16 * MT;
     constexpr int kRec = gq_rec_bytes(BM);
     constexpr int kXP = kRec / 16;
@@ -250,14 +308,52 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
     // conditional last round splits the step into blocks, and the compiler
     // then sinks the epilogues below it, keeping every MFMA result live
     constexpr int kSx = kXPT * 4096;
-    __shared__ __attribute__((aligned(16))) uint8_t sx0[kSx];
-    __shared__ __attribute__((aligned(16))) uint8_t sx1[kSx];
-    const int b = blockIdx.x;
+    __shared__ __attribute__((aligned(16))) uint8_t sx0[XM == 0 ? kSx : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t sx1[XM == 0 ? kSx : 16];
+    extern __shared__ __attribute__((aligned(16))) uint8_t gq_slice[];
+    if constexpr (FUSE) {
+        if ((int)blockIdx.x < A.nprod) {  // producer: blocks p, p + nprod * 256, ...
+            const int64_t nblocks = A.Mp * (A.n_in / 32);
+            for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nblocks;
+                 i += (int64_t)A.nprod * 256)
+                gq_quantize_one<BM, bias, true>(A.X, A.ldx, A.M, A.n_in,
+                                                const_cast<uint8_t *>(A.x), i);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __syncthreads();
+            if (threadIdx.x == 0)
+                __hip_atomic_fetch_add(A.flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
+    // a consumer has seen every producer arrive: count it; the last resets
+    // both counters
+    auto passed = [&]() {
+        if (__hip_atomic_fetch_add(A.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (uint32_t)A.ncons - 1) {
+            __hip_atomic_store(A.flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(A.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+    // the producers are a multiple of 8 workgroups, so b keeps the XCD of
+    // blockIdx.x
+    const int b = (int)blockIdx.x - (FUSE ? A.nprod : 0);
     const int xcd = b & 7, t = b >> 3;
     const int per = A.MB * A.S;
     const int nblk = (t / per) * 8 + xcd, rest = t % per;
     const int slice = rest / A.MB, mblk = rest % A.MB;
-    if (nblk >= A.NB) return;
+    if (nblk >= A.NB) {
+        if constexpr (FUSE) {
+            if (threadIdx.x == 0) {
+                uint32_t it = 0;
+                while (__hip_atomic_load(A.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                           (uint32_t)A.nprod && ++it < kGQSpin)
+                    __builtin_amdgcn_s_sleep(1);
+                passed();
+            }
+        }
+        return;
+    }
     const int c0 = slice * A.SBK;
     const int c1 = c0 + A.SBK < A.nk ? c0 + A.SBK : A.nk;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -285,11 +381,16 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
         for (int k = 0; k < kXPT; k++)
             *reinterpret_cast<uint4 *>(dst + ((int)threadIdx.x + kG2Threads * k) * 16) = o.xs[k];
     };
-    auto load_w = [&](int c, Ops &o) {
+    // records written in this launch (FUSE) are read with agent-scope
+    // loads, past a stale line in this XCD's L2
+    constexpr int kXAux = FUSE ? 16 : 0;
+    auto load_x = [&](int c, Ops &o) {
 #pragma unroll
         for (int k = 0; k < kXPT; k++)
             o.xs[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    xr, (int)threadIdx.x * 16, c * kRec + 4096 * k, 0));
+                                                    xr, (int)threadIdx.x * 16, c * kRec + 4096 * k, kXAux));
+    };
+    auto load_wt = [&](int c, Ops &o) {
         const int so = (c * 4 + wave) * kChunk;
         if constexpr (FMT == T_Q8_0) {
 #pragma unroll
@@ -313,6 +414,10 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
         for (int nt = 0; nt < 2; nt++)
             o.d[nt] = __builtin_bit_cast(
                 float4, __builtin_amdgcn_raw_buffer_load_b128(wr, r16 * 16, so + gq_d_off<FMT>() + nt * 256, 0));
+    };
+    auto load_w = [&](int c, Ops &o) {
+        load_x(c, o);
+        load_wt(c, o);
     };
     // the MFMA operand (8 quants) of block j, n tile nt
     auto operand = [&](const Ops &o, int j, int nt) -> long {
@@ -368,20 +473,82 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
         }
         store_x(nxt, xn);
     };
+    // XM 1, 2: step c with the slice's records in LDS and only the weights
+    // in the ring
+    auto step_lds = [&](int c, const Ops &cur, Ops &ahead) {
+        const int ca = c + kD - 1 < c1 ? c + kD - 1 : c1 - 1;
+        load_wt(ca, ahead);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *X = gq_slice + (c - c0) * kRec;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const long b0 = operand(cur, j, 0), b1 = operand(cur, j, 1);
+            const float dw0 = j == 0 ? cur.d[0].x : j == 1 ? cur.d[0].y : j == 2 ? cur.d[0].z : cur.d[0].w;
+            const float dw1 = j == 0 ? cur.d[1].x : j == 1 ? cur.d[1].y : j == 2 ? cur.d[1].z : cur.d[1].w;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const long a = *reinterpret_cast<const long *>(X + (4 * mt + j) * 512 + lane * 8);
+                const int off = (j * BM + 16 * mt + 4 * g) * 4;
+                v4iq_t cb = {0, 0, 0, 0};
+                if constexpr (bias != 0) cb = *reinterpret_cast<const v4iq_t *>(X + gq_rec_bs(BM) + off);
+                const v4iq_t s0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, cb, 0, 0, 0);
+                const v4iq_t s1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, cb, 0, 0, 0);
+                const float4 dx = *reinterpret_cast<const float4 *>(X + gq_rec_dx(BM) + off);
+                const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    y[mt][0][i] = fma_f32((float)s0[i], dw0 * dxv[i], y[mt][0][i]);
+                    y[mt][1][i] = fma_f32((float)s1[i], dw1 * dxv[i], y[mt][1][i]);
+                }
+            }
+        }
+    };
 
-    // kD (even) steps per round, so the LDS buffer of step c is
-    // sx0 for c - c0 even and sx1 for c - c0 odd
-    static_assert(kD % 2 == 0, "LDS buffers alternate by step");
     Ops o[kD];
+    if constexpr (XM == 0) {
+        // kD (even) steps per round, so the LDS buffer of step c is sx0 for
+        // c - c0 even and sx1 for c - c0 odd
+        static_assert(kD % 2 == 0, "LDS buffers alternate by step");
 #pragma unroll
-    for (int u = 0; u + 1 < kD; u++) load_w(c0 + u < c1 ? c0 + u : c1 - 1, o[u]);
-    store_x(o[0], sx0);
-    for (int c = c0; c < c1; c += kD) {
+        for (int u = 0; u + 1 < kD; u++) load_w(c0 + u < c1 ? c0 + u : c1 - 1, o[u]);
+        store_x(o[0], sx0);
+        for (int c = c0; c < c1; c += kD) {
 #pragma unroll
-        for (int u = 0; u < kD; u++)
-            if (c + u < c1)
-                step(c + u, o[u], o[(u + kD - 1) % kD], o[(u + 1) % kD],
-                     (u & 1) ? sx1 : sx0, (u & 1) ? sx0 : sx1);
+            for (int u = 0; u < kD; u++)
+                if (c + u < c1)
+                    step(c + u, o[u], o[(u + kD - 1) % kD], o[(u + 1) % kD],
+                         (u & 1) ? sx1 : sx0, (u & 1) ? sx0 : sx1);
+        }
+    } else {
+        // the first weights go out first (before the wait on the producers)
+#pragma unroll
+        for (int u = 0; u + 1 < kD; u++) load_wt(c0 + u < c1 ? c0 + u : c1 - 1, o[u]);
+        if constexpr (FUSE) {
+            if (threadIdx.x == 0) {
+                uint32_t it = 0;
+                while (__hip_atomic_load(A.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                           (uint32_t)A.nprod && ++it < kGQSpin)
+                    __builtin_amdgcn_s_sleep(1);
+                passed();
+            }
+            __syncthreads();
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        }
+        // the slice's records, 1 KiB per wave instruction straight into LDS
+        // (whole KiBs: the last may read into the next record, or zero past
+        // the buffer, into LDS that no step reads)
+        const int kib = ((c1 - c0) * kRec + 1023) / 1024;
+        for (int i = wave; i < kib; i += kG2Threads / 64)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void *)(gq_slice + i * 1024), 16, lane * 16,
+                c0 * kRec + i * 1024, 0, kXAux);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int c = c0; c < c1; c += kD) {
+#pragma unroll
+            for (int u = 0; u < kD; u++)
+                if (c + u < c1) step_lds(c + u, o[u], o[(u + kD - 1) % kD]);
+        }
     }
 
     const int64_t n0 = (int64_t)nblk * kG2BN + 32 * wave;

@@ -45,6 +45,7 @@ struct Options {
     int64_t gemm6_min_m = -1;  // smallest M on the Q6_K GEMM (rule: kGemm6MinM)
     int64_t gemmh_min_m = -1;  // smallest M on the F16 GEMM (rule: kGemmhMinM)
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
+    int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0, 1, 2 (gemmq_kernel XM; rule: 1 where it fits)
 };
 
 struct OptionName {
@@ -59,6 +60,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM_SBK", &Options::gemm_sbk},     {"GEMM2_MIN_M", &Options::gemm2_min_m},
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
     {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
+    {"GEMMQ_XMODE", &Options::gemmq_xmode},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -1080,11 +1082,14 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
 // the launch first writes the activation planes from X; false when an
 // earlier launch on the stream wrote the same planes (several weights
 // sharing one X and one record layout, sihip_gemm_multi_dev).
+// xmode: the Q8_0-pair GEMM's record mode (gemmq_kernel XM; -1: its rule).
+// Its fused mode uses the last two counters.
 struct GemmBufs {
     uint8_t *ws;
     float *part;
     uint32_t *cnt;
     bool quant = true;
+    int xmode = -1;
 };
 
 // Y[m, :] = W x[m, :] for m < M on the matrix cores, with the workspaces
@@ -1131,10 +1136,26 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     const int64_t nk = L.n_in / 128;
     const int64_t threads = p.Mp * L.n_in / 32;
     constexpr int bias = FMT == T_Q4_0 ? 8 : FMT == T_Q5_0 ? 16 : 0;
-    if (B.quant)
+    const int64_t NB = (L.n_out + kG2BN - 1) / kG2BN;
+    // record mode: with up to 32-row m blocks and a K slice whose records
+    // fit kGQSliceLds, the slice's records go to LDS up front (mode 1: 2-7%
+    // faster than the ring at M = 8-16, e.g. kv 1024 x 5120 13.1 against
+    // 14.1 us per call). Mode 2 (the launch's first workgroups quantize X:
+    // a multiple of 8 producers, so the others keep their XCD order; the
+    // K-slice counters stay below the last two, which it uses) runs only
+    // when the GEMMQ_XMODE option asks for it: its agent-scope record
+    // loads miss the L2, and it was slower than a separate quantization
+    // launch on every config-4 shape (27648 x 5120 at M = 8: 34.5 against
+    // 30.3 us), faster only on 4864 x 896 (10.0 against 11.4).
+    const int64_t lds = gq_lds_bytes(BM, p.SBK);
+    int xm = MT <= 2 && lds <= kGQSliceLds ? 1 : 0;
+    if (B.xmode == 0) xm = 0;
+    if (B.xmode == 2 && xm == 1 && B.quant && (p.Mp / BM) * NB <= kGemmCounters - 2) xm = 2;
+    const bool fuse = xm == 2;
+    if (B.quant && !fuse)
         hipLaunchKernelGGL((gemmq_quantize_x<BM, bias>), dim3((unsigned)((threads + 255) / 256)),
                            dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws);
-    GQArgs A;
+    GQArgs A{};
     A.w = w->gemm2;
     A.x = B.ws;
     A.y = Y;
@@ -1149,8 +1170,27 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     A.SBK = p.SBK;
     A.part = p.S > 1 ? B.part : nullptr;
     A.cnt = p.S > 1 ? B.cnt : nullptr;
-    const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
-    hipLaunchKernelGGL((gemmq_kernel<FMT, MT>), grid, dim3(kG2Threads), 0, st, A);
+    const int64_t cons = (int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S;
+    if constexpr (MT <= 2) {
+        if (fuse) {
+            A.X = X;
+            A.ldx = ldx;
+            A.n_in = L.n_in;
+            A.nprod = (int)(((threads + 255) / 256 + 7) / 8 * 8);
+            A.ncons = (int)cons;
+            A.flag = B.cnt + kGemmCounters - 2;
+            A.done = B.cnt + kGemmCounters - 1;
+            hipLaunchKernelGGL((gemmq_kernel<FMT, MT, 2>), dim3((unsigned)(A.nprod + cons)),
+                               dim3(kG2Threads), (unsigned)lds, st, A);
+            return hipGetLastError();
+        }
+        if (xm == 1) {
+            hipLaunchKernelGGL((gemmq_kernel<FMT, MT, 1>), dim3((unsigned)cons), dim3(kG2Threads),
+                               (unsigned)lds, st, A);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemmq_kernel<FMT, MT, 0>), dim3((unsigned)cons), dim3(kG2Threads), 0, st, A);
     return hipGetLastError();
 }
 
@@ -1232,10 +1272,12 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
                             int64_t ldy, hipStream_t st) {
     const Layout &L = w->L;
     if (p.v2 && is_q80_pair(L.type)) {
+        GemmBufs BQ = B;
+        BQ.xmode = (int)ctx->opt.gemmq_xmode;
         const hipError_t e =
-            L.type == T_Q8_0   ? launch_gemmq_mt<T_Q8_0>(w, p, B, X, ldx, M, Y, ldy, st)
-            : L.type == T_Q4_0 ? launch_gemmq_mt<T_Q4_0>(w, p, B, X, ldx, M, Y, ldy, st)
-                               : launch_gemmq_mt<T_Q5_0>(w, p, B, X, ldx, M, Y, ldy, st);
+            L.type == T_Q8_0   ? launch_gemmq_mt<T_Q8_0>(w, p, BQ, X, ldx, M, Y, ldy, st)
+            : L.type == T_Q4_0 ? launch_gemmq_mt<T_Q4_0>(w, p, BQ, X, ldx, M, Y, ldy, st)
+                               : launch_gemmq_mt<T_Q5_0>(w, p, BQ, X, ldx, M, Y, ldy, st);
         if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
         return SIHIP_OK;
     }

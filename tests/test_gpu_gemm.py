@@ -432,3 +432,32 @@ def test_gemmq_vs_oracle(dev, oracle, option, wt, n_out, n_in, M, mt, sbk):
     what = f"gemmq {sa.NAMES[wt]} {n_out}x{n_in} M={M} MT={mt} SBK={sbk}"
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
     assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
+
+
+@pytest.mark.parametrize("wt", [sa.Q4_0, sa.Q5_0, sa.Q8_0], ids=lambda t: sa.NAMES[t])
+def test_gemmq_record_modes_match(dev, option, wt):
+    """The Q8_0-pair GEMM's record modes give the same bits, call after
+    call: records through the register ring (mode 0), a K slice's records
+    in LDS up front (1), and those records written by the launch's own first
+    workgroups instead of a separate quantization launch (2); on weights
+    whose n blocks leave idle workgroups (300 rows), with and without K
+    slices, 16- and 32-row m blocks, and M past a multiple of 8."""
+    option("GEMMQ_MIN_M", "1")
+    rng = np.random.default_rng(4040 + wt)
+    cases = [(300, 1280, 5, -1), (27648, 5120, 8, -1), (5120, 27648, 13, -1), (1024, 5120, 16, 0),
+             (4864, 896, 3, 2), (5120, 5120, 24, -1)]
+    for n_out, n_in, M, sbk in cases:
+        W = synth.make_weights(wt, n_out, n_in, rng)
+        w = dev.upload(wt, n_out, n_in, W)
+        try:
+            option("GEMM_SBK", str(sbk))
+            outs = []
+            for mode in ("0", "2", "1", "2", "0"):
+                option("GEMMQ_XMODE", mode)
+                X = _rows(np.random.default_rng(n_out + M), M, n_in)
+                outs.append(dev.gemm(w, X).view(np.uint32))
+            what = f"{sa.NAMES[wt]} {n_out}x{n_in} M={M} SBK={sbk}"
+            for y in outs[1:]:
+                assert np.array_equal(y, outs[0]), what + ": record modes differ"
+        finally:
+            w.free()
