@@ -72,7 +72,12 @@ const char *sihip_last_error(const sihip_ctx *ctx);
  * the environment variable SIHIP_<name> at sihip_init; a negative value
  * restores the built-in rule. Names: WG_PER_CU, WAVE_TARGET, SPLIT_ELEMS,
  * TILE_COLS (these four apply to later uploads and launches), GEMM_MIN_M,
- * GEMM_MT, GEMM_SBK. Unknown names: SIHIP_EINVAL. */
+ * GEMM_MT, GEMM_SBK, GEMM2_MIN_M, GEMM2_WAVES, GEMM6_MIN_M, GEMMH_MIN_M,
+ * GEMMQ_MIN_M, GEMMQ_XMODE, and Q80_SCALAR: 1 quantizes Q8_0-pair
+ * activations with the reference's portable scalar routine (reference
+ * kernels.c:542-558), as the reference does when SI_SCALAR is set or the
+ * host lacks AVX2 (kernels.c:56-85); the rule is the SIMD routine
+ * (kernels_avx2.c:594-645). Unknown names: SIHIP_EINVAL. */
 int sihip_set_option(sihip_ctx *ctx, const char *name, int64_t value);
 
 /* ---- weights --------------------------------------------------------- */

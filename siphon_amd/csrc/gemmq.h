@@ -57,14 +57,14 @@ __host__ __device__ constexpr int gq_rec_bs(int BM) { return 144 * BM; }
 // stores for the GEMM launched after this one.
 template <int BM, int BIAS, bool COHERENT>
 __device__ inline void gq_quantize_one(const float *x, int64_t ldx, int64_t M, int64_t n_in,
-                                       uint8_t *rec, int64_t i) {
+                                       uint8_t *rec, int64_t i, int scalar) {
     const int64_t nbl = n_in / 32;
     const int64_t m = i / nbl, kb = i % nbl;
     const int64_t c = kb / 4;
     const int j = (int)(kb % 4);
     Q80Block q;
     if (m < M) {
-        q = q80_block(x + m * ldx + kb * 32);
+        q = q80_block_sel(x + m * ldx + kb * 32, scalar);
     } else {
         q.d = 0.0f;
         q.sum = 0;
@@ -98,10 +98,11 @@ __device__ inline void gq_quantize_one(const float *x, int64_t ldx, int64_t M, i
 // One thread per Q8_0 block (row m, block kb); rows M..Mp-1 are zero.
 template <int BM, int BIAS>
 __global__ __launch_bounds__(256) void gemmq_quantize_x(const float *x, int64_t ldx, int64_t M,
-                                                        int64_t Mp, int64_t n_in, uint8_t *rec) {
+                                                        int64_t Mp, int64_t n_in, uint8_t *rec,
+                                                        int scalar) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= Mp * (n_in / 32)) return;
-    gq_quantize_one<BM, BIAS, false>(x, ldx, M, n_in, rec, i);
+    gq_quantize_one<BM, BIAS, false>(x, ldx, M, n_in, rec, i, scalar);
 }
 
 // ---- weight copy in the order of this kernel ----------------------------------
@@ -261,6 +262,7 @@ struct GQArgs {
     int64_t ldx, n_in;
     int nprod, ncons;
     uint32_t *flag, *done;
+    int q80s;             // the scalar Q8_0 quantizer (q80_block_sel)
 };
 
 // Bound of a consumer's wait on the producers, in polls of about 64 cycles
@@ -317,7 +319,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
             for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nblocks;
                  i += (int64_t)A.nprod * 256)
                 gq_quantize_one<BM, bias, true>(A.X, A.ldx, A.M, A.n_in,
-                                                const_cast<uint8_t *>(A.x), i);
+                                                const_cast<uint8_t *>(A.x), i, A.q80s);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __syncthreads();

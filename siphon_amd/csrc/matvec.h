@@ -94,6 +94,7 @@ struct MVArgs {
     int64_t ldx, ldxq;
     int nc;               // activation columns staged (== the kernel's NC)
     int64_t col_bytes;    // LDS bytes per column
+    int q80s;             // Q8_0 pair from f32: the scalar quantizer (q80_block_sel)
 };
 
 // ---- prologue: activations -> LDS ----------------------------------------
@@ -198,7 +199,7 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
                 float d;
                 int sum;
                 if (a.x) {
-                    const Q80Block r = q80_block(a.x + c * a.ldx + (b0 + b) * 32);
+                    const Q80Block r = q80_block_sel(a.x + c * a.ldx + (b0 + b) * 32, a.q80s);
                     for (int t = 0; t < 8; t++) q[t] = r.q[t];
                     d = r.d;
                     sum = r.sum;
@@ -554,10 +555,10 @@ __global__ __launch_bounds__(kThreads) void quantize_q8K_kernel(const float *x, 
 }
 
 __global__ __launch_bounds__(kThreads) void quantize_q80_kernel(const float *x, uint8_t *out,
-                                                                int64_t nb) {
+                                                                int64_t nb, int scalar) {
     const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (b >= nb) return;
-    const Q80Block r = q80_block(x + b * 32);
+    const Q80Block r = q80_block_sel(x + b * 32, scalar);
     uint8_t *o = out + b * 34;
     o[0] = (uint8_t)(r.dbits & 0xff);
     o[1] = (uint8_t)(r.dbits >> 8);

@@ -188,4 +188,53 @@ __device__ inline Q80Block q80_block(const float *x) {
     return b;
 }
 
+// The portable scalar Q8_0 quantizer (reference src/kernels.c:542-558),
+// which the reference selects instead of the SIMD one when SI_SCALAR is set
+// (kernels.c:80-83): amax by the running comparison amax > |v| ? amax : |v|
+// in element order, d = amax / 127 (then stored as f16), id = 1 / d (0 for
+// d == 0) and q = roundf(x * id), halves away from zero. |x * id| stays
+// within 127 (plus rounding), so the clamp below never changes a value; it
+// only keeps the conversion defined.
+__device__ inline Q80Block q80_block_scalar(const float *x) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 t = reinterpret_cast<const float4 *>(x)[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const float a = fabsf(v[j]);
+        amax = amax > a ? amax : a;
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    Q80Block b;
+    b.dbits = f32_to_f16_bits(d);
+    b.d = f16_bits_to_f32(b.dbits);
+    int s = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float r = __builtin_roundf(__fmul_rn(v[4 * t + k], id));
+            int q = cvt_i32_indef(r);
+            q = q > 127 ? 127 : (q < -128 ? -128 : q);
+            s += q;
+            w |= (uint32_t)(q & 0xff) << (8 * k);
+        }
+        b.q[t] = w;
+    }
+    b.sum = s;
+    return b;
+}
+
+// The Q8_0 quantizer a launch uses: the SIMD semantics (q80_block), or
+// the scalar ones when `scalar` is set (a wave-uniform launch argument).
+__device__ inline Q80Block q80_block_sel(const float *x, int scalar) {
+    return scalar ? q80_block_scalar(x) : q80_block(x);
+}
+
 }  // namespace sihip

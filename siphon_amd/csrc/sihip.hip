@@ -46,6 +46,8 @@ struct Options {
     int64_t gemmh_min_m = -1;  // smallest M on the F16 GEMM (rule: kGemmhMinM)
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
     int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0, 1, 2 (gemmq_kernel XM; rule: 1 where it fits)
+    int64_t q80_scalar = -1;   // Q8_0 activations by the scalar quantizer (reference
+                               // kernels.c:542-558, its SI_SCALAR mode), 1: on (rule: off)
 };
 
 struct OptionName {
@@ -60,7 +62,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM_SBK", &Options::gemm_sbk},     {"GEMM2_MIN_M", &Options::gemm2_min_m},
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
     {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
-    {"GEMMQ_XMODE", &Options::gemmq_xmode},
+    {"GEMMQ_XMODE", &Options::gemmq_xmode}, {"Q80_SCALAR", &Options::q80_scalar},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -727,6 +729,7 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         }
         A.nseg = count;
         A.n_in = n_in;
+        A.q80s = ctx->opt.q80_scalar > 0;
         A.x = x ? x + m * ldx : nullptr;
         A.xq = xq ? xq + m * ldxq : nullptr;
         A.ldx = ldx;
@@ -1090,6 +1093,7 @@ struct GemmBufs {
     uint32_t *cnt;
     bool quant = true;
     int xmode = -1;
+    int q80s = 0;  // the scalar Q8_0 quantizer (Q80_SCALAR option)
 };
 
 // Y[m, :] = W x[m, :] for m < M on the matrix cores, with the workspaces
@@ -1154,8 +1158,9 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     const bool fuse = xm == 2;
     if (B.quant && !fuse)
         hipLaunchKernelGGL((gemmq_quantize_x<BM, bias>), dim3((unsigned)((threads + 255) / 256)),
-                           dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws);
+                           dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws, B.q80s);
     GQArgs A{};
+    A.q80s = B.q80s;
     A.w = w->gemm2;
     A.x = B.ws;
     A.y = Y;
@@ -1274,6 +1279,7 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
     if (p.v2 && is_q80_pair(L.type)) {
         GemmBufs BQ = B;
         BQ.xmode = (int)ctx->opt.gemmq_xmode;
+        BQ.q80s = ctx->opt.q80_scalar > 0;
         const hipError_t e =
             L.type == T_Q8_0   ? launch_gemmq_mt<T_Q8_0>(w, p, BQ, X, ldx, M, Y, ldy, st)
             : L.type == T_Q4_0 ? launch_gemmq_mt<T_Q4_0>(w, p, BQ, X, ldx, M, Y, ldy, st)
@@ -1906,7 +1912,7 @@ extern "C" int sihip_quantize_q8_0(sihip_ctx *ctx, const float *x, void *out, in
     HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, x, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
     hipLaunchKernelGGL(quantize_q80_kernel, dim3((unsigned)((nb + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, ctx->stream, (const float *)ctx->d_in,
-                       (uint8_t *)ctx->d_out, nb);
+                       (uint8_t *)ctx->d_out, nb, (int)(ctx->opt.q80_scalar > 0));
     HIP_OK(ctx, hipGetLastError());
     HIP_OK(ctx, hipMemcpyAsync(out, ctx->d_out, (size_t)nb * 34, hipMemcpyDeviceToHost, ctx->stream));
     HIP_OK(ctx, hipStreamSynchronize(ctx->stream));

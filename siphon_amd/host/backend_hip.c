@@ -7,6 +7,9 @@
 #include <string.h>
 
 #include "sihip.h"
+#ifndef SI_HIP_STANDALONE
+#include "siphon/kernels.h"
+#endif
 
 /* entry points resolved from the library */
 typedef struct {
@@ -21,6 +24,7 @@ typedef struct {
     uint64_t (*weight_device_bytes)(const sihip_weight *);
     int (*gemv)(sihip_ctx *, const sihip_weight *, const float *, float *, int64_t);
     int (*gemm)(sihip_ctx *, const sihip_weight *, const float *, int64_t, float *);
+    int (*set_option)(sihip_ctx *, const char *, int64_t);
 } hip_fns;
 
 /* one uploaded tensor, keyed by its mmap data pointer; type and shape are
@@ -256,6 +260,7 @@ int si_backend_hip_open(const char *lib_path, int device, si_backend **out) {
     RESOLVE(weight_device_bytes, "sihip_weight_device_bytes");
     RESOLVE(gemv, "sihip_gemv");
     RESOLVE(gemm, "sihip_gemm");
+    RESOLVE(set_option, "sihip_set_option");
     if (hb->f.abi_version() != SIHIP_ABI_VERSION) {
         si_set_err("hip: %s has ABI version %d, this build expects %d", path,
                    hb->f.abi_version(), SIHIP_ABI_VERSION);
@@ -265,6 +270,17 @@ int si_backend_hip_open(const char *lib_path, int device, si_backend **out) {
     }
     if (hb->f.init(device, &hb->ctx)) {
         si_set_err("hip: device %d: %s", device, hb->f.last_error(NULL));
+        dlclose(hb->dl);
+        free(hb);
+        return SI_EIO;
+    }
+    /* Q8_0 activations as the reference's CPU path makes them: its scalar
+     * quantizer (kernels.c:542-558) when it runs the scalar kernels (no
+     * AVX2, or SI_SCALAR set; kernels.c:56-85), else the SIMD one */
+    if (si_kern_impl_get() == SI_KERN_SCALAR &&
+        hb->f.set_option(hb->ctx, "Q80_SCALAR", 1)) {
+        si_set_err("hip: %s", hb->f.last_error(hb->ctx));
+        hb->f.shutdown(hb->ctx);
         dlclose(hb->dl);
         free(hb);
         return SI_EIO;

@@ -8,6 +8,7 @@
  *   si_set_err, si_errstr           reference include/siphon/common.h:36-38
  *   si_tp (opaque lane pool)        reference include/siphon/threadpool.h:19
  *   si_backend_cpu                  reference include/siphon/tensor.h:58
+ *   si_kern_impl, si_kern_impl_get  reference include/siphon/kernels.h:28-35
  * plus the one line a Siphon tree adds to support this backend:
  *   SI_LOC_DEVICE = 2               the device location the reference leaves
  *                                   for a later backend (tensor.h:25-29);
@@ -61,5 +62,12 @@ struct si_backend {
 const char *si_errstr(void);
 void si_set_err(const char *fmt, ...);
 si_backend *si_backend_cpu(void);
+
+typedef enum {
+    SI_KERN_SCALAR = 0,
+    SI_KERN_AVX2 = 1,
+} si_kern_impl;
+
+si_kern_impl si_kern_impl_get(void);
 
 #endif /* SI_MIRROR_H */

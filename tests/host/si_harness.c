@@ -5,6 +5,7 @@
  * vtable through plain functions for ctypes. */
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "si_hip_backend.h"
@@ -35,6 +36,13 @@ static void cpu_row_to_f32(si_backend *be, const si_tensor *w, uint64_t row, flo
 static si_backend g_cpu = {"cpu", SI_LOC_HOST, NULL, cpu_row_to_f32};
 
 si_backend *si_backend_cpu(void) { return &g_cpu; }
+
+/* The reference's kernel choice as its SI_SCALAR override sets it
+ * (reference kernels.c:80-83); the harness assumes an AVX2 host otherwise. */
+si_kern_impl si_kern_impl_get(void) {
+    const char *env = getenv("SI_SCALAR");
+    return env && env[0] && strcmp(env, "0") != 0 ? SI_KERN_SCALAR : SI_KERN_AVX2;
+}
 
 static si_tensor make_tensor(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in,
                              const void *data, uint64_t bytes) {

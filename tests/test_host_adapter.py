@@ -173,3 +173,30 @@ def test_load_time_upload(harness, oracle):
         assert harness.weights(be) == (n, nbytes)
     finally:
         harness.close(be)
+
+
+@pytest.mark.gpu
+def test_si_scalar_selects_the_scalar_q8_0_quantizer(harness, oracle, monkeypatch):
+    """With SI_SCALAR set the reference quantizes Q8_0 activations with its
+    scalar routine (reference kernels.c:80-83, 542-558); the adapter opened
+    then makes the device do the same."""
+    from tests.test_gpu_q80_scalar import oracle_rows, tie_vector
+    rng = np.random.default_rng(23)
+    n_out, n_in = 64, 1024
+    W = synth.make_weights(sa.Q8_0, n_out, n_in, rng)
+    x = tie_vector(rng, n_in)
+    for scalar in (True, False):
+        if scalar:
+            monkeypatch.setenv("SI_SCALAR", "1")
+        else:
+            monkeypatch.delenv("SI_SCALAR", raising=False)
+        rc, be = harness.open(HIP_SO)
+        assert rc == 0, harness.errstr()
+        try:
+            y = np.zeros(n_out, np.float32)
+            assert harness.gemv(be, sa.Q8_0, n_out, n_in, W, x, y, n_out) == 0, harness.errstr()
+        finally:
+            harness.close(be)
+        ref, l1 = oracle_rows(oracle, sa.Q8_0, W, n_in,
+                              oracle.quantize(sa.Q8_0, x, scalar_q8_0=scalar))
+        assert np.all(np.abs(y.astype(np.float64) - ref) <= 1e-5 * l1 + 1e-6), scalar
