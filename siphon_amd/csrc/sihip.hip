@@ -21,6 +21,7 @@
 #include "gemm.h"
 #include "f32w.h"
 #include "gemm2.h"
+#include "gemm2s.h"
 #include "gemm6.h"
 #include "gemmh.h"
 #include "gemmq.h"
@@ -46,6 +47,7 @@ struct Options {
     int64_t gemmh_min_m = -1;  // smallest M on the F16 GEMM (rule: kGemmhMinM)
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
     int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0, 1, 2 (gemmq_kernel XM; rule: 1 where it fits)
+    int64_t gemm2s_max_m = -1; // largest M on the small-M Q4_K GEMM, 0: none (rule: 16)
     int64_t q80_scalar = -1;   // Q8_0 activations by the scalar quantizer (reference
                                // kernels.c:542-558, its SI_SCALAR mode), 1: on (rule: off)
 };
@@ -63,6 +65,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
     {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
     {"GEMMQ_XMODE", &Options::gemmq_xmode}, {"Q80_SCALAR", &Options::q80_scalar},
+    {"GEMM2S_MAX_M", &Options::gemm2s_max_m},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -907,6 +910,11 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
 // M = 2048: 323 against 357 us) and slower at M = 256 (67 against 50 us).
 constexpr int64_t kGemm2MinM = 384;
 static int64_t gemm2_min_m(const Options &o) { return o.gemm2_min_m > 0 ? o.gemm2_min_m : kGemm2MinM; }
+// Largest M that takes the small-M Q4_K GEMM (gemm2s.h; at most its 16-row
+// m tile); option GEMM2S_MAX_M, 0 turns it off.
+static int64_t gemm2s_max_m(const Options &o) {
+    return o.gemm2s_max_m >= 0 ? (o.gemm2s_max_m < 16 ? o.gemm2s_max_m : 16) : 16;
+}
 
 // Smallest M that takes the Q6_K GEMM (gemm6.h); option GEMM6_MIN_M. Up to
 // 4 columns the matvec kernel streams the 6.56-bit GGUF bytes once, less
@@ -938,6 +946,7 @@ static int64_t gemmq_min_m(const Options &o) { return o.gemmq_min_m > 0 ? o.gemm
 // sizes and K slices.
 struct GemmPlan {
     bool v2;           // a 16x16 kernel (Q4_K: gemm2.h, Q6_K: gemm6.h); mt counts 16-row m tiles
+    bool small = false;  // Q4_K at M <= 16: gemm2s_q4k_kernel (gemm2s.h)
     int mt;            // 32-row MFMA tiles per wave along m
     int64_t Mp;        // M rounded up to the workgroup's rows
     int64_t ws_bytes;  // quantized activation planes
@@ -1038,6 +1047,20 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
         // 448; 27648 x 5120 unsliced 48.4 against 54.8), with 64-row blocks
         // two (ffn_down at M = 512: 83.8 us in 512 against 107 in 256)
         plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB, 2, p.mt <= 2 ? ctx->n_cu : 0);
+        return p;
+    }
+    if (L.type == T_Q4_K && M <= gemm2s_max_m(ctx->opt)) {
+        // one 16-row record block, a workgroup per 32 weight rows whose
+        // waves split the super-blocks (gemm2s.h): no K slices
+        p.v2 = true;
+        p.small = true;
+        p.mt = 1;
+        p.Mp = 16;
+        p.ws_bytes = nb * g2_rec_bytes(16);
+        p.S = 1;
+        p.SBK = (int)nb;
+        p.steps = nb;
+        p.part_bytes = 0;
         return p;
     }
     if (L.type == T_Q4_K && M >= gemm2_min_m(ctx->opt)) {
@@ -1305,6 +1328,27 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
             case 2: e = launch_gemm6<2>(w, p, B, X, ldx, M, Y, ldy, st); break;
             default: e = launch_gemm6<4>(w, p, B, X, ldx, M, Y, ldy, st); break;
         }
+        if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+        return SIHIP_OK;
+    }
+    if (p.v2 && p.small) {
+        const Layout &L = w->L;
+        const int64_t nb = L.n_in / 256;
+        if (B.quant)
+            hipLaunchKernelGGL(gemm2_quantize_x<16>, dim3((unsigned)((16 * nb + 15) / 16)),
+                               dim3(kG2Threads), 0, st, X, ldx, M, (int64_t)16, nb, B.ws);
+        G2SArgs A;
+        A.w = w->gemm2;
+        A.x = B.ws;
+        A.y = Y;
+        A.ldy = ldy;
+        A.n_out = L.n_out;
+        A.M = M;
+        A.nb = (int)nb;
+        A.yscale = std::ldexp(1.0f, -w->gexp);
+        hipLaunchKernelGGL(gemm2s_q4k_kernel, dim3((unsigned)((L.n_out + 31) / 32)),
+                           dim3(kG2Threads), 0, st, A);
+        const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
         return SIHIP_OK;
     }
