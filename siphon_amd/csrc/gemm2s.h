@@ -7,17 +7,17 @@
 // the weight stream: each weight byte is read once and meets all M rows in
 // the MFMAs. The launch is shaped like a matvec rather than a GEMM:
 //   - a workgroup owns one 32-row block of the weight (one GEMM-copy chunk
-//     column) and its 4 waves split the super-blocks of the row among
-//     themselves (wave w takes c = w, w + 4, ...), so every wave streams
-//     its own chunks and n_out / 32 workgroups of 4 waves cover the matrix
-//     without K slices across workgroups;
+//     column) and its KW waves split the super-blocks of the row among
+//     themselves (wave w takes c = w, w + KW, ...), so every wave streams
+//     its own chunks and n_out / 32 workgroups cover the matrix without K
+//     slices across workgroups;
 //   - a wave keeps the next super-block's weights and activation fragments
 //     in flight while it computes the current one (two register sets);
 //   - the activation fragments (16 bytes per lane and K-step, the record's
 //     MFMA operand order) are read straight from the records in global
 //     memory, which every workgroup shares through the L2, so no LDS
 //     staging and no barrier sit in the loop;
-//   - the 4 partial 32-row tiles meet in LDS once at the end and wave 0
+//   - the KW partial 32-row tiles meet in LDS once at the end and wave 0
 //     adds them in wave order (deterministic) and stores the M rows.
 #pragma once
 
@@ -25,7 +25,6 @@
 
 namespace sihip {
 
-constexpr int kG2SWaves = 4;
 
 struct G2SArgs {
     const uint8_t *w;     // GEMM-copy chunks [nblk32][nb] (gemm2.h)
@@ -37,11 +36,13 @@ struct G2SArgs {
     float yscale;         // 2^-E
 };
 
-__global__ __launch_bounds__(kG2Threads)
+// KW: waves per workgroup, which split the super-blocks of its 32 rows.
+template <int KW>
+__global__ __launch_bounds__(64 * KW)
 __attribute__((amdgpu_waves_per_eu(2))) void gemm2s_q4k_kernel(G2SArgs A) {
     constexpr int BM = 16;
     constexpr int kRec = g2_rec_bytes(BM);
-    __shared__ __attribute__((aligned(16))) float red[kG2SWaves - 1][2][4][64];
+    __shared__ __attribute__((aligned(16))) float red[KW - 1][2][4][64];
     const int blk = blockIdx.x;  // 32-row block
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -67,7 +68,11 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemm2s_q4k_kernel(G2SArgs A) {
         return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
     };
     auto load = [&](int c, Stage &s) {
-        const int so = c * kG2ChunkQ4K, xo = c * kRec;
+        // c is wave-uniform; readfirstlane keeps the offsets scalar (a loop
+        // counter the compiler holds in a VGPR would make every buffer load
+        // a waterfall loop over lanes)
+        const int cu = __builtin_amdgcn_readfirstlane(c);
+        const int so = cu * kG2ChunkQ4K, xo = cu * kRec;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) s.nib[ks] = ld4(wr, v_nib + ks * 1024, so);
 #pragma unroll
@@ -130,13 +135,13 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemm2s_q4k_kernel(G2SArgs A) {
     int c = wave;
     if (c < A.nb) load(c, s0);
     while (c < A.nb) {
-        if (c + kG2SWaves < A.nb) load(c + kG2SWaves, s1);
+        if (c + KW < A.nb) load(c + KW, s1);
         compute(s0);
-        c += kG2SWaves;
+        c += KW;
         if (c >= A.nb) break;
-        if (c + kG2SWaves < A.nb) load(c + kG2SWaves, s0);
+        if (c + KW < A.nb) load(c + KW, s0);
         compute(s1);
-        c += kG2SWaves;
+        c += KW;
     }
     // partial tiles of waves 1..3 to LDS; wave 0 adds them in wave order
     if (wave > 0) {
@@ -148,7 +153,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemm2s_q4k_kernel(G2SArgs A) {
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
-    for (int wv = 0; wv < kG2SWaves - 1; wv++)
+    for (int wv = 0; wv < KW - 1; wv++)
 #pragma unroll
         for (int nt = 0; nt < 2; nt++)
 #pragma unroll

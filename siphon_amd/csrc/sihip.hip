@@ -22,6 +22,7 @@
 #include "f32w.h"
 #include "gemm2.h"
 #include "gemm2s.h"
+#include "gemm6s.h"
 #include "gemm6.h"
 #include "gemmh.h"
 #include "gemmq.h"
@@ -48,6 +49,8 @@ struct Options {
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
     int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0, 1, 2 (gemmq_kernel XM; rule: 1 where it fits)
     int64_t gemm2s_max_m = -1; // largest M on the small-M Q4_K GEMM, 0: none (rule: 16)
+    int64_t gemm6s_max_m = -1; // largest M on the small-M Q6_K GEMM, 0: none (rule: 16)
+    int64_t gemms_waves = -1;  // waves per workgroup of the small-M GEMMs, 4 or 8 (rule: by rows)
     int64_t q80_scalar = -1;   // Q8_0 activations by the scalar quantizer (reference
                                // kernels.c:542-558, its SI_SCALAR mode), 1: on (rule: off)
 };
@@ -65,7 +68,8 @@ static const OptionName kOptionNames[] = {
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
     {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
     {"GEMMQ_XMODE", &Options::gemmq_xmode}, {"Q80_SCALAR", &Options::q80_scalar},
-    {"GEMM2S_MAX_M", &Options::gemm2s_max_m},
+    {"GEMM2S_MAX_M", &Options::gemm2s_max_m}, {"GEMM6S_MAX_M", &Options::gemm6s_max_m},
+    {"GEMMS_WAVES", &Options::gemms_waves},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -128,6 +132,10 @@ struct sihip_weight {
     // -dmin * mn * 2^E)
     uint8_t *gemm2 = nullptr;
     int64_t gemm2_bytes = 0;
+    // Q6_K: the GGUF-size copy of the small-M GEMM (gemm6s.h), built on the
+    // first call with 5 <= M <= 16 or by sihip_weight_prepare_gemm
+    uint8_t *gsmall = nullptr;
+    int64_t gsmall_bytes = 0;
     int gexp = 0;
     // column slices of the matvec (split == 1: whole rows per workgroup);
     // part and cnt live in the same allocation as the planes
@@ -501,13 +509,14 @@ extern "C" int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w) {
     (void)hipFree(w->dev);
     if (w->gemm) (void)hipFree(w->gemm);
     if (w->gemm2) (void)hipFree(w->gemm2);
+    if (w->gsmall) (void)hipFree(w->gsmall);
     order_free(w->order);
     delete w;
     return SIHIP_OK;
 }
 
 extern "C" uint64_t sihip_weight_device_bytes(const sihip_weight *w) {
-    return w ? (uint64_t)(w->L.total_bytes + w->split_bytes + w->gemm_bytes + w->gemm2_bytes) : 0;
+    return w ? (uint64_t)(w->L.total_bytes + w->split_bytes + w->gemm_bytes + w->gemm2_bytes + w->gsmall_bytes) : 0;
 }
 
 extern "C" int sihip_weight_tile_cols(const sihip_weight *w) { return w ? w->L.G : 0; }
@@ -888,6 +897,35 @@ static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     return SIHIP_OK;
 }
 
+static int64_t gemm6s_max_m(const Options &o);
+
+// The GGUF-size Q6_K copy of the small-M GEMM (gemm6s.h).
+static int build_gemm6s_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
+    if (capturing(st))
+        return set_err(ctx, SIHIP_EINVAL,
+                       "the weight's GEMM copy would be built during graph capture: call "
+                       "sihip_weight_prepare_gemm before capturing");
+    const Layout &L = w->L;
+    const int64_t nblk32 = (L.n_out + 31) / 32;
+    const int64_t bytes = gemm6s_layout_bytes(nblk32, L.n_in / 256);
+    const int64_t threads = nblk32 * (L.n_in / 256) * (kG6SChunk / 16);
+    uint8_t *g = nullptr;
+    hipError_t e = hipMalloc(&g, (size_t)bytes);
+    if (e != hipSuccess)
+        return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
+                       hipGetErrorString(e));
+    hipLaunchKernelGGL(gemm6s_layout_q6k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       L, (const uint8_t *)w->dev, g, nblk32);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        (void)hipFree(g);
+        return set_err(ctx, SIHIP_EDEVICE, "gemm layout: %s", hipGetErrorString(e));
+    }
+    w->gsmall = g;
+    w->gsmall_bytes = bytes;
+    return SIHIP_OK;
+}
+
 extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
     if (!ctx || !w) return set_err(ctx, SIHIP_EINVAL, "weight_prepare_gemm: NULL argument");
     if (!gemm_mfma_supported(w->L)) return SIHIP_OK;
@@ -898,6 +936,10 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
     }
     if (gemm16_supported(w->L) && !w->gemm2) {
         const int rc = build_gemm2_copy(ctx, w, ctx->stream);
+        if (rc) return rc;
+    }
+    if (w->L.type == T_Q6_K && gemm6s_max_m(ctx->opt) > 0 && !w->gsmall) {
+        const int rc = build_gemm6s_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
     HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
@@ -914,6 +956,11 @@ static int64_t gemm2_min_m(const Options &o) { return o.gemm2_min_m > 0 ? o.gemm
 // m tile); option GEMM2S_MAX_M, 0 turns it off.
 static int64_t gemm2s_max_m(const Options &o) {
     return o.gemm2s_max_m >= 0 ? (o.gemm2s_max_m < 16 ? o.gemm2s_max_m : 16) : 16;
+}
+// Largest M that takes the small-M Q6_K GEMM (gemm6s.h; at most 16);
+// option GEMM6S_MAX_M, 0 turns it off.
+static int64_t gemm6s_max_m(const Options &o) {
+    return o.gemm6s_max_m >= 0 ? (o.gemm6s_max_m < 16 ? o.gemm6s_max_m : 16) : 16;
 }
 
 // Smallest M that takes the Q6_K GEMM (gemm6.h); option GEMM6_MIN_M. Up to
@@ -1025,6 +1072,20 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
                         p.mt <= 4 ? 3 * ctx->n_cu / 4 : 0);
         else
             plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, 5, (p.mt == 1 ? 2 : 3) * ctx->n_cu);
+        return p;
+    }
+    if (L.type == T_Q6_K && M <= gemm6s_max_m(ctx->opt)) {
+        // one 16-row record block, a workgroup per 32 weight rows whose
+        // waves split the super-blocks, the GGUF-size copy (gemm6s.h)
+        p.v2 = true;
+        p.small = true;
+        p.mt = 1;
+        p.Mp = 16;
+        p.ws_bytes = nb * g2_rec_bytes(16);
+        p.S = 1;
+        p.SBK = (int)nb;
+        p.steps = nb;
+        p.part_bytes = 0;
         return p;
     }
     if (L.type == T_Q6_K) {
@@ -1295,6 +1356,16 @@ static hipError_t launch_gemm6(const sihip_weight *w, const GemmPlan &p, const G
     return hipGetLastError();
 }
 
+// Waves per workgroup of the small-M GEMMs (gemm2s.h, gemm6s.h), which
+// split a 32-row block's super-blocks: 8 while the blocks are fewer than
+// the CUs, so the waves still fill the SIMDs, else 4 (M = 8: Q4_K 4096 x
+// 4096 10.0 us per call in 8 against 10.5 in 4, 14336 x 4096 15.9 in 4
+// against 17.4 in 8); the GEMMS_WAVES option (4 or 8) overrides.
+static int small_gemm_waves(const sihip_ctx *ctx, const Layout &L) {
+    if (ctx->opt.gemms_waves == 4 || ctx->opt.gemms_waves == 8) return (int)ctx->opt.gemms_waves;
+    return (L.n_out + 31) / 32 < ctx->n_cu ? 8 : 4;
+}
+
 static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPlan &p,
                             const GemmBufs &B, const float *X, int64_t ldx, int64_t M, float *Y,
                             int64_t ldy, hipStream_t st) {
@@ -1318,6 +1389,36 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
             case 4: e = launch_gemmh<4>(w, p, B, X, ldx, M, Y, ldy, st); break;
             default: e = launch_gemmh<8>(w, p, B, X, ldx, M, Y, ldy, st); break;
         }
+        if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+        return SIHIP_OK;
+    }
+    if (p.v2 && p.small && L.type == T_Q6_K) {
+        const int64_t nb = L.n_in / 256;
+        if (B.quant)
+            hipLaunchKernelGGL(gemm2_quantize_x<16>, dim3((unsigned)((16 * nb + 15) / 16)),
+                               dim3(kG2Threads), 0, st, X, ldx, M, (int64_t)16, nb, B.ws);
+        G6SArgs A;
+        A.w = w->gsmall;
+        A.x = B.ws;
+        A.y = Y;
+        A.ldy = ldy;
+        A.n_out = L.n_out;
+        A.M = M;
+        A.nb = (int)nb;
+        const dim3 grid((unsigned)((L.n_out + 31) / 32));
+        const bool w4 = small_gemm_waves(ctx, L) == 4;
+        const dim3 blk(w4 ? 256 : 512);
+        switch ((M + 3) / 4) {
+            case 1: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<1, 4>), grid, blk, 0, st, A);
+                    else hipLaunchKernelGGL((gemm6s_q6k_kernel<1, 8>), grid, blk, 0, st, A); break;
+            case 2: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<2, 4>), grid, blk, 0, st, A);
+                    else hipLaunchKernelGGL((gemm6s_q6k_kernel<2, 8>), grid, blk, 0, st, A); break;
+            case 3: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<3, 4>), grid, blk, 0, st, A);
+                    else hipLaunchKernelGGL((gemm6s_q6k_kernel<3, 8>), grid, blk, 0, st, A); break;
+            default: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<4, 4>), grid, blk, 0, st, A);
+                     else hipLaunchKernelGGL((gemm6s_q6k_kernel<4, 8>), grid, blk, 0, st, A); break;
+        }
+        const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
         return SIHIP_OK;
     }
@@ -1346,8 +1447,11 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
         A.M = M;
         A.nb = (int)nb;
         A.yscale = std::ldexp(1.0f, -w->gexp);
-        hipLaunchKernelGGL(gemm2s_q4k_kernel, dim3((unsigned)((L.n_out + 31) / 32)),
-                           dim3(kG2Threads), 0, st, A);
+        const dim3 grid((unsigned)((L.n_out + 31) / 32));
+        if (small_gemm_waves(ctx, L) == 4)
+            hipLaunchKernelGGL(gemm2s_q4k_kernel<4>, grid, dim3(256), 0, st, A);
+        else
+            hipLaunchKernelGGL(gemm2s_q4k_kernel<8>, grid, dim3(512), 0, st, A);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
         return SIHIP_OK;
@@ -1418,6 +1522,19 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
     return SIHIP_OK;
 }
 
+// The GEMM copy a plan's kernel reads: the small-M Q6_K copy, the 16x16
+// kernels' copy or the 32-row K-quant GEMM's copy.
+static const uint8_t *plan_copy(const sihip_weight *w, const GemmPlan &p) {
+    if (p.small && w->L.type == T_Q6_K) return w->gsmall;
+    return p.v2 ? w->gemm2 : w->gemm;
+}
+
+static int build_plan_copy(sihip_ctx *ctx, sihip_weight *w, const GemmPlan &p, hipStream_t st) {
+    if (plan_copy(w, p)) return SIHIP_OK;
+    if (p.small && w->L.type == T_Q6_K) return build_gemm6s_copy(ctx, w, st);
+    return p.v2 ? build_gemm2_copy(ctx, w, st) : build_gemm_copy(ctx, w, st);
+}
+
 // The MFMA GEMM on the context's workspaces (grown as needed, outside
 // graph capture) and the weight's GEMM copy (built on first use). The
 // activation planes live in the context, so calls on one context must not
@@ -1426,15 +1543,9 @@ static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X,
                          int64_t M, float *Y, int64_t ldy, hipStream_t st) {
     sihip_weight *w = const_cast<sihip_weight *>(wc);  // the GEMM copies are caches of w
     const GemmPlan p = plan_gemm(ctx, w->L, M);
-    if (p.v2 && !w->gemm2) {
-        const int rc = build_gemm2_copy(ctx, w, st);
-        if (rc) return rc;
-    }
-    if (!p.v2 && !w->gemm) {
-        const int rc = build_gemm_copy(ctx, w, st);
-        if (rc) return rc;
-    }
-    int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)p.ws_bytes, st);
+    int rc = build_plan_copy(ctx, w, p, st);
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, (size_t)p.ws_bytes, st);
     if (rc) return rc;
     if (p.S > 1) {
         rc = ensure(ctx, &ctx->d_gpart, &ctx->d_gpart_cap, (size_t)p.part_bytes, st);
@@ -1510,14 +1621,8 @@ static int run_gemm_multi(sihip_ctx *ctx, int count, const sihip_weight *const *
     }
     for (int i = 0; i < count; i++) {
         sihip_weight *w = const_cast<sihip_weight *>(wc[i]);  // GEMM copies are caches of w
-        if (plan[i].v2 && !w->gemm2) {
-            const int rc = build_gemm2_copy(ctx, w, st);
-            if (rc) return rc;
-        }
-        if (!plan[i].v2 && !w->gemm) {
-            const int rc = build_gemm_copy(ctx, w, st);
-            if (rc) return rc;
-        }
+        const int rc = build_plan_copy(ctx, w, plan[i], st);
+        if (rc) return rc;
     }
     int rc = ensure(ctx, &ctx->d_ws, &ctx->d_ws_cap, total, st);
     if (rc) return rc;
@@ -1688,7 +1793,7 @@ extern "C" int sihip_gemm_dev_noalloc(sihip_ctx *ctx, const sihip_weight *w, con
     if (!gemm_on_mfma(ctx, w, M))
         return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out, st);
     GemmPlan p = plan_gemm(ctx, w->L, M);
-    if (!(p.v2 ? w->gemm2 : w->gemm))
+    if (!plan_copy(w, p))
         return set_err(ctx, SIHIP_EINVAL,
                        "gemm_dev_noalloc: the weight has no GEMM copy; call "
                        "sihip_weight_prepare_gemm first");
