@@ -22,7 +22,7 @@
 #include "f32w.h"
 #include "gemm2.h"
 #include "gemm2s.h"
-#include "gemm6s.h"
+#include "gemmks.h"
 #include "gemm6.h"
 #include "gemmh.h"
 #include "gemmq.h"
@@ -49,7 +49,8 @@ struct Options {
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
     int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0, 1, 2 (gemmq_kernel XM; rule: 1 where it fits)
     int64_t gemm2s_max_m = -1; // largest M on the small-M Q4_K GEMM, 0: none (rule: 16)
-    int64_t gemm6s_max_m = -1; // largest M on the small-M Q6_K GEMM, 0: none (rule: 16)
+    int64_t gemmks_max_m = -1; // largest M on the small-M K-quant GEMM, 0: none (rule: 16)
+    int64_t gemmks_q4k = -1;   // Q4_K small M on gemmks.h (1) or gemm2s.h (0) (rule: 0)
     int64_t gemms_waves = -1;  // waves per workgroup of the small-M GEMMs, 4 or 8 (rule: by rows)
     int64_t q80_scalar = -1;   // Q8_0 activations by the scalar quantizer (reference
                                // kernels.c:542-558, its SI_SCALAR mode), 1: on (rule: off)
@@ -68,7 +69,8 @@ static const OptionName kOptionNames[] = {
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
     {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
     {"GEMMQ_XMODE", &Options::gemmq_xmode}, {"Q80_SCALAR", &Options::q80_scalar},
-    {"GEMM2S_MAX_M", &Options::gemm2s_max_m}, {"GEMM6S_MAX_M", &Options::gemm6s_max_m},
+    {"GEMM2S_MAX_M", &Options::gemm2s_max_m}, {"GEMMKS_MAX_M", &Options::gemmks_max_m},
+    {"GEMMKS_Q4K", &Options::gemmks_q4k},
     {"GEMMS_WAVES", &Options::gemms_waves},
 };
 
@@ -132,8 +134,9 @@ struct sihip_weight {
     // -dmin * mn * 2^E)
     uint8_t *gemm2 = nullptr;
     int64_t gemm2_bytes = 0;
-    // Q6_K: the GGUF-size copy of the small-M GEMM (gemm6s.h), built on the
-    // first call with 5 <= M <= 16 or by sihip_weight_prepare_gemm
+    // K-quants: the near-GGUF-size copy of the small-M GEMM (gemmks.h),
+    // built on the first call with 5 <= M <= 16 or by
+    // sihip_weight_prepare_gemm
     uint8_t *gsmall = nullptr;
     int64_t gsmall_bytes = 0;
     int gexp = 0;
@@ -897,25 +900,32 @@ static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     return SIHIP_OK;
 }
 
-static int64_t gemm6s_max_m(const Options &o);
+static int64_t gemmks_max_m(const Options &o);
 
-// The GGUF-size Q6_K copy of the small-M GEMM (gemm6s.h).
-static int build_gemm6s_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
+// The near-GGUF-size K-quant copy of the small-M GEMM (gemmks.h).
+static int build_gemmks_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     if (capturing(st))
         return set_err(ctx, SIHIP_EINVAL,
                        "the weight's GEMM copy would be built during graph capture: call "
                        "sihip_weight_prepare_gemm before capturing");
     const Layout &L = w->L;
-    const int64_t nblk32 = (L.n_out + 31) / 32;
-    const int64_t bytes = gemm6s_layout_bytes(nblk32, L.n_in / 256);
-    const int64_t threads = nblk32 * (L.n_in / 256) * (kG6SChunk / 16);
+    const int64_t nblk32 = (L.n_out + 31) / 32, nb = L.n_in / 256;
+    const int64_t bytes = nblk32 * nb * gemmks_chunk(L.type);
+    const int64_t threads = nblk32 * nb * (gemmks_chunk(L.type) / 16);
     uint8_t *g = nullptr;
     hipError_t e = hipMalloc(&g, (size_t)bytes);
     if (e != hipSuccess)
         return set_err(ctx, SIHIP_ENOMEM, "gemm weight copy (%lld bytes): %s", (long long)bytes,
                        hipGetErrorString(e));
-    hipLaunchKernelGGL(gemm6s_layout_q6k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
-                       L, (const uint8_t *)w->dev, g, nblk32);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    const uint8_t *src = (const uint8_t *)w->dev;
+    switch (L.type) {
+        case T_Q2_K: hipLaunchKernelGGL(gemmks_layout<T_Q2_K>, grid, dim3(256), 0, st, L, src, g, nblk32); break;
+        case T_Q3_K: hipLaunchKernelGGL(gemmks_layout<T_Q3_K>, grid, dim3(256), 0, st, L, src, g, nblk32); break;
+        case T_Q4_K: hipLaunchKernelGGL(gemmks_layout<T_Q4_K>, grid, dim3(256), 0, st, L, src, g, nblk32); break;
+        case T_Q5_K: hipLaunchKernelGGL(gemmks_layout<T_Q5_K>, grid, dim3(256), 0, st, L, src, g, nblk32); break;
+        default: hipLaunchKernelGGL(gemmks_layout<T_Q6_K>, grid, dim3(256), 0, st, L, src, g, nblk32); break;
+    }
     e = hipGetLastError();
     if (e != hipSuccess) {
         (void)hipFree(g);
@@ -938,8 +948,9 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
         const int rc = build_gemm2_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
-    if (w->L.type == T_Q6_K && gemm6s_max_m(ctx->opt) > 0 && !w->gsmall) {
-        const int rc = build_gemm6s_copy(ctx, w, ctx->stream);
+    if (is_kquant(w->L.type) && gemmks_max_m(ctx->opt) > 0 && !w->gsmall &&
+        !(w->L.type == T_Q4_K && ctx->opt.gemmks_q4k != 1)) {
+        const int rc = build_gemmks_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
     HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
@@ -957,10 +968,10 @@ static int64_t gemm2_min_m(const Options &o) { return o.gemm2_min_m > 0 ? o.gemm
 static int64_t gemm2s_max_m(const Options &o) {
     return o.gemm2s_max_m >= 0 ? (o.gemm2s_max_m < 16 ? o.gemm2s_max_m : 16) : 16;
 }
-// Largest M that takes the small-M Q6_K GEMM (gemm6s.h; at most 16);
-// option GEMM6S_MAX_M, 0 turns it off.
-static int64_t gemm6s_max_m(const Options &o) {
-    return o.gemm6s_max_m >= 0 ? (o.gemm6s_max_m < 16 ? o.gemm6s_max_m : 16) : 16;
+// Largest M that takes the small-M K-quant GEMM (gemmks.h; at most 16);
+// option GEMMKS_MAX_M, 0 turns it off.
+static int64_t gemmks_max_m(const Options &o) {
+    return o.gemmks_max_m >= 0 ? (o.gemmks_max_m < 16 ? o.gemmks_max_m : 16) : 16;
 }
 
 // Smallest M that takes the Q6_K GEMM (gemm6.h); option GEMM6_MIN_M. Up to
@@ -993,7 +1004,8 @@ static int64_t gemmq_min_m(const Options &o) { return o.gemmq_min_m > 0 ? o.gemm
 // sizes and K slices.
 struct GemmPlan {
     bool v2;           // a 16x16 kernel (Q4_K: gemm2.h, Q6_K: gemm6.h); mt counts 16-row m tiles
-    bool small = false;  // Q4_K at M <= 16: gemm2s_q4k_kernel (gemm2s.h)
+    bool small = false;  // M <= 16: gemmks_kernel (gemmks.h), or for Q4_K gemm2s_q4k_kernel
+    bool q4s = false;    // Q4_K small M on gemm2s.h (the 16x16 GEMM's copy)
     int mt;            // 32-row MFMA tiles per wave along m
     int64_t Mp;        // M rounded up to the workgroup's rows
     int64_t ws_bytes;  // quantized activation planes
@@ -1074,9 +1086,13 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
             plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, 5, (p.mt == 1 ? 2 : 3) * ctx->n_cu);
         return p;
     }
-    if (L.type == T_Q6_K && M <= gemm6s_max_m(ctx->opt)) {
+    // (Q4_K: gemm2s.h below, unless the GEMMKS_Q4K option is 1; on the
+    // Llama-3-8B shapes at M = 8 it took 10.0 / 7.9 / 15.8 us per call for
+    // 4096 / 1024 / 14336 x 4096 against 10.9 / 9.9 / 16.0 here)
+    if (is_kquant(L.type) && M <= gemmks_max_m(ctx->opt) &&
+        !(L.type == T_Q4_K && ctx->opt.gemmks_q4k != 1)) {
         // one 16-row record block, a workgroup per 32 weight rows whose
-        // waves split the super-blocks, the GGUF-size copy (gemm6s.h)
+        // waves split the super-blocks, the near-GGUF-size copy (gemmks.h)
         p.v2 = true;
         p.small = true;
         p.mt = 1;
@@ -1115,6 +1131,7 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
         // waves split the super-blocks (gemm2s.h): no K slices
         p.v2 = true;
         p.small = true;
+        p.q4s = true;
         p.mt = 1;
         p.Mp = 16;
         p.ws_bytes = nb * g2_rec_bytes(16);
@@ -1356,14 +1373,42 @@ static hipError_t launch_gemm6(const sihip_weight *w, const GemmPlan &p, const G
     return hipGetLastError();
 }
 
-// Waves per workgroup of the small-M GEMMs (gemm2s.h, gemm6s.h), which
-// split a 32-row block's super-blocks: 8 while the blocks are fewer than
-// the CUs, so the waves still fill the SIMDs, else 4 (M = 8: Q4_K 4096 x
-// 4096 10.0 us per call in 8 against 10.5 in 4, 14336 x 4096 15.9 in 4
-// against 17.4 in 8); the GEMMS_WAVES option (4 or 8) overrides.
+template <uint32_t FMT, int NH>
+static void launch_gemmks_nh(int kw, dim3 grid, hipStream_t st, const GKSArgs &A) {
+    constexpr int SW = gemmks_sw<FMT, NH>();
+    if (kw == 2)
+        hipLaunchKernelGGL((gemmks_kernel<FMT, NH, 2, SW>), grid, dim3(128), 0, st, A);
+    else if (kw == 4)
+        hipLaunchKernelGGL((gemmks_kernel<FMT, NH, 4, SW>), grid, dim3(256), 0, st, A);
+    else
+        hipLaunchKernelGGL((gemmks_kernel<FMT, NH, 8, SW>), grid, dim3(512), 0, st, A);
+}
+
+// The small-M K-quant GEMM for M <= 4 nh activation rows.
+template <uint32_t FMT>
+static void launch_gemmks(int nh, int kw, dim3 grid, hipStream_t st, const GKSArgs &A) {
+    switch (nh) {
+        case 1: launch_gemmks_nh<FMT, 1>(kw, grid, st, A); break;
+        case 2: launch_gemmks_nh<FMT, 2>(kw, grid, st, A); break;
+        case 3: launch_gemmks_nh<FMT, 3>(kw, grid, st, A); break;
+        default: launch_gemmks_nh<FMT, 4>(kw, grid, st, A); break;
+    }
+}
+
+// Waves per workgroup of the small-M GEMMs (gemm2s.h, gemmks.h), which
+// split a 32-row block's super-blocks: the most of 8, 4, 2 that keep the
+// launch's waves within 10 per CU (about 2.5 per SIMD: two resident at the
+// VGPRs these kernels use, so the workgroups run in little more than one
+// round). M = 8, per call: Q2_K 27648 x 5120 (864 blocks) 23.6 us in 2
+// waves, 25.4 in 4, 32.2 in 8; 5120 x 27648 (160 blocks) 28.5 in 8, 32.7
+// in 4, 56.9 in 2; Q4_K 14336 x 4096 (448 blocks) 15.9 in 4 against 17.4
+// in 8. The Q4_K kernel of gemm2s.h has 4 and 8. The GEMMS_WAVES option (2,
+// 4 or 8) overrides.
 static int small_gemm_waves(const sihip_ctx *ctx, const Layout &L) {
-    if (ctx->opt.gemms_waves == 4 || ctx->opt.gemms_waves == 8) return (int)ctx->opt.gemms_waves;
-    return (L.n_out + 31) / 32 < ctx->n_cu ? 8 : 4;
+    if (ctx->opt.gemms_waves == 2 || ctx->opt.gemms_waves == 4 || ctx->opt.gemms_waves == 8)
+        return (int)ctx->opt.gemms_waves;
+    const int64_t blocks = (L.n_out + 31) / 32, room = 10 * (int64_t)ctx->n_cu;
+    return blocks * 8 <= room ? 8 : blocks * 4 <= room ? 4 : 2;
 }
 
 static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPlan &p,
@@ -1392,12 +1437,12 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
         if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
         return SIHIP_OK;
     }
-    if (p.v2 && p.small && L.type == T_Q6_K) {
+    if (p.v2 && p.small && !p.q4s) {
         const int64_t nb = L.n_in / 256;
         if (B.quant)
             hipLaunchKernelGGL(gemm2_quantize_x<16>, dim3((unsigned)((16 * nb + 15) / 16)),
                                dim3(kG2Threads), 0, st, X, ldx, M, (int64_t)16, nb, B.ws);
-        G6SArgs A;
+        GKSArgs A;
         A.w = w->gsmall;
         A.x = B.ws;
         A.y = Y;
@@ -1406,17 +1451,14 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
         A.M = M;
         A.nb = (int)nb;
         const dim3 grid((unsigned)((L.n_out + 31) / 32));
-        const bool w4 = small_gemm_waves(ctx, L) == 4;
-        const dim3 blk(w4 ? 256 : 512);
-        switch ((M + 3) / 4) {
-            case 1: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<1, 4>), grid, blk, 0, st, A);
-                    else hipLaunchKernelGGL((gemm6s_q6k_kernel<1, 8>), grid, blk, 0, st, A); break;
-            case 2: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<2, 4>), grid, blk, 0, st, A);
-                    else hipLaunchKernelGGL((gemm6s_q6k_kernel<2, 8>), grid, blk, 0, st, A); break;
-            case 3: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<3, 4>), grid, blk, 0, st, A);
-                    else hipLaunchKernelGGL((gemm6s_q6k_kernel<3, 8>), grid, blk, 0, st, A); break;
-            default: if (w4) hipLaunchKernelGGL((gemm6s_q6k_kernel<4, 4>), grid, blk, 0, st, A);
-                     else hipLaunchKernelGGL((gemm6s_q6k_kernel<4, 8>), grid, blk, 0, st, A); break;
+        const int kw = small_gemm_waves(ctx, L);
+        const int nh = (int)((M + 3) / 4);
+        switch (L.type) {
+            case T_Q2_K: launch_gemmks<T_Q2_K>(nh, kw, grid, st, A); break;
+            case T_Q3_K: launch_gemmks<T_Q3_K>(nh, kw, grid, st, A); break;
+            case T_Q4_K: launch_gemmks<T_Q4_K>(nh, kw, grid, st, A); break;
+            case T_Q5_K: launch_gemmks<T_Q5_K>(nh, kw, grid, st, A); break;
+            default: launch_gemmks<T_Q6_K>(nh, kw, grid, st, A); break;
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
@@ -1448,7 +1490,7 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
         A.nb = (int)nb;
         A.yscale = std::ldexp(1.0f, -w->gexp);
         const dim3 grid((unsigned)((L.n_out + 31) / 32));
-        if (small_gemm_waves(ctx, L) == 4)
+        if (small_gemm_waves(ctx, L) < 8)
             hipLaunchKernelGGL(gemm2s_q4k_kernel<4>, grid, dim3(256), 0, st, A);
         else
             hipLaunchKernelGGL(gemm2s_q4k_kernel<8>, grid, dim3(512), 0, st, A);
@@ -1525,13 +1567,13 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
 // The GEMM copy a plan's kernel reads: the small-M Q6_K copy, the 16x16
 // kernels' copy or the 32-row K-quant GEMM's copy.
 static const uint8_t *plan_copy(const sihip_weight *w, const GemmPlan &p) {
-    if (p.small && w->L.type == T_Q6_K) return w->gsmall;
+    if (p.small && !(w->L.type == T_Q4_K && p.q4s)) return w->gsmall;
     return p.v2 ? w->gemm2 : w->gemm;
 }
 
 static int build_plan_copy(sihip_ctx *ctx, sihip_weight *w, const GemmPlan &p, hipStream_t st) {
     if (plan_copy(w, p)) return SIHIP_OK;
-    if (p.small && w->L.type == T_Q6_K) return build_gemm6s_copy(ctx, w, st);
+    if (p.small && !(w->L.type == T_Q4_K && p.q4s)) return build_gemmks_copy(ctx, w, st);
     return p.v2 ? build_gemm2_copy(ctx, w, st) : build_gemm_copy(ctx, w, st);
 }
 
