@@ -73,7 +73,9 @@ const char *sihip_last_error(const sihip_ctx *ctx);
  * restores the built-in rule. Names: WG_PER_CU, WAVE_TARGET, SPLIT_ELEMS,
  * TILE_COLS (these four apply to later uploads and launches), GEMM_MIN_M,
  * GEMM_MT, GEMM_SBK, GEMM2_MIN_M, GEMM2_WAVES, GEMM6_MIN_M, GEMMH_MIN_M,
- * GEMMQ_MIN_M, GEMMQ_XMODE, and Q80_SCALAR: 1 quantizes Q8_0-pair
+ * GEMMQ_MIN_M, GEMMQ_XMODE, GEMM2S_MAX_M, GEMMKS_MAX_M (the largest M on
+ * the small-M K-quant GEMMs, 0: none), GEMMKS_Q4K, GEMMS_WAVES, and
+ * Q80_SCALAR: 1 quantizes Q8_0-pair
  * activations with the reference's portable scalar routine (reference
  * kernels.c:542-558), as the reference does when SI_SCALAR is set or the
  * host lacks AVX2 (kernels.c:56-85); the rule is the SIMD routine
@@ -95,8 +97,8 @@ int sihip_weight_upload(sihip_ctx *ctx, uint32_t ggml_type, uint64_t n_out,
                         uint64_t bytes, sihip_weight **out);
 int sihip_weight_free(sihip_ctx *ctx, sihip_weight *w);
 /* Build now the weight's second device copy in the order of the
- * matrix-core GEMM (Q4_K, Q5_K, Q2_K, Q3_K; other types: no-op), which sihip_gemm
- * otherwise builds on its first call with M >= 5. No reference
+ * matrix-core GEMMs (the K-quants, F16, Q4_0, Q5_0, Q8_0), which sihip_gemm
+ * otherwise builds on its first call with M >= 3. No reference
  * counterpart: it belongs to the batched prefill slot, which the reference
  * lacks (its prompt runs token by token, cmd_run.c:275-283). For loaders
  * that put everything on the device before the first token. Idempotent. */

@@ -135,7 +135,7 @@ struct sihip_weight {
     uint8_t *gemm2 = nullptr;
     int64_t gemm2_bytes = 0;
     // K-quants: the near-GGUF-size copy of the small-M GEMM (gemmks.h),
-    // built on the first call with 5 <= M <= 16 or by
+    // built on the first call with 3 <= M <= 16 or by
     // sihip_weight_prepare_gemm
     uint8_t *gsmall = nullptr;
     int64_t gsmall_bytes = 0;
@@ -782,9 +782,13 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 // at M = 4 takes 17.5 us there against 22 us on the matrix cores, at M = 8
 // 33.7 against 22). Q5_K, Q2_K and Q3_K use the same threshold: at M = 8
 // (config 4's 32B-class shapes) their matrix-core calls take 2.0-3.9x less
-// time than the matvec kernel's. The GEMM_MIN_M option overrides it (tests
-// force both paths).
-static int64_t gemm_min_m(const Options &o) { return o.gemm_min_m > 0 ? o.gemm_min_m : 5; }
+// time than the matvec kernel's. With the small-M kernels (gemm2s.h,
+// gemmks.h) the threshold is 3: Llama-3-8B shapes per call at M = 3, matvec
+// against small-M kernel: q/k/v 28.6 / 22.1 us, gate/up 35.5 / 27.8,
+// ffn_down (Q6_K) 27.6 / 18.8; at M = 4 27.7 / 22.4, 31.9 / 28.2, 21.4 /
+// 18.9; at M = 2 the matvec kernel wins (17.1 / 21.8, 19.8 / 27.7, 15.7 /
+// 18.7). The GEMM_MIN_M option overrides it (tests force both paths).
+static int64_t gemm_min_m(const Options &o) { return o.gemm_min_m > 0 ? o.gemm_min_m : 3; }
 
 static bool is_q80_pair(uint32_t t) { return t == T_Q4_0 || t == T_Q5_0 || t == T_Q8_0; }
 
@@ -974,12 +978,12 @@ static int64_t gemmks_max_m(const Options &o) {
     return o.gemmks_max_m >= 0 ? (o.gemmks_max_m < 16 ? o.gemmks_max_m : 16) : 16;
 }
 
-// Smallest M that takes the Q6_K GEMM (gemm6.h); option GEMM6_MIN_M. Up to
-// 4 columns the matvec kernel streams the 6.56-bit GGUF bytes once, less
-// traffic than the GEMM's 2-byte digit copy; from 5 it would stream them
-// twice or more (ffn_down 4096 x 14336 at M = 8: 44.8 us on the matvec
-// kernel, 34.4 us on the GEMM).
-constexpr int64_t kGemm6MinM = 5;
+// Smallest M that takes a Q6_K GEMM (the small-M kernel of gemmks.h up to
+// M = 16, gemm6.h above); option GEMM6_MIN_M. As for the other K-quants
+// (gemm_min_m) 3: the small-M kernel streams the GGUF bytes once, so it
+// wins from M = 3 (ffn_down 4096 x 14336: 18.8 against 27.6 us on the
+// matvec kernel), which stays faster at M = 2.
+constexpr int64_t kGemm6MinM = 3;
 static int64_t gemm6_min_m(const Options &o) { return o.gemm6_min_m > 0 ? o.gemm6_min_m : kGemm6MinM; }
 
 // Smallest M that takes the F16 GEMM (gemmh.h); option GEMMH_MIN_M. Its copy

@@ -1,0 +1,116 @@
+"""GPU parity of the small-M GEMMs (3 <= M <= 16, the batched decode step):
+gemm2s_q4k_kernel (Q4_K) and gemmks_kernel (Q2_K, Q3_K, Q5_K, Q6_K; Q4_K by
+option) against the oracle, every output, |gpu - ref| <= 1e-5 * sum|terms|
++ 1e-6. Shapes cover a single super-block per row (fewer super-blocks than
+waves per workgroup), super-block counts that the waves do not divide,
+row counts that leave a 32-row block part empty, every 4-row activation
+group count (M = 3 to 16), each waves-per-workgroup choice, and
+rows at the ends of each format's operand range."""
+import numpy as np
+import pytest
+
+import siphon_amd as sa
+from siphon_amd import synth
+
+from .test_gpu_gemm import _extreme_q2k, _extreme_q3k, _extreme_q5k, _extreme_q6k, _rows
+from .test_gpu_parity import assert_close
+
+pytestmark = pytest.mark.gpu
+
+KQ = [sa.Q2_K, sa.Q3_K, sa.Q4_K, sa.Q5_K, sa.Q6_K]
+
+
+def _weights(wt, n_out, n_in, rng):
+    W = synth.make_weights(wt, n_out, n_in, rng)
+    if wt == sa.Q2_K:
+        W = _extreme_q2k(W, n_out, n_in)
+    elif wt == sa.Q3_K:
+        W = _extreme_q3k(W, n_out, n_in)
+    elif wt == sa.Q5_K:
+        W = _extreme_q5k(W, n_out, n_in)
+    elif wt == sa.Q6_K:
+        W = _extreme_q6k(W, n_out, n_in)
+    return W
+
+
+def _check(dev, oracle, wt, n_out, n_in, M, seed, what):
+    rng = np.random.default_rng(seed)
+    W = _weights(wt, n_out, n_in, rng)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(wt, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
+
+
+@pytest.mark.parametrize("wt", KQ, ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 12, 16])
+@pytest.mark.parametrize("n_out,n_in", [(33, 256), (200, 1024), (96, 2304)])
+def test_small_m_vs_oracle(dev, oracle, wt, M, n_out, n_in):
+    _check(dev, oracle, wt, n_out, n_in, M, 7000 + 97 * wt + 13 * M + n_in,
+           f"{sa.NAMES[wt]} {n_out}x{n_in} M={M}")
+
+
+@pytest.mark.parametrize("wt", KQ, ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("waves", [2, 4, 8])
+def test_small_m_waves_per_workgroup(dev, oracle, option, wt, waves):
+    option("GEMMS_WAVES", waves)
+    _check(dev, oracle, wt, 160, 2560, 8, 7100 + wt + waves, f"{sa.NAMES[wt]} waves={waves}")
+
+
+@pytest.mark.parametrize("M", [5, 8, 16])
+def test_small_m_q4k_on_the_generic_kernel(dev, oracle, option, M):
+    """Q4_K at small M on gemmks.h (the GEMMKS_Q4K option) as well as on
+    gemm2s.h (the rule)."""
+    option("GEMMKS_Q4K", 1)
+    _check(dev, oracle, sa.Q4_K, 200, 1024, M, 7200 + M, f"Q4_K gemmks M={M}")
+
+
+def test_small_m_graph_replays_match_eager(dev):
+    """A captured small-M call (Q4_K on gemm2s.h, Q6_K and Q3_K on gemmks.h)
+    replays bit-identically to the eager call, several times with eager
+    calls in between."""
+    from .test_gpu_slices import _HipGraph, bits
+    rng = np.random.default_rng(7300)
+    n_out, n_in, M = 4096, 4096, 8
+    ws = [dev.upload(wt, n_out, n_in, synth.make_weights(wt, n_out, n_in, rng))
+          for wt in (sa.Q4_K, sa.Q6_K, sa.Q3_K)]
+    hg = _HipGraph()
+    bufs = []
+    try:
+        for w in ws:
+            w.prepare_gemm()
+        nan = np.full(M * n_out, np.nan, np.float32)
+        xd = dev.to_device(rng.standard_normal((M, n_in)).astype(np.float32))
+        ye = [dev.to_device(nan) for _ in ws]
+        yg = [dev.to_device(nan) for _ in ws]
+        bufs = [xd, *ye, *yg]
+        for w, y in zip(ws, ye):
+            dev.gemm_dev(w, xd.ptr, M, y.ptr, hg.stream.value)
+        dev.synchronize()
+        want = [y.to_host(np.float32, M * n_out).copy() for y in ye]
+        hg.begin()
+        for w, y in zip(ws, yg):
+            dev.gemm_dev(w, xd.ptr, M, y.ptr, hg.stream.value)
+        hg.end()
+        for _ in range(3):
+            for y in yg:
+                y.fill(nan)
+            hg.replay()
+            for y, e in zip(yg, want):
+                assert np.array_equal(bits(y.to_host(np.float32, M * n_out)), bits(e))
+            for w, y in zip(ws, ye):
+                y.fill(nan)
+                dev.gemm_dev(w, xd.ptr, M, y.ptr, hg.stream.value)
+            dev.synchronize()
+            for y, e in zip(ye, want):
+                assert np.array_equal(bits(y.to_host(np.float32, M * n_out)), bits(e))
+    finally:
+        hg.close()
+        for b in bufs:
+            b.free()
+        for w in ws:
+            w.free()
