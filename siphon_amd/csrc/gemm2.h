@@ -227,7 +227,13 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     constexpr int BM = 16 * MT;
     constexpr int kRec = g2_rec_bytes(BM);
     constexpr int kPieces = kRec / 1024;
-    __shared__ __attribute__((aligned(16))) uint8_t sx[2][kRec];
+    // two LDS objects, not one array indexed by the step's parity: each
+    // step reads one and copies the next record into the other, and only
+    // distinct objects let the compiler see that the step's LDS reads do
+    // not depend on the copy in flight (it otherwise waits for the copy
+    // before the first read, which exposes its whole latency)
+    __shared__ __attribute__((aligned(16))) uint8_t sx0[kRec];
+    __shared__ __attribute__((aligned(16))) uint8_t sx1[kRec];
     // XCD-aware order: workgroups go round-robin over the 8 XCDs, so the m
     // blocks and slices of one n block (which read the same weights) are
     // consecutive workgroups of one XCD and share its L2
@@ -254,15 +260,17 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     const int v_nib = lane * 16, v_scl = kG2Scl + r16 * 16, v_d = kG2D + r16 * 4;
     const int v_min = kG2Min + lane * 16;
 
-    // this wave's share of the 1 KiB pieces of a record
-    auto dma = [&](int c, int buf) {
+    // this wave's share of the 1 KiB pieces of a record; every wave issues
+    // the same number of copies (a wave past the last piece copies the last
+    // piece again: the same bytes to the same place), so the copies are
+    // straight-line code with a fixed count
+    auto dma = [&](int c, uint8_t *dst) {
 #pragma unroll
         for (int k = 0; k < (kPieces + 3) / 4; k++) {
-            const int i = wave + 4 * k;
-            if (i < kPieces)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    xr, (__attribute__((address_space(3))) void *)(&sx[buf][i * 1024]), 16, v_nib,
-                    c * kRec + i * 1024, 0, 0);
+            const int i = wave + 4 * k < kPieces ? wave + 4 * k : kPieces - 1;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, v_nib,
+                c * kRec + i * 1024, 0, 0);
         }
     };
     struct Raw {
@@ -300,10 +308,10 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
         for (int nt = 0; nt < 2; nt++) y[mt][nt] = (v4f2_t){0.0f, 0.0f, 0.0f, 0.0f};
 
     Raw raw;
-    dma(c0, 0);
+    dma(c0, sx0);
     load_w(c0, raw);
-    for (int c = c0; c < c1; c++) {
-        const int buf = (c - c0) & 1;
+    // one super-block: X holds its record, the next one is copied to Xn
+    auto step = [&](int c, const uint8_t *X, uint8_t *Xn) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         // decode this super-block's operands
@@ -329,9 +337,10 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
         // ahead; unconditional (the last super-block loads itself again), so
         // the registers of the prefetch are the ones decoded next
         const int cn = c + 1 < c1 ? c + 1 : c;
-        dma(cn, buf ^ 1);
+        dma(cn, Xn);
         load_w(cn, raw);
-        const uint8_t *X = sx[buf];
+        // keep the copies and loads here, ahead of the tiles' LDS reads
+        __builtin_amdgcn_sched_barrier(0);
         // quants of m tile mt + 1 are read while mt computes (ping-pong by
         // the parity of the unrolled tile index); group sums and scales at
         // the start of their own tile, in time for its epilogue
@@ -368,7 +377,13 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
                 y[mt][1][i] = fma_f32(dxv[i], u1, y[mt][1][i]);
             }
         }
+    };
+    int c = c0;
+    for (; c + 1 < c1; c += 2) {
+        step(c, sx0, sx1);
+        step(c + 1, sx1, sx0);
     }
+    if (c < c1) step(c, sx0, sx1);
     // result register i of lane l: row 4 (l / 16) + i of the m tile,
     // column l % 16 of the n tile; whole tiles inside M and n_out store
     // without per-element tests
