@@ -129,20 +129,31 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemm2s_q4k_kernel(G2SArgs A) {
                 y[nt][i] = fma_f32(dxv[i], u, y[nt][i]);
             }
     };
-    // super-blocks wave, wave + 4, ...: two register sets alternate, the
-    // loads of the next super-block issued before the current one computes
+    // super-blocks wave, wave + KW, ...: two register sets alternate, the
+    // loads of the next super-block issued before the current one computes.
+    // The loop runs over pairs that both exist, so its loads need no
+    // condition (the one past the end reads the last super-block again,
+    // which nothing computes): a load under a condition makes the compiler
+    // count it as possibly missing, and the compute that follows then waits
+    // for every load in flight, the prefetch too. The empty asm statement
+    // (a memory clobber) after the loads keeps the compiler from sinking
+    // them below the compute, and the scheduling barrier keeps the compute
+    // from moving above them.
+    const int last = A.nb - 1;
     Stage s0, s1;
     int c = wave;
-    if (c < A.nb) load(c, s0);
-    while (c < A.nb) {
-        if (c + KW < A.nb) load(c + KW, s1);
+    load(c < last ? c : last, s0);
+    for (; c + KW < A.nb; c += 2 * KW) {
+        load(c + KW, s1);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         compute(s0);
-        c += KW;
-        if (c >= A.nb) break;
-        if (c + KW < A.nb) load(c + KW, s0);
+        load(c + 2 * KW < last ? c + 2 * KW : last, s0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         compute(s1);
-        c += KW;
     }
+    if (c < A.nb) compute(s0);
     // partial tiles of waves 1..3 to LDS; wave 0 adds them in wave order
     if (wave > 0) {
 #pragma unroll

@@ -457,15 +457,41 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmks_kernel(GKSArgs A) {
     // SW and activation set j % 2 while the weights of the next SW - 1
     // super-blocks of this wave (from HBM) and the activations of the next
     // one (from the L2) are in flight; the ring indices are compile-time
-    // constants in the unrolled body
+    // constants in the unrolled body. Whole rounds (every super-block of
+    // the round exists) load without conditions (past the end a load reads
+    // the last super-block again, which nothing computes): a load under a
+    // condition makes the compiler count it as possibly missing, and every
+    // compute after it then waits for all loads in flight, the ring's later
+    // sets too. A memory clobber and a scheduling barrier keep the loads
+    // ahead of the compute (else the compiler sinks them below it, next to
+    // their use, or moves the compute above them). The last partial round
+    // loads and computes under conditions (for a wave with at most U
+    // super-blocks that is the whole loop).
+    // The whole rounds take a second copy of the compute, which spills at
+    // NH > 2 and for Q5_K; those run one loop whose loads are unconditional
+    // and whose compute is not.
     constexpr int U = SW % 2 ? 2 * SW : SW;
+    constexpr bool kRounds = NH <= 2 && FMT != T_Q5_K;
     WStage ws[SW];
     XStage xs[2];
+    const int last = A.nb - 1;
+    auto cl = [&](int c) { return c < last ? c : last; };
 #pragma unroll
-    for (int k = 0; k < SW - 1; k++)
-        if (wave + k * KW < A.nb) load_w(wave + k * KW, ws[k]);
-    if (wave < A.nb) load_x(wave, xs[0]);
-    for (int c0 = wave; c0 < A.nb; c0 += U * KW) {
+    for (int k = 0; k < SW - 1; k++) load_w(cl(wave + k * KW), ws[k]);
+    load_x(cl(wave), xs[0]);
+    if constexpr (kRounds) {
+        int c0 = wave;
+        for (; c0 + (U - 1) * KW < A.nb; c0 += U * KW) {
+#pragma unroll
+            for (int j = 0; j < U; j++) {
+                const int c = c0 + j * KW;
+                load_w(cl(c + (SW - 1) * KW), ws[(j + SW - 1) % SW]);
+                load_x(cl(c + KW), xs[(j + 1) % 2]);
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                compute(ws[j % SW], xs[j % 2]);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < U; j++) {
             const int c = c0 + j * KW;
@@ -474,6 +500,20 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmks_kernel(GKSArgs A) {
                 if (cw < A.nb) load_w(cw, ws[(j + SW - 1) % SW]);
                 if (cx < A.nb) load_x(cx, xs[(j + 1) % 2]);
                 compute(ws[j % SW], xs[j % 2]);
+            }
+        }
+    } else {
+        // one copy of the compute: loads without conditions, the compute
+        // under its own
+        for (int c0 = wave; c0 < A.nb; c0 += U * KW) {
+#pragma unroll
+            for (int j = 0; j < U; j++) {
+                const int c = c0 + j * KW;
+                load_w(cl(c + (SW - 1) * KW), ws[(j + SW - 1) % SW]);
+                load_x(cl(c + KW), xs[(j + 1) % 2]);
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                if (c < A.nb) compute(ws[j % SW], xs[j % 2]);
             }
         }
     }

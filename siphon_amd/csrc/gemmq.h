@@ -514,13 +514,23 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
 #pragma unroll
         for (int u = 0; u + 1 < kD; u++) load_w(c0 + u < c1 ? c0 + u : c1 - 1, o[u]);
         store_x(o[0], sx0);
-        for (int c = c0; c < c1; c += kD) {
+        // whole rounds of kD steps without conditions, then the last
+        // partial round: a condition inside the round splits it into blocks,
+        // and the compiler's wait counts at the joins assume the loads of a
+        // skipped step were never issued, so every step waited for the
+        // ring's later slots too (the ring then bought no depth)
+        int c = c0;
+        for (; c + kD <= c1; c += kD) {
 #pragma unroll
             for (int u = 0; u < kD; u++)
-                if (c + u < c1)
-                    step(c + u, o[u], o[(u + kD - 1) % kD], o[(u + 1) % kD],
-                         (u & 1) ? sx1 : sx0, (u & 1) ? sx0 : sx1);
+                step(c + u, o[u], o[(u + kD - 1) % kD], o[(u + 1) % kD], (u & 1) ? sx1 : sx0,
+                     (u & 1) ? sx0 : sx1);
         }
+#pragma unroll
+        for (int u = 0; u < kD; u++)
+            if (c + u < c1)
+                step(c + u, o[u], o[(u + kD - 1) % kD], o[(u + 1) % kD], (u & 1) ? sx1 : sx0,
+                     (u & 1) ? sx0 : sx1);
     } else {
         // the first weights go out first (before the wait on the producers)
 #pragma unroll

@@ -904,7 +904,7 @@ static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
     return SIHIP_OK;
 }
 
-static int64_t gemmks_max_m(const Options &o);
+static int64_t gemmks_max_m(const Options &o, uint32_t type);
 
 // The near-GGUF-size K-quant copy of the small-M GEMM (gemmks.h).
 static int build_gemmks_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
@@ -952,7 +952,7 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
         const int rc = build_gemm2_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
-    if (is_kquant(w->L.type) && gemmks_max_m(ctx->opt) > 0 && !w->gsmall &&
+    if (is_kquant(w->L.type) && gemmks_max_m(ctx->opt, w->L.type) > 0 && !w->gsmall &&
         !(w->L.type == T_Q4_K && ctx->opt.gemmks_q4k != 1)) {
         const int rc = build_gemmks_copy(ctx, w, ctx->stream);
         if (rc) return rc;
@@ -973,13 +973,22 @@ static int64_t gemm2s_max_m(const Options &o) {
     return o.gemm2s_max_m >= 0 ? (o.gemm2s_max_m < 16 ? o.gemm2s_max_m : 16) : 16;
 }
 // Largest M that takes the small-M K-quant GEMM (gemmks.h; at most 16);
-// option GEMMKS_MAX_M, 0 turns it off.
-static int64_t gemmks_max_m(const Options &o) {
-    return o.gemmks_max_m >= 0 ? (o.gemmks_max_m < 16 ? o.gemmks_max_m : 16) : 16;
+// option GEMMKS_MAX_M (all K-quants), 0 turns it off. The rule is by
+// format: past 8 rows the kernel takes 3 or 4 activation groups per MFMA
+// and its registers spill, so the matrix-core GEMMs above take over.
+// Config-4 shapes (27648 x 5120, 5120 x 27648, 5120 x 5120), us per call:
+//   M = 12: Q2_K 33.8 / 65.5 / 20.4 here, 24.2 / 28.3 / 14.5 there;
+//           Q5_K 111 / 155 / 32.4 here, 33.7 / 36.1 / 16.2 there;
+//           Q3_K 25.2 / 32.0 / 12.6 here, 30.7 / 34.6 / 15.9 there;
+//           Q6_K 37.2 / 43.3 / 14.1 here, 52.0 / 58.8 / 15.7 there;
+//   M = 16: Q3_K 106 / 110 / 28.1 here, Q6_K 160 / 191 / 43.7 here.
+static int64_t gemmks_max_m(const Options &o, uint32_t type) {
+    if (o.gemmks_max_m >= 0) return o.gemmks_max_m < 16 ? o.gemmks_max_m : 16;
+    return type == T_Q3_K || type == T_Q6_K ? 12 : 8;
 }
 
 // Smallest M that takes a Q6_K GEMM (the small-M kernel of gemmks.h up to
-// M = 16, gemm6.h above); option GEMM6_MIN_M. As for the other K-quants
+// M = 12, gemm6.h above); option GEMM6_MIN_M. As for the other K-quants
 // (gemm_min_m) 3: the small-M kernel streams the GGUF bytes once, so it
 // wins from M = 3 (ffn_down 4096 x 14336: 18.8 against 27.6 us on the
 // matvec kernel), which stays faster at M = 2.
@@ -1093,7 +1102,7 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
     // (Q4_K: gemm2s.h below, unless the GEMMKS_Q4K option is 1; on the
     // Llama-3-8B shapes at M = 8 it took 10.0 / 7.9 / 15.8 us per call for
     // 4096 / 1024 / 14336 x 4096 against 10.9 / 9.9 / 16.0 here)
-    if (is_kquant(L.type) && M <= gemmks_max_m(ctx->opt) &&
+    if (is_kquant(L.type) && M <= gemmks_max_m(ctx->opt, L.type) &&
         !(L.type == T_Q4_K && ctx->opt.gemmks_q4k != 1)) {
         // one 16-row record block, a workgroup per 32 weight rows whose
         // waves split the super-blocks, the near-GGUF-size copy (gemmks.h)

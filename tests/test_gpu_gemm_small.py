@@ -1,7 +1,8 @@
-"""GPU parity of the small-M GEMMs (3 <= M <= 16, the batched decode step):
-gemm2s_q4k_kernel (Q4_K) and gemmks_kernel (Q2_K, Q3_K, Q5_K, Q6_K; Q4_K by
-option) against the oracle, every output, |gpu - ref| <= 1e-5 * sum|terms|
-+ 1e-6. Shapes cover a single super-block per row (fewer super-blocks than
+"""GPU parity of the small-M GEMMs (the batched decode step): gemm2s_q4k_kernel
+(Q4_K, 3 <= M <= 16) and gemmks_kernel (Q2_K, Q5_K up to M = 8, Q3_K, Q6_K up
+to M = 12, by option every K-quant up to 16) against the oracle, every
+output, |gpu - ref| <= 1e-5 * sum|terms| + 1e-6; the M values past a
+format's rule run its larger GEMM. Shapes cover a single super-block per row (fewer super-blocks than
 waves per workgroup), super-block counts that the waves do not divide,
 row counts that leave a 32-row block part empty, every 4-row activation
 group count (M = 3 to 16), each waves-per-workgroup choice, and
@@ -61,7 +62,18 @@ def test_small_m_waves_per_workgroup(dev, oracle, option, wt, waves):
     _check(dev, oracle, wt, 160, 2560, 8, 7100 + wt + waves, f"{sa.NAMES[wt]} waves={waves}")
 
 
-@pytest.mark.parametrize("M", [5, 8, 16])
+@pytest.mark.parametrize("wt", KQ, ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("M", [9, 12, 13, 16])
+def test_small_m_wide_groups_by_option(dev, oracle, option, wt, M):
+    """Three and four activation groups per MFMA (M = 9 to 16), which the
+    rule gives to the larger GEMMs for some formats: GEMMKS_MAX_M = 16 keeps
+    every K-quant on gemmks.h (Q4_K with GEMMKS_Q4K)."""
+    option("GEMMKS_MAX_M", 16)
+    option("GEMMKS_Q4K", 1)
+    _check(dev, oracle, wt, 200, 1024, M, 7400 + 31 * wt + M, f"{sa.NAMES[wt]} gemmks M={M}")
+
+
+@pytest.mark.parametrize("M", [5, 8])
 def test_small_m_q4k_on_the_generic_kernel(dev, oracle, option, M):
     """Q4_K at small M on gemmks.h (the GEMMKS_Q4K option) as well as on
     gemm2s.h (the rule)."""
