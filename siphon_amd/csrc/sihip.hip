@@ -1415,13 +1415,19 @@ static void launch_gemmks(int nh, int kw, dim3 grid, hipStream_t st, const GKSAr
 // round). M = 8, per call: Q2_K 27648 x 5120 (864 blocks) 23.6 us in 2
 // waves, 25.4 in 4, 32.2 in 8; 5120 x 27648 (160 blocks) 28.5 in 8, 32.7
 // in 4, 56.9 in 2; Q4_K 14336 x 4096 (448 blocks) 15.9 in 4 against 17.4
-// in 8. The Q4_K kernel of gemm2s.h has 4 and 8. The GEMMS_WAVES option (2,
-// 4 or 8) overrides.
+// in 8. Except for Q2_K (the smallest blocks), eight waves also need at
+// least 8 super-blocks each: rows of 4096 and 5120 (16 and 20 per row) run
+// faster in 4 (M = 8, per call: Llama-3-8B q/k/v 24.6 to 22.6 us, wo 10.1
+// to 9.6; Q3_K 5120 x 5120 12.4 to 11.7, Q5_K 14.1 to 13.2; ffn_down, 56
+// per row, 20.5 to 20.2), while Q2_K 5120 x 5120 is faster in 8 (11.8
+// against 12.9). The Q4_K kernel of gemm2s.h has 4 and 8. The GEMMS_WAVES
+// option (2, 4 or 8) overrides.
 static int small_gemm_waves(const sihip_ctx *ctx, const Layout &L) {
     if (ctx->opt.gemms_waves == 2 || ctx->opt.gemms_waves == 4 || ctx->opt.gemms_waves == 8)
         return (int)ctx->opt.gemms_waves;
     const int64_t blocks = (L.n_out + 31) / 32, room = 10 * (int64_t)ctx->n_cu;
-    return blocks * 8 <= room ? 8 : blocks * 4 <= room ? 4 : 2;
+    if (blocks * 8 <= room && (L.type == T_Q2_K || L.n_in / 256 >= 64)) return 8;
+    return blocks * 4 <= room ? 4 : 2;
 }
 
 static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPlan &p,
