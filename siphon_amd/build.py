@@ -1,10 +1,13 @@
 """Build the native parts in-tree:
 
   siphon_amd/lib/libsiphon_hip.so      C-ABI HIP library (gfx950 kernels)
-  siphon_amd/lib/libsiphon_backend.so  C17 host adapter (si_backend "hip")
+  siphon_amd/lib/backend_hip.o,        C17 host side (the si_backend "hip"
+    si_prefill.o                       adapter, the batched prefill): build check
   oracle/libsiq_oracle.so              CPU oracle (test infrastructure)
   oracle/_ref/libsiphon_ref.so         compiled reference checker (only
                                        where /root/reference exists)
+  oracle/_ref/libsiphon_engine_ref.so  the reference engine with this
+                                       repository's prefill (same condition)
 """
 from __future__ import annotations
 
@@ -57,17 +60,22 @@ def build_hip(verbose: bool = False) -> str:
 
 
 def build_backend(verbose: bool = False) -> str:
-    """Compile the C17 "hip" si_backend adapter (siphon_amd/host) as the
-    reference host would: C17, -Werror, no HIP headers. Inside Siphon it is
-    one more source file of the engine; here it is compiled against the
-    mirror of Siphon's declarations (SI_HIP_STANDALONE) to check it builds.
-    tests/host links it into a test harness."""
+    """Compile the C17 host side (siphon_amd/host: the "hip" si_backend
+    adapter and the batched prefill) as the reference host would: C17,
+    -Werror, no HIP headers, no contraction of a*b+c. Inside Siphon they are
+    more source files of the engine; here they are compiled against the
+    mirror of Siphon's declarations (SI_HIP_STANDALONE) to check they build.
+    tests/host and oracle/Makefile (target `engine`) link them into test
+    harnesses."""
     os.makedirs(LIB_DIR, exist_ok=True)
-    src = os.path.join(PKG, "host", "backend_hip.c")
-    out = os.path.join(LIB_DIR, "backend_hip.o")
-    _run(["gcc", "-std=c17", "-O2", "-fPIC", "-c", "-Wall", "-Wextra", "-Werror",
-          "-D_POSIX_C_SOURCE=200809L", "-DSI_HIP_STANDALONE", "-I", os.path.join(ROOT, "include"),
-          "-I", os.path.join(PKG, "host"), "-o", out, src], verbose)
+    out = None
+    for name in ("backend_hip", "si_prefill"):
+        src = os.path.join(PKG, "host", name + ".c")
+        out = os.path.join(LIB_DIR, name + ".o")
+        _run(["gcc", "-std=c17", "-O2", "-fPIC", "-c", "-Wall", "-Wextra", "-Werror",
+              "-ffp-contract=off", "-D_POSIX_C_SOURCE=200809L", "-DSI_HIP_STANDALONE",
+              "-I", os.path.join(ROOT, "include"), "-I", os.path.join(PKG, "host"), "-o", out, src],
+             verbose)
     return out
 
 
@@ -75,7 +83,7 @@ def build_oracle(verbose: bool = False) -> None:
     odir = os.path.join(ROOT, "oracle")
     _run(["make", "-s", "-C", odir, "libsiq_oracle.so"], verbose)
     if os.path.isdir("/root/reference/src"):
-        _run(["make", "-s", "-C", odir, "ref"], verbose)
+        _run(["make", "-s", "-C", odir, "ref", "engine"], verbose)
 
 
 def build_test_checkers(verbose: bool = False) -> None:

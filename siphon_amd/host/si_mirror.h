@@ -9,11 +9,15 @@
  *   si_tp (opaque lane pool)        reference include/siphon/threadpool.h:19
  *   si_backend_cpu                  reference include/siphon/tensor.h:58
  *   si_kern_impl, si_kern_impl_get  reference include/siphon/kernels.h:28-35
- * plus the one line a Siphon tree adds to support this backend:
+ * plus the two lines a Siphon tree adds to support this backend:
  *   SI_LOC_DEVICE = 2               the device location the reference leaves
  *                                   for a later backend (tensor.h:25-29);
  *                                   si_backend_hip_place tags the tensors it
  *                                   made resident with it.
+ *   si_backend.gemm                 a trailing vtable slot (after row_to_f32,
+ *                                   tensor.h:54) for M activation rows in one
+ *                                   call: the batched prefill's matmuls. The
+ *                                   CPU backend fills it with M gemv calls.
  * The backend itself stays tagged SI_LOC_HOST: gemv takes and returns host
  * arrays. */
 #ifndef SI_MIRROR_H
@@ -57,6 +61,13 @@ struct si_backend {
     void (*gemv)(si_backend *be, const si_tensor *w, const float *x, float *y, int64_t n_out,
                  si_tp *tp);
     void (*row_to_f32)(si_backend *be, const si_tensor *w, uint64_t row, float *out);
+    /* Y[m, i] = <w.row(i), X[m, :]> for m < M, i < ne[1]: X is [M x ne[0]]
+     * and Y [M x ne[1]], row-major host arrays, each X row converted to the
+     * pair format on its own (the same per-row result as gemv, up to the
+     * f32 summation order). SI_OK, or a negative SI_* code with si_set_err
+     * called and Y untouched. */
+    int (*gemm)(si_backend *be, const si_tensor *w, const float *X, int64_t M, float *Y,
+                si_tp *tp);
 };
 
 const char *si_errstr(void);

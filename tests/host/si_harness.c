@@ -1,8 +1,9 @@
 /* Test harness for the "hip" si_backend adapter (siphon_amd/host).
  * TEST INFRASTRUCTURE ONLY. It supplies what a Siphon build would: the
- * error-string functions and a CPU backend whose row_to_f32 dequantizes
- * with this repository's CPU oracle (oracle/siq_oracle.c), and exposes the
- * vtable through plain functions for ctypes. */
+ * error-string functions and a CPU backend whose gemv, gemm (one gemv per
+ * row, as the reference CPU backend fills the slot) and row_to_f32 use this
+ * repository's CPU oracle (oracle/siq_oracle.c), and exposes the vtable
+ * through plain functions for ctypes. */
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -33,7 +34,28 @@ static void cpu_row_to_f32(si_backend *be, const si_tensor *w, uint64_t row, flo
     siq_dequant_row(w->type, (const char *)w->data + row * row_bytes, out, (int64_t)w->ne[0]);
 }
 
-static si_backend g_cpu = {"cpu", SI_LOC_HOST, NULL, cpu_row_to_f32};
+/* gemv with the oracle's exact dots (f32 results); y untouched on error */
+static void cpu_gemv(si_backend *be, const si_tensor *w, const float *x, float *y, int64_t n_out,
+                     si_tp *tp) {
+    (void)be;
+    (void)tp;
+    if (!siq_gemv(w->type, w->data, n_out, (int64_t)w->ne[0], x, y, NULL, 1))
+        si_set_err("cpu gemv: unsupported type %u", (unsigned)w->type);
+}
+
+/* the gemm slot as the CPU backend fills it: one gemv per activation row */
+static int cpu_gemm(si_backend *be, const si_tensor *w, const float *X, int64_t M, float *Y,
+                    si_tp *tp) {
+    const int64_t n_in = (int64_t)w->ne[0], n_out = w->ne[1] ? (int64_t)w->ne[1] : 1;
+    g_err[0] = 0;
+    for (int64_t m = 0; m < M; m++) {
+        be->gemv(be, w, X + m * n_in, Y + m * n_out, n_out, tp);
+        if (g_err[0]) return SI_EINVAL;
+    }
+    return SI_OK;
+}
+
+static si_backend g_cpu = {"cpu", SI_LOC_HOST, cpu_gemv, cpu_row_to_f32, cpu_gemm};
 
 si_backend *si_backend_cpu(void) { return &g_cpu; }
 
@@ -77,6 +99,16 @@ int th_gemv(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, const 
     const si_tensor t = make_tensor(be, type, n_out, n_in, data, bytes);
     be->gemv(be, &t, x, y, n, NULL);
     return g_err[0] ? -1 : 0;
+}
+
+si_backend *th_cpu(void) { return &g_cpu; }
+
+/* the vtable's gemm slot of be (the hip backend or th_cpu()) */
+int th_vtable_gemm(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, const void *data,
+                   uint64_t bytes, const float *X, int64_t M, float *Y) {
+    g_err[0] = 0;
+    const si_tensor t = make_tensor(be, type, n_out, n_in, data, bytes);
+    return be->gemm(be, &t, X, M, Y, NULL);
 }
 
 int th_gemm(si_backend *be, uint32_t type, uint64_t n_out, uint64_t n_in, const void *data,

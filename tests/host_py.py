@@ -32,6 +32,8 @@ class Harness:
         L.th_name.restype = ctypes.c_char_p
         L.th_gemv.argtypes = [vp, u32, u64, u64, vp, u64, vp, vp, i64]
         L.th_gemm.argtypes = [vp, u32, u64, u64, vp, u64, vp, i64, vp]
+        L.th_cpu.restype = vp
+        L.th_vtable_gemm.argtypes = [vp, u32, u64, u64, vp, u64, vp, i64, vp]
         L.th_row_to_f32.argtypes = [vp, u32, u64, u64, vp, u64, u64, vp]
         L.th_weights.argtypes = [vp, ctypes.POINTER(u64)]
         L.th_upload.argtypes = [vp, u32, u64, u64, vp, u64]
@@ -63,6 +65,15 @@ class Harness:
     def gemm(self, be, wt, n_out, n_in, W, X, Y):
         return self.L.th_gemm(be, wt, n_out, n_in, W.ctypes.data, W.nbytes, X.ctypes.data,
                               X.shape[0], Y.ctypes.data)
+
+    def cpu(self):
+        """The harness's CPU backend (oracle dots, gemm slot = one gemv per row)."""
+        return self.L.th_cpu()
+
+    def vtable_gemm(self, be, wt, n_out, n_in, W, X, Y):
+        """be->gemm through the vtable slot."""
+        return self.L.th_vtable_gemm(be, wt, n_out, n_in, W.ctypes.data, W.nbytes, X.ctypes.data,
+                                     X.shape[0], Y.ctypes.data)
 
     def row_to_f32(self, be, wt, n_out, n_in, W, row, out):
         return self.L.th_row_to_f32(be, wt, n_out, n_in, W.ctypes.data, W.nbytes, row,

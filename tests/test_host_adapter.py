@@ -40,6 +40,53 @@ def test_open_reports_no_device_or_opens(harness):
         assert "device" in harness.errstr()
 
 
+def test_cpu_vtable_gemm_slot(harness, oracle):
+    """The gemm slot as the CPU backend fills it (one gemv per activation
+    row; the line INTEGRATION.md adds to the reference backend.c) gives the
+    rows of M separate gemv calls, for every weight type."""
+    be = harness.cpu()
+    rng = np.random.default_rng(41)
+    for wt, n_out, n_in in ((sa.Q4_K, 40, 512), (sa.Q6_K, 17, 256), (sa.Q8_0, 9, 96),
+                            (sa.F16, 8, 64), (sa.Q2_K, 5, 256)):
+        W = synth.make_weights(wt, n_out, n_in, rng)
+        X = rng.standard_normal((3, n_in)).astype(np.float32)
+        Y = np.full((3, n_out), np.nan, np.float32)
+        assert harness.vtable_gemm(be, wt, n_out, n_in, W, X, Y) == 0, harness.errstr()
+        R, _ = oracle.gemm(wt, W, n_out, n_in, X)
+        assert np.array_equal(Y, R.astype(np.float32)), sa.NAMES[wt]
+
+
+@pytest.mark.gpu
+def test_vtable_gemm_slot_both_backends(harness, oracle):
+    """be->gemm through the vtable on the hip backend and on the CPU backend
+    (one gemv per row), each against the oracle's M per-row gemvs, for
+    every weight type; the hip slot fills Y and leaves it untouched on a
+    bad call."""
+    rc, be = harness.open(HIP_SO)
+    assert rc == 0, harness.errstr()
+    keep = []
+    try:
+        rng = np.random.default_rng(43)
+        for wt, n_out, n_in in ((sa.Q4_K, 300, 2048), (sa.Q6_K, 129, 1024), (sa.Q8_0, 77, 896),
+                                (sa.Q4_0, 64, 512), (sa.Q5_0, 65, 512), (sa.Q2_K, 96, 512),
+                                (sa.Q3_K, 96, 512), (sa.Q5_K, 96, 512), (sa.F16, 64, 512)):
+            W = synth.make_weights(wt, n_out, n_in, rng)
+            keep.append(W)
+            X = rng.standard_normal((5, n_in)).astype(np.float32)
+            R, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+            for b in (be, harness.cpu()):
+                Y = np.full((5, n_out), np.nan, np.float32)
+                assert harness.vtable_gemm(b, wt, n_out, n_in, W, X, Y) == 0, harness.errstr()
+                assert np.all(np.abs(Y.astype(np.float64) - R) <= 1e-5 * L1 + 1e-6), \
+                    (sa.NAMES[wt], b == be)
+        Y = np.full((0, 300), np.nan, np.float32)
+        assert harness.vtable_gemm(be, sa.Q4_K, 300, 2048, keep[0], np.zeros((0, 2048), np.float32),
+                                   Y) == SI_EINVAL
+        assert "bad arguments" in harness.errstr()
+    finally:
+        harness.close(be)
+
+
 @pytest.mark.gpu
 def test_vtable_gemv_gemm_row_to_f32(harness, oracle):
     rc, be = harness.open(HIP_SO)
@@ -105,8 +152,9 @@ def test_vtable_error_contract(harness):
 def test_reused_address_is_not_served_stale(harness, oracle):
     """A host buffer that is freed and reused for a different tensor (a
     different type or shape at the same address, or the same type and
-    shape with other contents, told apart by a fingerprint of the first
-    and last 64 bytes) gets a fresh upload."""
+    shape with other contents, told apart by a fingerprint of 16 spans of
+    the tensor: its edges and 14 evenly spaced inside) gets a fresh upload,
+    also when only the inside changed."""
     rc, be = harness.open(HIP_SO)
     assert rc == 0, harness.errstr()
     try:
@@ -133,6 +181,15 @@ def test_reused_address_is_not_served_stale(harness, oracle):
         assert harness.gemv(be, sa.F16, 64, 512, buf[:W3.nbytes], x2, y3, 64) == 0
         ref3, l3 = oracle.gemv(sa.F16, W3, 64, 512, x2)
         assert np.all(np.abs(y3.astype(np.float64) - ref3) <= 1e-5 * l3 + 1e-6)
+        assert harness.weights(be)[0] == 1
+        # same edges, new rows 16..47 (16 KiB in the middle of 64 KiB)
+        W4 = W3.copy()
+        W4[16:48] = synth.make_weights(sa.F16, 32, 512, rng)
+        buf[:W4.nbytes] = W4.reshape(-1)
+        y4 = np.zeros(64, np.float32)
+        assert harness.gemv(be, sa.F16, 64, 512, buf[:W4.nbytes], x2, y4, 64) == 0
+        ref4, l4 = oracle.gemv(sa.F16, W4, 64, 512, x2)
+        assert np.all(np.abs(y4.astype(np.float64) - ref4) <= 1e-5 * l4 + 1e-6)
         assert harness.weights(be)[0] == 1
     finally:
         harness.close(be)
