@@ -21,11 +21,13 @@ the layers' gemm slot on the matrix cores) and check:
 - every gemm call the prefill made, on its recorded inputs, against the
   oracle's per-row dots within the path's bar |gpu - ref| <= 1e-5 *
   sum|terms| + 1e-6 (every output);
-- end to end, against the CPU token loop: the KV caches agree to within
-  4 f16 ulps (the GEMMs round their f32 sums in another order, which moves
-  an f16 rounding by an ulp where a value sits near a rounding boundary,
-  and attention passes such moves on to the next layer), and the last
-  logits to within 1e-3 of the largest logit.
+- end to end, against the CPU token loop: every cached K and V value within
+  4 f16 spacings of its head vector's largest magnitude, at most 1 % of
+  them moved at all (the GEMMs round their f32 sums in another order, which
+  moves an f16 rounding where a value sits near a rounding boundary, and
+  attention passes such moves on to the next layer; a value near zero after
+  cancellation can move by many of its own, much finer, spacings), and the
+  last logits within 1e-4 of the largest logit.
 """
 import numpy as np
 import pytest
@@ -217,12 +219,13 @@ def test_prefill_errors(lib, model):
         lib.L.re_engine_free(e)
 
 
-def _f16_ulps(a, b):
-    """|a - b| in units of the f16 spacing at a (f16 bit patterns in)."""
+def _vector_ulps(a, b, axis):
+    """|a - b| in units of the f16 spacing at the largest magnitude of each
+    head vector (f16 bit patterns in; `axis` runs over the vector)."""
     fa = a.view(np.float16).astype(np.float64)
     fb = b.view(np.float16).astype(np.float64)
-    spacing = np.spacing(np.abs(a.view(np.float16))).astype(np.float64)
-    return np.abs(fa - fb) / spacing
+    top = np.max(np.abs(fa), axis=axis, keepdims=True).astype(np.float16)
+    return np.abs(fa - fb) / np.spacing(top).astype(np.float64)
 
 
 @pytest.mark.gpu
@@ -255,12 +258,13 @@ def test_prefill_hip_matches_token_loop(lib, oracle, model, n):
             assert np.all(err <= 1e-5 * L1 + 1e-6), (arch, sa.NAMES[wt], M, float(np.max(err / L1)))
         k0, v0 = lib.caches(e_ref, n)
         k1, v1 = lib.caches(e_pre, n)
-        ku, vu = _f16_ulps(k0, k1), _f16_ulps(v0, v1)
-        print(f"{arch} n={n}: K max {ku.max():.0f} ulp ({np.mean(ku > 0):.2e} moved), "
-              f"V max {vu.max():.0f} ulp ({np.mean(vu > 0):.2e} moved), "
-              f"logits max |d| {np.max(np.abs(got - want)):.3e} of {np.max(np.abs(want)):.3e}")
-        assert ku.max() <= 4 and vu.max() <= 4
-        assert np.max(np.abs(got - want)) <= 1e-3 * np.max(np.abs(want))
+        ku, vu = _vector_ulps(k0, k1, 3), _vector_ulps(v0, v1, 2)
+        moved = np.mean(np.concatenate([(k0 != k1).ravel(), (v0 != v1).ravel()]))
+        print(f"{arch} n={n}: K max {ku.max():.2f}, V max {vu.max():.2f} ulps of the head "
+              f"vector's largest value; {moved:.2e} of the cache moved; logits max |d| "
+              f"{np.max(np.abs(got - want)):.3e} of {np.max(np.abs(want)):.3e}")
+        assert ku.max() <= 4 and vu.max() <= 4 and moved <= 0.01
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
     finally:
         lib.L.re_layers_cpu(m)
         lib.L.re_rec_clear()
