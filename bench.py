@@ -225,6 +225,9 @@ def main():
         nbytes = sum(w.gguf_bytes + 4 * w.n_out for w in ws) + 4 * ws[0].n_in
         per[label] = (nbytes, us)
         del g
+    probe = probe_floors(dev, torch, stream,
+                         {label: sum(layers[0][n].gguf_bytes for n in names)
+                          for label, names in groups})
     dom = "gate_up" if "gate_up" in per else "ffn_gate"
     nbytes, us = per[dom]
     achieved = nbytes / (us * 1e-6) / 1e9
@@ -239,6 +242,11 @@ def main():
                                      if dom == "gate_up" else None),
         "per_launch_us": {k: round(v[1], 2) for k, v in per.items()},
         "per_launch_GBs": {k: round(v[0] / (v[1] * 1e-6) / 1e9, 1) for k, v in per.items()},
+        # the read-only probe over the same weight bytes, launched the same
+        # way (32 launches of the kind back to back in one graph): the floor
+        # of a launch of that size, and each kind's time over it
+        "per_launch_probe_us": {k: round(v, 2) for k, v in probe.items()},
+        "per_launch_over_probe": {k: round(per[k][1] / probe[k], 3) for k in per},
     }
 
     result = {
@@ -624,6 +632,42 @@ def bench_configs(dev, torch, stream, rng, rotate_bytes=512 << 20):
     return out
 
 
+def probe_floors(dev, torch, stream, sizes, reps=10):
+    """For each launch kind (label: bytes per launch), the library's
+    read-only probe (sihip_probe_read_dev: nontemporal 16-byte loads, four
+    in flight per thread) over that many bytes, 32 launches over consecutive
+    slices of one buffer (past the 256 MB MALL) in one HIP graph, timed with
+    HIP events on the launch stream: average microseconds per launch."""
+    sp = stream.cuda_stream
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    span = max(sizes.values())
+    buf = torch.ones((N_LAYERS * span + 4095) // 4, dtype=torch.int32, device="cuda")
+    out = {}
+    for label, nb in sizes.items():
+        def run():
+            for il in range(N_LAYERS):
+                dev.probe_read_dev(buf.data_ptr() + il * span, nb, sink.data_ptr(), sp)
+        with torch.cuda.stream(stream):
+            run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            run()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            with torch.cuda.stream(stream):
+                g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out[label] = e0.elapsed_time(e1) * 1e3 / (reps * N_LAYERS)
+        del g
+    del buf
+    return out
+
+
 def profile_calibration(dev, torch, stream, reps=10):
     """HBM ceilings the decode pass is measured against, with the library's
     read-only probe kernel (sihip_probe_read_dev):
@@ -685,7 +729,8 @@ def profile_calibration(dev, torch, stream, reps=10):
     pass_ms = e0.elapsed_time(e1) / reps
     pass_gbs = N_LAYERS * layer_bytes / (pass_ms * 1e-3) / 1e9
     del g, buf
-    return {"stream_read": {"bytes": big, "ms": round(t * 1e3, 3), "GB/s": round(stream_gbs, 1),
+    floors = probe_floors(dev, torch, stream, dict(zip([g[0] for g in groups], sizes)), reps)
+    return {"probe_us_per_launch_kind": {k: round(v, 2) for k, v in floors.items()},"stream_read": {"bytes": big, "ms": round(t * 1e3, 3), "GB/s": round(stream_gbs, 1),
                             "hbm_frac": round(stream_gbs / HBM_PEAK_GBS, 4)},
             "pass_read_only": {"launches": N_LAYERS * len(sizes), "bytes": N_LAYERS * layer_bytes,
                                "launch_bytes": dict(zip([g[0] for g in groups], sizes)),

@@ -4,6 +4,18 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// The cross-workgroup hand-off of K-slice and column-slice partial sums
+// (slices_finish here, split_reduce in matvec.h) relies on what gfx950 does,
+// not on the HIP memory model: sc1 stores and loads bypass the per-XCD L2,
+// s_waitcnt vmcnt(0) waits for a wave's stores to complete before its
+// workgroup counts its arrival with a relaxed agent-scope atomic, and the
+// last workgroup's sc1 loads are issued after that count returns. Another
+// target needs that ordering shown again (or release/acquire arrivals)
+// before these kernels are built for it.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "agent.h: the K-slice partial-sum hand-off is validated on gfx950 only (sc1 stores/loads, vmcnt(0) before a relaxed agent-scope arrival count)"
+#endif
+
 namespace sihip {
 
 // A load at agent scope (sc1: coherent across the XCDs' L2 caches, like an

@@ -52,10 +52,8 @@ __host__ __device__ constexpr int gq_rec_dx(int BM) { return 128 * BM; }
 __host__ __device__ constexpr int gq_rec_bs(int BM) { return 144 * BM; }
 
 // Q8_0 block i (row m = i / (n_in / 32), block kb) of X into its record;
-// rows M..Mp-1 are zero. COHERENT: agent-scope stores, which the workgroups
-// of the same launch read back (the fused GEMM below); otherwise plain
-// stores for the GEMM launched after this one.
-template <int BM, int BIAS, bool COHERENT>
+// rows M..Mp-1 are zero.
+template <int BM, int BIAS>
 __device__ inline void gq_quantize_one(const float *x, int64_t ldx, int64_t M, int64_t n_in,
                                        uint8_t *rec, int64_t i, int scalar) {
     const int64_t nbl = n_in / 32;
@@ -75,24 +73,12 @@ __device__ inline void gq_quantize_one(const float *x, int64_t ldx, int64_t M, i
     uint8_t *R = rec + (mb * (n_in / 128) + c) * gq_rec_bytes(BM);
     // lane group g of the fragment takes elements 8 g .. 8 g + 7 (words 2g, 2g+1)
     uint8_t *frag = R + (4 * (mr >> 4) + j) * 512;
-    float *dx = reinterpret_cast<float *>(R + gq_rec_dx(BM)) + j * BM + mr;
-    int *bs = reinterpret_cast<int *>(R + gq_rec_bs(BM)) + j * BM + mr;
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-        uint64_t *dst = reinterpret_cast<uint64_t *>(frag + (16 * g + (mr & 15)) * 8);
-        const uint64_t v = (uint64_t)q.q[2 * g] | ((uint64_t)q.q[2 * g + 1] << 32);
-        if constexpr (COHERENT)
-            __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            *dst = v;
-    }
-    if constexpr (COHERENT) {
-        __hip_atomic_store(dx, q.d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(bs, -BIAS * q.sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-        *dx = q.d;
-        *bs = -BIAS * q.sum;
-    }
+    for (int g = 0; g < 4; g++)
+        *reinterpret_cast<uint64_t *>(frag + (16 * g + (mr & 15)) * 8) =
+            (uint64_t)q.q[2 * g] | ((uint64_t)q.q[2 * g + 1] << 32);
+    reinterpret_cast<float *>(R + gq_rec_dx(BM))[j * BM + mr] = q.d;
+    reinterpret_cast<int *>(R + gq_rec_bs(BM))[j * BM + mr] = -BIAS * q.sum;
 }
 
 // One thread per Q8_0 block (row m, block kb); rows M..Mp-1 are zero.
@@ -102,7 +88,7 @@ __global__ __launch_bounds__(256) void gemmq_quantize_x(const float *x, int64_t 
                                                         int scalar) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= Mp * (n_in / 32)) return;
-    gq_quantize_one<BM, BIAS, false>(x, ldx, M, n_in, rec, i, scalar);
+    gq_quantize_one<BM, BIAS>(x, ldx, M, n_in, rec, i, scalar);
 }
 
 // ---- weight copy in the order of this kernel ----------------------------------
@@ -252,30 +238,15 @@ struct GQArgs {
     int S, SBK;           // K slices over steps
     float *part;
     uint32_t *cnt;
-    // fused activation quantization (gemmq_kernel<.., true>): the first
-    // nprod workgroups quantize X (M x n_in, row stride ldx) into the
-    // records and count their arrival on *flag; the other ncons wait for
-    // all of them before their first record read. The last of those to
-    // pass resets *flag and *done (its own count) to zero for the next
-    // launch.
-    const float *X;
-    int64_t ldx, n_in;
-    int nprod, ncons;
-    uint32_t *flag, *done;
     int q80s;             // the scalar Q8_0 quantizer (q80_block_sel)
 };
-
-// Bound of a consumer's wait on the producers, in polls of about 64 cycles
-// each (some 0.1 s): the producers run first whatever the grid, so the wait
-// ends long before; the bound keeps a fault elsewhere from hanging the GPU.
-constexpr uint32_t kGQSpin = 1u << 21;
 
 // steps in flight per wave: a ring of gq_depth(MT) register sets (two at
 // MT = 4, whose accumulators leave no room for four)
 __host__ __device__ constexpr int gq_depth(int MT) { return MT >= 4 ? 2 : 4; }
 
-// Dynamic LDS of gemmq_kernel<.., XM = 1 or 2>: the records of sbk steps in
-// whole KiBs. Those modes run where it is at most kGQSliceLds.
+// Dynamic LDS of gemmq_kernel<.., XM = 1>: the records of sbk steps in
+// whole KiBs. That mode runs where it is at most kGQSliceLds.
 __host__ __device__ constexpr int64_t gq_lds_bytes(int BM, int64_t sbk) {
     return (sbk * gq_rec_bytes(BM) + 1023) / 1024 * 1024;
 }
@@ -290,15 +261,11 @@ constexpr int64_t kGQSliceLds = 64 * 1024;
 //   0: through the register ring into two LDS buffers, a step ahead;
 //   1: all records of its K slice copied into LDS (dynamic, gq_lds_bytes)
 //      before the first step, so the steps read LDS only, with no record
-//      loads, LDS stores or barriers between them;
-//   2: as 1, the records written by the launch's own first workgroups
-//      (agent-scope stores, read with agent-scope loads) instead of a
-//      quantization launch before it; the other workgroups request their
-//      first weights before they wait for them.
+//      loads, LDS stores or barriers between them.
 template <uint32_t FMT, int MT, int XM>
 __global__ __launch_bounds__(kG2Threads)
 __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
-    constexpr bool FUSE = XM == 2;
+    static_assert(XM == 0 || XM == 1, "record modes 0 and 1");
     constexpr int BM = 16 * MT;
     constexpr int kRec = gq_rec_bytes(BM);
     constexpr int kXP = kRec / 16;
@@ -313,49 +280,12 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t sx0[XM == 0 ? kSx : 16];
     __shared__ __attribute__((aligned(16))) uint8_t sx1[XM == 0 ? kSx : 16];
     extern __shared__ __attribute__((aligned(16))) uint8_t gq_slice[];
-    if constexpr (FUSE) {
-        if ((int)blockIdx.x < A.nprod) {  // producer: blocks p, p + nprod * 256, ...
-            const int64_t nblocks = A.Mp * (A.n_in / 32);
-            for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nblocks;
-                 i += (int64_t)A.nprod * 256)
-                gq_quantize_one<BM, bias, true>(A.X, A.ldx, A.M, A.n_in,
-                                                const_cast<uint8_t *>(A.x), i, A.q80s);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            __syncthreads();
-            if (threadIdx.x == 0)
-                __hip_atomic_fetch_add(A.flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
-        }
-    }
-    // a consumer has seen every producer arrive: count it; the last resets
-    // both counters
-    auto passed = [&]() {
-        if (__hip_atomic_fetch_add(A.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            (uint32_t)A.ncons - 1) {
-            __hip_atomic_store(A.flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(A.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    };
-    // the producers are a multiple of 8 workgroups, so b keeps the XCD of
-    // blockIdx.x
-    const int b = (int)blockIdx.x - (FUSE ? A.nprod : 0);
+    const int b = (int)blockIdx.x;
     const int xcd = b & 7, t = b >> 3;
     const int per = A.MB * A.S;
     const int nblk = (t / per) * 8 + xcd, rest = t % per;
     const int slice = rest / A.MB, mblk = rest % A.MB;
-    if (nblk >= A.NB) {
-        if constexpr (FUSE) {
-            if (threadIdx.x == 0) {
-                uint32_t it = 0;
-                while (__hip_atomic_load(A.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-                           (uint32_t)A.nprod && ++it < kGQSpin)
-                    __builtin_amdgcn_s_sleep(1);
-                passed();
-            }
-        }
-        return;
-    }
+    if (nblk >= A.NB) return;
     const int c0 = slice * A.SBK;
     const int c1 = c0 + A.SBK < A.nk ? c0 + A.SBK : A.nk;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -383,14 +313,11 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
         for (int k = 0; k < kXPT; k++)
             *reinterpret_cast<uint4 *>(dst + ((int)threadIdx.x + kG2Threads * k) * 16) = o.xs[k];
     };
-    // records written in this launch (FUSE) are read with agent-scope
-    // loads, past a stale line in this XCD's L2
-    constexpr int kXAux = FUSE ? 16 : 0;
     auto load_x = [&](int c, Ops &o) {
 #pragma unroll
         for (int k = 0; k < kXPT; k++)
             o.xs[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    xr, (int)threadIdx.x * 16, c * kRec + 4096 * k, kXAux));
+                                                    xr, (int)threadIdx.x * 16, c * kRec + 4096 * k, 0));
     };
     auto load_wt = [&](int c, Ops &o) {
         const int so = (c * 4 + wave) * kChunk;
@@ -475,7 +402,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
         }
         store_x(nxt, xn);
     };
-    // XM 1, 2: step c with the slice's records in LDS and only the weights
+    // XM 1: step c with the slice's records in LDS and only the weights
     // in the ring
     auto step_lds = [&](int c, const Ops &cur, Ops &ahead) {
         const int ca = c + kD - 1 < c1 ? c + kD - 1 : c1 - 1;
@@ -532,20 +459,9 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
                 step(c + u, o[u], o[(u + kD - 1) % kD], o[(u + 1) % kD], (u & 1) ? sx1 : sx0,
                      (u & 1) ? sx0 : sx1);
     } else {
-        // the first weights go out first (before the wait on the producers)
+        // the first weights go out first
 #pragma unroll
         for (int u = 0; u + 1 < kD; u++) load_wt(c0 + u < c1 ? c0 + u : c1 - 1, o[u]);
-        if constexpr (FUSE) {
-            if (threadIdx.x == 0) {
-                uint32_t it = 0;
-                while (__hip_atomic_load(A.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-                           (uint32_t)A.nprod && ++it < kGQSpin)
-                    __builtin_amdgcn_s_sleep(1);
-                passed();
-            }
-            __syncthreads();
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        }
         // the slice's records, 1 KiB per wave instruction straight into LDS
         // (whole KiBs: the last may read into the next record, or zero past
         // the buffer, into LDS that no step reads)
@@ -553,7 +469,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
         for (int i = wave; i < kib; i += kG2Threads / 64)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 xr, (__attribute__((address_space(3))) void *)(gq_slice + i * 1024), 16, lane * 16,
-                c0 * kRec + i * 1024, 0, kXAux);
+                c0 * kRec + i * 1024, 0, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         for (int c = c0; c < c1; c += kD) {

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -47,7 +48,7 @@ struct Options {
     int64_t gemm6_min_m = -1;  // smallest M on the Q6_K GEMM (rule: kGemm6MinM)
     int64_t gemmh_min_m = -1;  // smallest M on the F16 GEMM (rule: kGemmhMinM)
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
-    int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0, 1, 2 (gemmq_kernel XM; rule: 1 where it fits)
+    int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0 or 1 (gemmq_kernel XM; rule: 1 where it fits)
     int64_t gemm2s_max_m = -1; // largest M on the small-M Q4_K GEMM, 0: none (rule: 16)
     int64_t gemmks_max_m = -1; // largest M on the small-M K-quant GEMM, 0: none (rule: 16)
     int64_t gemmks_q4k = -1;   // Q4_K small M on gemmks.h (1) or gemm2s.h (0) (rule: 0)
@@ -234,6 +235,8 @@ static int ensure(sihip_ctx *ctx, void **buf, size_t *cap, size_t bytes, hipStre
 constexpr size_t kNoAllocCntBytes = (size_t)kGemmCounters * 4;
 constexpr size_t kNoAllocBytes = ((size_t)16 << 20) + kNoAllocCntBytes;  // 16 MiB + counters
 static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+// devices whose scratch counters sihip_init clears (one flag each)
+constexpr int kMaxDevices = 64;
 
 extern "C" int sihip_abi_version(void) { return SIHIP_ABI_VERSION; }
 
@@ -269,11 +272,30 @@ extern "C" int sihip_init(int device, sihip_ctx **out) {
         (void)hipFree(cnt);
         return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: GEMM slice counters: memset failed");
     }
-    // the scratch counters start at zero (each sliced launch leaves them so)
-    if (hipMemset((uint8_t *)sp + (kNoAllocBytes - kNoAllocCntBytes), 0, kNoAllocCntBytes) !=
-        hipSuccess) {
-        (void)hipFree(cnt);
-        return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: scratch counters: memset failed");
+    // The scratch counters start at zero (each sliced launch leaves them
+    // so). The scratch is one per device and shared by every context, so
+    // they are cleared once per device and process, by its first context:
+    // clearing them again when a later context is created could reset them
+    // under a sliced launch of another context still running on another
+    // stream.
+    {
+        static std::mutex mu;
+        static bool cleared[kMaxDevices];
+        std::lock_guard<std::mutex> lock(mu);
+        if (device >= kMaxDevices) {
+            (void)hipFree(cnt);
+            return set_err(nullptr, SIHIP_EINVAL, "sihip_init: device %d past %d", device,
+                           kMaxDevices);
+        }
+        if (!cleared[device]) {
+            if (hipMemset((uint8_t *)sp + (kNoAllocBytes - kNoAllocCntBytes), 0, kNoAllocCntBytes) !=
+                    hipSuccess ||
+                hipDeviceSynchronize() != hipSuccess) {
+                (void)hipFree(cnt);
+                return set_err(nullptr, SIHIP_EDEVICE, "sihip_init: scratch counters: memset failed");
+            }
+            cleared[device] = true;
+        }
     }
     sihip_ctx *c = new sihip_ctx();
     c->device = device;
@@ -1258,19 +1280,11 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     // record mode: with up to 32-row m blocks and a K slice whose records
     // fit kGQSliceLds, the slice's records go to LDS up front (mode 1: 2-7%
     // faster than the ring at M = 8-16, e.g. kv 1024 x 5120 13.1 against
-    // 14.1 us per call). Mode 2 (the launch's first workgroups quantize X:
-    // a multiple of 8 producers, so the others keep their XCD order; the
-    // K-slice counters stay below the last two, which it uses) runs only
-    // when the GEMMQ_XMODE option asks for it: its agent-scope record
-    // loads miss the L2, and it was slower than a separate quantization
-    // launch on every config-4 shape (27648 x 5120 at M = 8: 34.5 against
-    // 30.3 us), faster only on 4864 x 896 (10.0 against 11.4).
+    // 14.1 us per call). The GEMMQ_XMODE option 0 forces the ring.
     const int64_t lds = gq_lds_bytes(BM, p.SBK);
     int xm = MT <= 2 && lds <= kGQSliceLds ? 1 : 0;
     if (B.xmode == 0) xm = 0;
-    if (B.xmode == 2 && xm == 1 && B.quant && (p.Mp / BM) * NB <= kGemmCounters - 2) xm = 2;
-    const bool fuse = xm == 2;
-    if (B.quant && !fuse)
+    if (B.quant)
         hipLaunchKernelGGL((gemmq_quantize_x<BM, bias>), dim3((unsigned)((threads + 255) / 256)),
                            dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws, B.q80s);
     GQArgs A{};
@@ -1291,18 +1305,6 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     A.cnt = p.S > 1 ? B.cnt : nullptr;
     const int64_t cons = (int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S;
     if constexpr (MT <= 2) {
-        if (fuse) {
-            A.X = X;
-            A.ldx = ldx;
-            A.n_in = L.n_in;
-            A.nprod = (int)(((threads + 255) / 256 + 7) / 8 * 8);
-            A.ncons = (int)cons;
-            A.flag = B.cnt + kGemmCounters - 2;
-            A.done = B.cnt + kGemmCounters - 1;
-            hipLaunchKernelGGL((gemmq_kernel<FMT, MT, 2>), dim3((unsigned)(A.nprod + cons)),
-                               dim3(kG2Threads), (unsigned)lds, st, A);
-            return hipGetLastError();
-        }
         if (xm == 1) {
             hipLaunchKernelGGL((gemmq_kernel<FMT, MT, 1>), dim3((unsigned)cons), dim3(kG2Threads),
                                (unsigned)lds, st, A);
