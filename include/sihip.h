@@ -233,6 +233,13 @@ int sihip_synchronize(sihip_ctx *ctx);
  *    dispatches to on x86): f16 d, int8 qs[32] per 32 (34 B).
  *  F16 pair conversion (reference backend.c:19-27): RNE binary16. */
 int sihip_quantize_q8_K(sihip_ctx *ctx, const float *x, void *out, int64_t n);
+/* X [M x n_in] (host, row-major) through the GEMMs' activation quantizer
+ * (the records of the matrix-core kernels, m blocks of bm = 16, 32, 64 or
+ * 128 rows), read back into out as each row's Q8_K blocks in the layout of
+ * si_quant_row_q8_K (kernels.h:67; 292 bytes per block, rows in order), so
+ * they can be compared with it bit for bit. */
+int sihip_quantize_q8_K_rows(sihip_ctx *ctx, const float *X, int64_t M, int64_t n_in,
+                             int bm, void *out);
 int sihip_quantize_q8_0(sihip_ctx *ctx, const float *x, void *out, int64_t n);
 int sihip_convert_f16(sihip_ctx *ctx, const float *x, void *out, int64_t n);
 

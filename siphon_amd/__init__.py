@@ -88,6 +88,7 @@ def load_library(path: str = HIP_SO) -> ctypes.CDLL:
                                        ctypes.POINTER(_vp), _vp]
     for fn in ("sihip_quantize_q8_K", "sihip_quantize_q8_0", "sihip_convert_f16"):
         getattr(L, fn).argtypes = [_vp, _vp, _vp, _i64]
+    L.sihip_quantize_q8_K_rows.argtypes = [_vp, _vp, _i64, _i64, ctypes.c_int, _vp]
     L.sihip_vec_dot.argtypes = [_vp, _u32, ctypes.c_int, _vp, _vp, _vp]
     L.sihip_dev_alloc.argtypes = [_vp, _u64, ctypes.POINTER(_vp)]
     L.sihip_dev_free.argtypes = [_vp, _vp]
@@ -261,6 +262,15 @@ class Device:
         fn = {Q8_K: self.L.sihip_quantize_q8_K, Q8_0: self.L.sihip_quantize_q8_0,
               F16: self.L.sihip_convert_f16}[pair]
         self._check(fn(self.ctx, _ptr(x), _ptr(out), x.size))
+        return out
+
+    def quantize_gemm_rows(self, X: np.ndarray, bm: int) -> np.ndarray:
+        """Rows of X through the matrix-core GEMMs' Q8_K activation records
+        (m blocks of bm rows), returned as Q8_K blocks (292 B each)."""
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        M, n_in = X.shape
+        out = np.zeros(M * (n_in // 256) * 292, dtype=np.uint8)
+        self._check(self.L.sihip_quantize_q8_K_rows(self.ctx, _ptr(X), M, n_in, bm, _ptr(out)))
         return out
 
     def vec_dot(self, wtype: int, n: int, w: np.ndarray, a: np.ndarray) -> float:

@@ -66,7 +66,14 @@ __host__ __device__ constexpr int g2_rec_bsum(int BM) { return 256 * BM; }
 __host__ __device__ constexpr int g2_rec_dx(int BM) { return 288 * BM; }
 
 // One 16-lane row per Q8_K block (row m, super-block c) of X; rows M..Mp-1
-// are zero. Grid: ceil(Mp * nb / 16) workgroups of 256.
+// are zero. Grid: gemm2_quantize_grid(Mp * nb) workgroups of 256. (A wave
+// per block, 4 elements per lane, measured no faster at M = 512 and slower
+// at M = 2048, 14.8 against 13.1 us: its 4-byte record stores.)
+constexpr int kG2QBlocks = kG2Threads / 16;  // blocks per workgroup
+__host__ __device__ inline int64_t gemm2_quantize_grid(int64_t blocks) {
+    return (blocks + kG2QBlocks - 1) / kG2QBlocks;
+}
+
 template <int BM>
 __global__ __launch_bounds__(kG2Threads) void gemm2_quantize_x(const float *x, int64_t ldx,
                                                                int64_t M, int64_t Mp, int64_t nb,

@@ -62,6 +62,11 @@ __host__ __device__ inline int64_t lds_col_bytes(uint32_t pair, int64_t n_in) {
 // together; selecting the matrix by a loaded value first would add a round
 // trip (measured: about 0.4 us per launch).
 constexpr int kMaxSegs = 4;
+// Segments of one launch: a matrix of a launch of several may be cut into
+// consecutive ranges of its row tiles, each a segment of its own, so that
+// every segment has the same workgroup count and the grid (the widest
+// segment's workgroups x the segments) has no surplus (run_matvec_multi).
+constexpr int kMaxLaunchSegs = 8;
 
 struct MVSeg {
     const uint8_t *plane[4];  // plane bases
@@ -86,7 +91,7 @@ struct MVSeg {
 };
 
 struct MVArgs {
-    MVSeg seg[kMaxSegs];
+    MVSeg seg[kMaxLaunchSegs];
     int nseg;
     int64_t n_in;
     const float *x;       // f32 activations, column c at x + c * ldx (or null)

@@ -736,6 +736,31 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
             if (rc) return rc;
         }
     }
+    // A launch of several matrices gets a grid of (its widest segment's
+    // workgroups) x (segments), and a segment narrower than the widest
+    // leaves the surplus to exit at once. Those exits still hold workgroup
+    // slots while their arguments load, and with two resident per CU the
+    // q/k/v launch (768 workgroups, 384 of them surplus) kept its Q6_K wv
+    // workgroups waiting for slots. A whole-row matrix whose workgroup count
+    // is a multiple of the narrowest matrix's is therefore cut into ranges
+    // of consecutive row tiles of that many workgroups (a range is the same
+    // matrix from a later tile: plane bases, y and rows offset), so every
+    // segment is equally wide: q/k/v runs as 6 x 64 workgroups.
+    int parts[kMaxSegs];
+    int nsegs = 0;
+    int64_t narrow = 0;
+    for (int i = 0; i < count; i++)
+        if (narrow == 0 || nwg[i] < narrow) narrow = nwg[i];
+    for (int i = 0; i < count; i++) {
+        const int64_t ntiles = (n_out[i] + w[i]->L.R - 1) / w[i]->L.R;
+        parts[i] = 1;
+        if (count > 1 && w[i]->split == 1 && nwg[i] > narrow && nwg[i] % narrow == 0 &&
+            ntiles == nwg[i] * kWaves)
+            parts[i] = (int)(nwg[i] / narrow);
+        nsegs += parts[i];
+    }
+    if (nsegs > kMaxLaunchSegs)
+        for (int i = 0; i < count; i++) parts[i] = 1;
     int64_t m = 0;
     while (m < M) {
         int nc = ncmax;
@@ -743,28 +768,41 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         MVArgs A;
         memset(&A, 0, sizeof(A));
         uint32_t wg = 0;
+        int ns = 0;
         for (int i = 0; i < count; i++) {
             const Layout &L = w[i]->L;
-            MVSeg &sg = A.seg[i];
-            for (int p = 0; p < 4; p++) sg.plane[p] = w[i]->dev + L.plane_off[p];
-            sg.y = y[i] + m * ldy[i];
-            sg.ldy = ldy[i];
-            sg.part = w[i]->part;
-            sg.cnt = w[i]->cnt;
-            sg.split = w[i]->split;
-            sg.spr = w[i]->spr;
-            sg.type = L.type;
-            sg.n_out = (uint32_t)n_out[i];
-            sg.ntiles = (uint32_t)((n_out[i] + L.R - 1) / L.R);
-            sg.nwg = (uint32_t)nwg[i];
-            sg.G = (uint32_t)L.G;
-            sg.logG = (uint32_t)L.logG;
-            sg.R = (uint32_t)L.R;
-            sg.S = (uint32_t)L.S;
-            sg.ncols = (uint32_t)L.ncols;
-            wg = (uint32_t)nwg[i] > wg ? (uint32_t)nwg[i] : wg;
+            const int64_t ntiles = (n_out[i] + L.R - 1) / L.R;
+            const int64_t per = ntiles / parts[i];  // row tiles of a range (parts[i] divides)
+            for (int k = 0; k < parts[i]; k++) {
+                const int64_t t0 = k * per;
+                const int64_t rows = k + 1 < parts[i] ? per * L.R : n_out[i] - t0 * L.R;
+                MVSeg &sg = A.seg[ns++];
+                // the records of tile t0 start at record (t0 * S) * 64 of a
+                // column-level plane, 8 times that of a unit-level one
+                for (int p = 0; p < 4; p++) {
+                    const int64_t per_col = is_kquant(L.type) && !L.plane_blk[p] ? 8 : 1;
+                    sg.plane[p] = w[i]->dev + L.plane_off[p] +
+                                  t0 * L.S * 64 * per_col * L.plane_bytes[p];
+                }
+                sg.y = y[i] + m * ldy[i] + t0 * L.R;
+                sg.ldy = ldy[i];
+                sg.part = w[i]->part;
+                sg.cnt = w[i]->cnt;
+                sg.split = w[i]->split;
+                sg.spr = w[i]->spr;
+                sg.type = L.type;
+                sg.n_out = (uint32_t)rows;
+                sg.ntiles = (uint32_t)((rows + L.R - 1) / L.R);
+                sg.nwg = (uint32_t)(nwg[i] / parts[i]);
+                sg.G = (uint32_t)L.G;
+                sg.logG = (uint32_t)L.logG;
+                sg.R = (uint32_t)L.R;
+                sg.S = (uint32_t)L.S;
+                sg.ncols = (uint32_t)L.ncols;
+                wg = sg.nwg > wg ? sg.nwg : wg;
+            }
         }
-        A.nseg = count;
+        A.nseg = ns;
         A.n_in = n_in;
         A.q80s = ctx->opt.q80_scalar > 0;
         A.x = x ? x + m * ldx : nullptr;
@@ -774,7 +812,7 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         A.nc = nc;
         A.col_bytes = cb;
         const hipError_t e =
-            launch_any(A, f0, f1, dim3(wg, (unsigned)count),
+            launch_any(A, f0, f1, dim3(wg, (unsigned)ns),
                        (size_t)(cb * nc + (any_sliced(A) ? kSliceLds : 0)), st);
         if (e != hipSuccess)
             return set_err(ctx, SIHIP_EDEVICE, "matvec launch: %s", hipGetErrorString(e));
@@ -1244,7 +1282,7 @@ static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const G
     const int64_t nb = L.n_in / 256;
     const int64_t blocks = p.Mp * nb;
     if (B.quant)
-        hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)),
+        hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)gemm2_quantize_grid(blocks)),
                            dim3(kG2Threads), 0, st, X, ldx, M, p.Mp, nb, ws);
     G2Args A;
     A.w = w->gemm2;
@@ -1366,7 +1404,7 @@ static hipError_t launch_gemm6(const sihip_weight *w, const GemmPlan &p, const G
     const int64_t nb = L.n_in / 256;
     const int64_t blocks = p.Mp * nb;
     if (B.quant)
-        hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)((blocks + 15) / 16)),
+        hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)gemm2_quantize_grid(blocks)),
                            dim3(kG2Threads), 0, st, X, ldx, M, p.Mp, nb, B.ws);
     G6Args A;
     A.w = w->gemm2;
@@ -1461,7 +1499,7 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
     if (p.v2 && p.small && !p.q4s) {
         const int64_t nb = L.n_in / 256;
         if (B.quant)
-            hipLaunchKernelGGL(gemm2_quantize_x<16>, dim3((unsigned)((16 * nb + 15) / 16)),
+            hipLaunchKernelGGL(gemm2_quantize_x<16>, dim3((unsigned)gemm2_quantize_grid(16 * nb)),
                                dim3(kG2Threads), 0, st, X, ldx, M, (int64_t)16, nb, B.ws);
         GKSArgs A;
         A.w = w->gsmall;
@@ -1499,7 +1537,7 @@ static int launch_gemm_mfma(sihip_ctx *ctx, const sihip_weight *w, const GemmPla
         const Layout &L = w->L;
         const int64_t nb = L.n_in / 256;
         if (B.quant)
-            hipLaunchKernelGGL(gemm2_quantize_x<16>, dim3((unsigned)((16 * nb + 15) / 16)),
+            hipLaunchKernelGGL(gemm2_quantize_x<16>, dim3((unsigned)gemm2_quantize_grid(16 * nb)),
                                dim3(kG2Threads), 0, st, X, ldx, M, (int64_t)16, nb, B.ws);
         G2SArgs A;
         A.w = w->gemm2;
@@ -2109,6 +2147,56 @@ extern "C" int sihip_quantize_q8_K(sihip_ctx *ctx, const float *x, void *out, in
     HIP_OK(ctx, hipGetLastError());
     HIP_OK(ctx, hipMemcpyAsync(out, ctx->d_out, (size_t)nb * 292, hipMemcpyDeviceToHost, ctx->stream));
     HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    return SIHIP_OK;
+}
+
+extern "C" int sihip_quantize_q8_K_rows(sihip_ctx *ctx, const float *X, int64_t M, int64_t n_in,
+                                        int bm, void *out) {
+    if (!ctx || !X || !out) return set_err(ctx, SIHIP_EINVAL, "quantize_q8_K_rows: NULL argument");
+    if (M <= 0 || n_in <= 0 || n_in % 256)
+        return set_err(ctx, SIHIP_EINVAL, "quantize_q8_K_rows: M > 0 and n_in %% 256 == 0 needed");
+    if (bm != 16 && bm != 32 && bm != 64 && bm != 128)
+        return set_err(ctx, SIHIP_EINVAL, "quantize_q8_K_rows: bm must be 16, 32, 64 or 128");
+    HIP_OK(ctx, hipSetDevice(ctx->device));
+    const int64_t nb = n_in / 256, Mp = (M + bm - 1) / bm * bm;
+    const int64_t rec = g2_rec_bytes(bm), rec_total = Mp / bm * nb * rec;
+    int rc = ensure(ctx, &ctx->d_in, &ctx->d_in_cap, (size_t)(M * n_in * 4));
+    if (rc) return rc;
+    rc = ensure(ctx, &ctx->d_out, &ctx->d_out_cap, (size_t)rec_total);
+    if (rc) return rc;
+    HIP_OK(ctx, hipMemcpyAsync(ctx->d_in, X, (size_t)(M * n_in * 4), hipMemcpyHostToDevice,
+                               ctx->stream));
+    const dim3 grid((unsigned)gemm2_quantize_grid(Mp * nb)), block(kG2Threads);
+    const float *xd = (const float *)ctx->d_in;
+    uint8_t *rd = (uint8_t *)ctx->d_out;
+    switch (bm) {
+        case 16: hipLaunchKernelGGL(gemm2_quantize_x<16>, grid, block, 0, ctx->stream, xd, n_in, M, Mp, nb, rd); break;
+        case 32: hipLaunchKernelGGL(gemm2_quantize_x<32>, grid, block, 0, ctx->stream, xd, n_in, M, Mp, nb, rd); break;
+        case 64: hipLaunchKernelGGL(gemm2_quantize_x<64>, grid, block, 0, ctx->stream, xd, n_in, M, Mp, nb, rd); break;
+        default: hipLaunchKernelGGL(gemm2_quantize_x<128>, grid, block, 0, ctx->stream, xd, n_in, M, Mp, nb, rd); break;
+    }
+    HIP_OK(ctx, hipGetLastError());
+    std::vector<uint8_t> host((size_t)rec_total);
+    HIP_OK(ctx, hipMemcpyAsync(host.data(), rd, (size_t)rec_total, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_OK(ctx, hipStreamSynchronize(ctx->stream));
+    // back to the reference block layout: f32 d, 256 quants, 16 int16 sums
+    uint8_t *o = (uint8_t *)out;
+    for (int64_t m = 0; m < M; m++)
+        for (int64_t c = 0; c < nb; c++) {
+            const uint8_t *R = host.data() + ((m / bm) * nb + c) * rec;
+            const int mr = (int)(m % bm);
+            uint8_t *b = o + (m * nb + c) * 292;
+            memcpy(b, R + g2_rec_dx(bm) + 4 * mr, 4);
+            for (int e = 0; e < 256; e++)
+                b[4 + e] = R[(4 * (mr >> 4) + e / 64) * 1024 + (16 * ((e / 16) & 3) + (mr & 15)) * 16 +
+                             e % 16];
+            for (int grp = 0; grp < 16; grp++) {
+                uint16_t h;
+                memcpy(&h, R + g2_rec_bsum(bm) + mr * 32 + 2 * grp, 2);
+                const int16_t v = (int16_t)half_to_float(h);
+                memcpy(b + 260 + 2 * grp, &v, 2);
+            }
+        }
     return SIHIP_OK;
 }
 

@@ -20,7 +20,7 @@ def test_header_declares_the_boundary():
     names = declared_functions()
     for required in ("sihip_abi_version", "sihip_init", "sihip_weight_upload", "sihip_gemv",
                      "sihip_gemm", "sihip_quantize_q8_K", "sihip_quantize_q8_0",
-                     "sihip_vec_dot"):
+                     "sihip_vec_dot", "sihip_quantize_q8_K_rows"):
         assert required in names
 
 
