@@ -628,8 +628,50 @@ def bench_configs(dev, torch, stream, rng, rotate_bytes=512 << 20):
             del g, X, Y
         for w in ws:
             w.free()
+        # the read-only probe over the same bytes, rotated the same way: the
+        # floor of a launch of that size
+        probe = probe_rotated(dev, torch, stream, entry["bytes"], copies)
+        entry["probe_us"] = round(probe, 2)
+        for k in list(entry):
+            if k.startswith("batch"):
+                entry[k]["over_probe"] = round(entry[k]["us_per_call"] / probe, 3)
         out[label] = entry
     return out
+
+
+def probe_rotated(dev, torch, stream, nbytes, copies):
+    """The read-only probe (sihip_probe_read_dev) over nbytes, `copies`
+    launches over consecutive slices of one buffer in one HIP graph (as
+    bench_configs rotates its weight copies past the MALL), timed with HIP
+    events on the launch stream: average microseconds per launch."""
+    sp = stream.cuda_stream
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    span = (nbytes + 255) // 256 * 256
+    nb16 = nbytes // 16 * 16
+    buf = torch.ones((copies * span + 4095) // 4, dtype=torch.int32, device="cuda")
+
+    def run():
+        for i in range(copies):
+            dev.probe_read_dev(buf.data_ptr() + i * span, nb16, sink.data_ptr(), sp)
+    with torch.cuda.stream(stream):
+        run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run()
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(3, int(2e9 // (copies * nbytes)))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        with torch.cuda.stream(stream):
+            g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+    del g, buf
+    return us
 
 
 def probe_floors(dev, torch, stream, sizes, reps=10):

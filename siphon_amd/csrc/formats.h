@@ -173,7 +173,11 @@ inline bool make_layout(uint32_t type, int64_t n_out, int64_t n_in, int G, Layou
 // rows or elems <= 0.
 constexpr int64_t kSliceElems = 4096;
 
-SIHD inline bool sliced_rows(int64_t n_in, int64_t elems) { return elems > 0 && n_in >= 2 * elems; }
+// Rows shorter than 2 * kSliceElems are never sliced, whatever the slice
+// length (a shorter slice only cuts the long rows finer).
+SIHD inline bool sliced_rows(int64_t n_in, int64_t elems) {
+    return elems > 0 && n_in >= 2 * elems && n_in >= 2 * kSliceElems;
+}
 
 SIHD inline int64_t slice_rounds(const Layout &L, int64_t elems) {
     const int64_t col_elems = is_kquant(L.type) ? 256 : 32;

@@ -550,15 +550,20 @@ extern "C" int sihip_weight_slice_rounds(const sihip_weight *w) { return w ? (in
 
 // ---- launches -----------------------------------------------------------------
 
-// Q8_K passes of the activation loaded before the weights: all four for
-// long unsliced rows of a single column where the kernel has register room
-// (the instances with Q6_K run at 2 waves per SIMD with registers to
-// spare), else the first. Launches with sliced matrices take one pass (a
-// slice of about 4096 elements is one).
+// Q8_K passes of the activation loaded before the weights (16 blocks of
+// 256 each): all four for long unsliced rows of a single column where the
+// kernel has register room (the instances with Q6_K run at 2 waves per
+// SIMD with registers to spare); two for the other K-quants' single-matrix
+// launches of rows up to 8192 (16 more VGPRs: Q2_K 148 -> 164 and Q3_K 137
+// -> 153 keep three waves per SIMD, Q4_K and Q5_K two), so a 5120-element
+// row's last 4 blocks do not wait for a second round trip after the first
+// pass is quantized; else the first. Launches with sliced matrices take one
+// pass (a slice of about 4096 elements is one).
 template <uint32_t F0, uint32_t F1>
 static int prologue_passes(const MVArgs &A) {
     if (pair_of(F0) != T_Q8_K || A.nc != 1 || A.n_in <= 4096) return 1;
-    return (F0 == T_Q6_K || F1 == T_Q6_K) ? 4 : 1;
+    if (F0 == T_Q6_K || F1 == T_Q6_K) return 4;
+    return A.nseg == 1 && A.n_in <= 8192 ? 2 : 1;
 }
 
 static bool any_sliced(const MVArgs &A) {
@@ -577,6 +582,12 @@ static hipError_t launch_nc(const MVArgs &A, dim3 grid, size_t lds, hipStream_t 
     if constexpr (NC == 1 && (F0 == T_Q6_K || F1 == T_Q6_K)) {
         if (prologue_passes<F0, F1>(A) == 4) {
             hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 4, false, MULTI>), grid, dim3(kThreads),
+                               lds, st, A);
+            return hipGetLastError();
+        }
+    } else if constexpr (NC == 1 && !MULTI && F0 == F1 && pair_of(F0) == T_Q8_K) {
+        if (prologue_passes<F0, F1>(A) == 2) {
+            hipLaunchKernelGGL((matvec_kernel<F0, F1, NC, 2, false, MULTI>), grid, dim3(kThreads),
                                lds, st, A);
             return hipGetLastError();
         }
