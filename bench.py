@@ -67,11 +67,13 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-format matvec measurements (configs 0, 1, 4)")
     ap.add_argument("--no-attn", action="store_true", help="skip the decode attention")
-    ap.add_argument("--profile", choices=("gemm", "traffic", "configs", "attn", "prefill", "calib"),
+    ap.add_argument("--profile", choices=("gemm", "traffic", "configs", "attn", "prefill", "batch8",
+                                          "calib"),
                     help="run one workload for a profiler and exit: the GEMM M sweep, "
                          "a 64 MiB copy plus 12 gate/up launches (HBM counter runs), "
                          "the per-format matvec measurements, the decode attention, "
-                         "the M=512 prefill pass over 32 layers, or the HBM calibration "
+                         "the M=512 prefill pass over 32 layers and the batch-8 decode step, "
+                         "the batch-8 decode step alone, or the HBM calibration "
                          "(a 4 GiB streaming read and the decode pass's launches read-only)")
     return ap.parse_args()
 
@@ -120,6 +122,9 @@ def main():
             layers, _ = build_layers(dev, rng, 0)
             out = bench_prefill_pass(dev, torch, stream, layers)
             out["decode_batch8"] = bench_batch_decode(dev, torch, stream, layers)
+        elif args.profile == "batch8":
+            layers, _ = build_layers(dev, rng, 0)
+            out = bench_batch_decode(dev, torch, stream, layers)
         elif args.profile == "configs":
             out = bench_configs(dev, torch, stream, rng)
         elif args.profile == "attn":

@@ -247,6 +247,210 @@ __host__ __device__ constexpr int gemmks_sw() {
     return NH > 2 ? 2 : FMT == T_Q3_K ? 4 : FMT == T_Q2_K ? 3 : 2;
 }
 
+// One super-block of a lane's weights (a 32-row block's chunk) and of its
+// activation fragments.
+template <uint32_t FMT>
+struct KSWStage {
+    uint4 qa[4];    // quant plane 0: nibble formats K-step ks; 2-bit formats [0..1] used
+    uint4 qb[2];    // quant plane 1 (Q6_K: 2 pieces, Q5_K/Q3_K: [0])
+    uint32_t sc[2][KS<FMT>::unit32 ? 2 : 1];  // n tile: this lane group's scale (and min) words
+    uint32_t d[2];  // n tile: f16 d and dmin (Q3_K, Q6_K: the word holding d)
+};
+template <int NH>
+struct KSXStage {
+    uint4 a[NH][4]; // masked activation fragments of rows 4 h + l % 4, K-step ks
+    float4 dx[NH];  // block scales of rows 4 h .. 4 h + 3
+};
+
+__device__ inline uint4 ks_ld4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// The weights of super-block c (wave-uniform) of the chunk column behind wr.
+// readfirstlane keeps the offsets scalar (a loop counter the compiler holds
+// in a VGPR would make every buffer load a waterfall loop over lanes).
+template <uint32_t FMT>
+__device__ inline void ks_load_w(__amdgpu_buffer_rsrc_t wr, int c, int lane, KSWStage<FMT> &s) {
+    using F = KS<FMT>;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int so = __builtin_amdgcn_readfirstlane(c) * F::chunk;
+    if constexpr (F::nib) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) s.qa[ks] = ks_ld4(wr, ks * 1024 + lane * 16, so);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; j++) s.qa[j] = ks_ld4(wr, lane * 32 + j * 16, so);
+    }
+    if constexpr (FMT == T_Q6_K) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) s.qb[j] = ks_ld4(wr, F::QA + lane * 32 + j * 16, so);
+    } else if constexpr (F::QB > 0) {
+        s.qb[0] = ks_ld4(wr, F::QA + lane * 16, so);
+    }
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        if constexpr (F::unit32) {
+            const uint2 t = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                          wr, F::SC + (16 * nt + r16) * 16 + 8 * (g >> 1), so, 0));
+            s.sc[nt][0] = t.x;
+            s.sc[nt][1] = t.y;
+        } else {
+            s.sc[nt][0] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::SC + (16 * nt + r16) * 16 + 4 * g, so, 0);
+        }
+    }
+    if constexpr (F::mins) {
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+            s.d[nt] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D + (16 * nt + r16) * 4, so, 0);
+    } else {
+        s.d[0] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D + (r16 >> 1) * 4, so, 0);
+        s.d[1] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D + 32 + (r16 >> 1) * 4, so, 0);
+    }
+}
+
+// The weight operand of K-step ks, n tile nt: dword i holds slots 4 i .. 4 i + 3.
+template <uint32_t FMT>
+__device__ inline v4i2_t ks_operand(const KSWStage<FMT> &s, int ks, int nt) {
+    const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u, m1 = 0x01010101u;
+    uint32_t q[4];
+    if constexpr (KS<FMT>::nib) {
+        const uint32_t w0 = nt ? s.qa[ks].z : s.qa[ks].x;
+        const uint32_t w1 = nt ? s.qa[ks].w : s.qa[ks].y;
+        q[0] = w0 & m4;
+        q[1] = w1 & m4;
+        q[2] = (w0 >> 4) & m4;
+        q[3] = (w1 >> 4) & m4;
+    } else {
+        const uint4 wv = s.qa[ks >> 1];
+        const uint32_t W = (ks & 1) ? (nt ? wv.w : wv.z) : (nt ? wv.y : wv.x);
+#pragma unroll
+        for (int t = 0; t < 4; t++) q[t] = (W >> (2 * t)) & m2;
+    }
+    if constexpr (FMT == T_Q6_K) {
+        const uint4 hv = s.qb[ks >> 1];
+        const uint32_t H = (ks & 1) ? (nt ? hv.w : hv.z) : (nt ? hv.y : hv.x);
+#pragma unroll
+        for (int t = 0; t < 4; t++) q[t] |= ((H >> (2 * t)) & m2) << 4;
+    }
+    if constexpr (FMT == T_Q5_K || FMT == T_Q3_K) {
+        const uint32_t Fw = ks == 0 ? s.qb[0].x : ks == 1 ? s.qb[0].y : ks == 2 ? s.qb[0].z : s.qb[0].w;
+        constexpr int pos = FMT == T_Q5_K ? 4 : 2;
+#pragma unroll
+        for (int t = 0; t < 4; t++) q[t] |= ((Fw >> (t + 4 * nt)) & m1) << pos;
+    }
+    // Q3_K: q - 4 (q + 124 < 256, bit 7 flipped); Q6_K: q - 32 (q + 96)
+    if constexpr (FMT == T_Q3_K) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) q[t] = (q[t] + 0x7C7C7C7Cu) ^ 0x80808080u;
+    }
+    if constexpr (FMT == T_Q6_K) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) q[t] = (q[t] + 0x60606060u) ^ 0x80808080u;
+    }
+    return (v4i2_t){(int)q[0], (int)q[1], (int)q[2], (int)q[3]};
+}
+
+// This lane's scale and min at K-step ks, n tile nt.
+template <uint32_t FMT>
+__device__ inline void ks_scale(const KSWStage<FMT> &s, int ks, int nt, int &sv, int &mv) {
+    if constexpr (KS<FMT>::unit32) {  // unit 2 ks + g / 2 at byte ks
+        sv = (int)((s.sc[nt][0] >> (8 * ks)) & 0xffu);
+        mv = (int)((s.sc[nt][1] >> (8 * ks)) & 0xffu);
+    } else if constexpr (FMT == T_Q2_K) {  // group 4 ks + g at byte ks
+        const uint32_t b = (s.sc[nt][0] >> (8 * ks)) & 0xffu;
+        sv = (int)(b & 15u);
+        mv = (int)(b >> 4);
+    } else {
+        sv = sbfe8(s.sc[nt][0], 8u * (uint32_t)ks);
+        mv = 0;
+    }
+}
+
+// One super-block: y[h][nt][i] += its contribution for activation rows
+// 4 h + i (the sums of this lane's own K slots; the 4 lane groups are added
+// after the last super-block).
+template <uint32_t FMT, int NH>
+__device__ inline void ks_compute(const KSWStage<FMT> &s, const KSXStage<NH> &x, int r16,
+                                  v4f2_t (&y)[NH][2]) {
+    using F = KS<FMT>;
+    v4i2_t S[NH][2], T[NH][2];
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            S[h][nt] = (v4i2_t){0, 0, 0, 0};
+            T[h][nt] = (v4i2_t){0, 0, 0, 0};
+        }
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        v4i2_t am[NH];
+#pragma unroll
+        for (int h = 0; h < NH; h++) am[h] = __builtin_bit_cast(v4i2_t, x.a[h][ks]);
+        v4i2_t P1[NH];
+        if constexpr (F::mins) {
+            const v4i2_t ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+            const v4i2_t z = {0, 0, 0, 0};
+#pragma unroll
+            for (int h = 0; h < NH; h++) P1[h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[h], ones, z, 0, 0, 0);
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const v4i2_t b = ks_operand<FMT>(s, ks, nt);
+            int sv, mv;
+            ks_scale<FMT>(s, ks, nt, sv, mv);
+#pragma unroll
+            for (int h = 0; h < NH; h++) {
+                const v4i2_t z = {0, 0, 0, 0};
+                const v4i2_t P = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[h], b, z, 0, 0, 0);
+                // |P|, |P1| < 2^17 and |s|, |m| <= 128: 24-bit products
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    S[h][nt][i] += __mul24(sv, P[i]);
+                    if constexpr (F::mins) T[h][nt][i] += __mul24(mv, P1[h][i]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        // mins formats: d in the low, dmin in the high half; Q3_K, Q6_K:
+        // the word of rows 2 (r16 / 2), + 1
+        const uint32_t dword = s.d[nt];
+        const float dw = half_to_float(F::mins ? (dword & 0xffffu) : (dword >> (16 * (r16 & 1))) & 0xffffu);
+        const float ndm = F::mins ? -half_to_float(dword >> 16) : 0.0f;
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            const float dxv[4] = {x.dx[h].x, x.dx[h].y, x.dx[h].z, x.dx[h].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if constexpr (F::mins) {
+                    const float u = fma_f32(dw, (float)S[h][nt][i], ndm * (float)T[h][nt][i]);
+                    y[h][nt][i] = fma_f32(dxv[i], u, y[h][nt][i]);
+                } else {
+                    y[h][nt][i] = fma_f32(dxv[i] * dw, (float)S[h][nt][i], y[h][nt][i]);
+                }
+            }
+        }
+    }
+}
+
+// Adds the 4 lane groups (each holds the sums over its own slots):
+// partners l ^ 16, then l ^ 32, the same order in every lane.
+template <int NH>
+__device__ inline void ks_add_groups(v4f2_t (&y)[NH][2]) {
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = y[h][nt][i];
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                y[h][nt][i] = v;
+            }
+}
+
 // NH: 4-row activation groups (M <= 4 NH); KW: waves per workgroup, which
 // split the super-blocks of its 32 rows; SW: super-blocks of weights a wave
 // has in registers (the one computed and SW - 1 in flight).
@@ -272,65 +476,17 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmks_kernel(GKSArgs A) {
     // record fragment. The other lanes load from past the end of the buffer
     // resource, which returns zeros without a memory access.
     const int a_off = (r16 >> 2) == g ? 0 : 0x40000000;
-    struct WStage {  // one super-block's weights
-        uint4 qa[4];    // quant plane 0: nibble formats K-step ks; 2-bit formats [0..1] used
-        uint4 qb[2];    // quant plane 1 (Q6_K: 2 pieces, Q5_K/Q3_K: [0])
-        uint32_t sc[2][F::unit32 ? 2 : 1];  // n tile: this lane group's scale (and min) words
-        uint32_t d[2];  // n tile: f16 d and dmin (Q3_K, Q6_K: the word holding d)
-    };
-    struct XStage {  // one super-block's activations
-        uint4 a[NH][4]; // activation fragments
-        float4 dx[NH];  // block scales of rows 4 h .. 4 h + 3
-    };
-    auto ld4 = [&](__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-    };
-    // c is wave-uniform; readfirstlane keeps the offsets scalar (a loop
-    // counter the compiler holds in a VGPR would make every buffer load a
-    // waterfall loop over lanes)
-    auto load_w = [&](int c, WStage &s) {
-        const int so = __builtin_amdgcn_readfirstlane(c) * kChunk;
-        if constexpr (F::nib) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) s.qa[ks] = ld4(wr, ks * 1024 + lane * 16, so);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 2; j++) s.qa[j] = ld4(wr, lane * 32 + j * 16, so);
-        }
-        if constexpr (FMT == T_Q6_K) {
-#pragma unroll
-            for (int j = 0; j < 2; j++) s.qb[j] = ld4(wr, F::QA + lane * 32 + j * 16, so);
-        } else if constexpr (F::QB > 0) {
-            s.qb[0] = ld4(wr, F::QA + lane * 16, so);
-        }
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            if constexpr (F::unit32) {
-                const uint2 t = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                              wr, F::SC + (16 * nt + r16) * 16 + 8 * (g >> 1), so, 0));
-                s.sc[nt][0] = t.x;
-                s.sc[nt][1] = t.y;
-            } else {
-                s.sc[nt][0] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::SC + (16 * nt + r16) * 16 + 4 * g, so, 0);
-            }
-        }
-        if constexpr (F::mins) {
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-                s.d[nt] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D + (16 * nt + r16) * 4, so, 0);
-        } else {
-            s.d[0] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D + (r16 >> 1) * 4, so, 0);
-            s.d[1] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D + 32 + (r16 >> 1) * 4, so, 0);
-        }
-    };
+    using WStage = KSWStage<FMT>;
+    using XStage = KSXStage<NH>;
+    auto load_w = [&](int c, WStage &s) { ks_load_w<FMT>(wr, c, lane, s); };
     auto load_x = [&](int c, XStage &s) {
         const int xo = __builtin_amdgcn_readfirstlane(c) * kRec;
 #pragma unroll
         for (int h = 0; h < NH; h++) {
             const int src = 16 * g + 4 * h + (lane & 3);
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) s.a[h][ks] = ld4(xr, a_off + ks * 1024 + src * 16, xo);
-            s.dx[h] = __builtin_bit_cast(float4, ld4(xr, g2_rec_dx(BM) + 16 * h, xo));
+            for (int ks = 0; ks < 4; ks++) s.a[h][ks] = ks_ld4(xr, a_off + ks * 1024 + src * 16, xo);
+            s.dx[h] = __builtin_bit_cast(float4, ks_ld4(xr, g2_rec_dx(BM) + 16 * h, xo));
         }
     };
     v4f2_t y[NH][2];
@@ -338,121 +494,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmks_kernel(GKSArgs A) {
     for (int h = 0; h < NH; h++)
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) y[h][nt] = (v4f2_t){0.0f, 0.0f, 0.0f, 0.0f};
-    // the weight operand of K-step ks, n tile nt: dword i holds slots 4 i .. 4 i + 3
-    auto operand = [&](const WStage &s, int ks, int nt) -> v4i2_t {
-        const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u, m1 = 0x01010101u;
-        uint32_t q[4];
-        if constexpr (F::nib) {
-            const uint32_t w0 = nt ? s.qa[ks].z : s.qa[ks].x;
-            const uint32_t w1 = nt ? s.qa[ks].w : s.qa[ks].y;
-            q[0] = w0 & m4;
-            q[1] = w1 & m4;
-            q[2] = (w0 >> 4) & m4;
-            q[3] = (w1 >> 4) & m4;
-        } else {
-            const uint4 wv = s.qa[ks >> 1];
-            const uint32_t W = (ks & 1) ? (nt ? wv.w : wv.z) : (nt ? wv.y : wv.x);
-#pragma unroll
-            for (int t = 0; t < 4; t++) q[t] = (W >> (2 * t)) & m2;
-        }
-        if constexpr (FMT == T_Q6_K) {
-            const uint4 hv = s.qb[ks >> 1];
-            const uint32_t H = (ks & 1) ? (nt ? hv.w : hv.z) : (nt ? hv.y : hv.x);
-#pragma unroll
-            for (int t = 0; t < 4; t++) q[t] |= ((H >> (2 * t)) & m2) << 4;
-        }
-        if constexpr (FMT == T_Q5_K || FMT == T_Q3_K) {
-            const uint32_t Fw = ks == 0 ? s.qb[0].x : ks == 1 ? s.qb[0].y : ks == 2 ? s.qb[0].z : s.qb[0].w;
-            constexpr int pos = FMT == T_Q5_K ? 4 : 2;
-#pragma unroll
-            for (int t = 0; t < 4; t++) q[t] |= ((Fw >> (t + 4 * nt)) & m1) << pos;
-        }
-        // Q3_K: q - 4 (q + 124 < 256, bit 7 flipped); Q6_K: q - 32 (q + 96)
-        if constexpr (FMT == T_Q3_K) {
-#pragma unroll
-            for (int t = 0; t < 4; t++) q[t] = (q[t] + 0x7C7C7C7Cu) ^ 0x80808080u;
-        }
-        if constexpr (FMT == T_Q6_K) {
-#pragma unroll
-            for (int t = 0; t < 4; t++) q[t] = (q[t] + 0x60606060u) ^ 0x80808080u;
-        }
-        return (v4i2_t){(int)q[0], (int)q[1], (int)q[2], (int)q[3]};
-    };
-    // this lane's scale and min at K-step ks, n tile nt
-    auto scale = [&](const WStage &s, int ks, int nt, int &sv, int &mv) {
-        if constexpr (F::unit32) {  // unit 2 ks + g / 2 at byte ks
-            sv = (int)((s.sc[nt][0] >> (8 * ks)) & 0xffu);
-            mv = (int)((s.sc[nt][1] >> (8 * ks)) & 0xffu);
-        } else if constexpr (FMT == T_Q2_K) {  // group 4 ks + g at byte ks
-            const uint32_t b = (s.sc[nt][0] >> (8 * ks)) & 0xffu;
-            sv = (int)(b & 15u);
-            mv = (int)(b >> 4);
-        } else {
-            sv = sbfe8(s.sc[nt][0], 8u * (uint32_t)ks);
-            mv = 0;
-        }
-    };
-    auto compute = [&](const WStage &s, const XStage &x) {
-        v4i2_t S[NH][2], T[NH][2];
-#pragma unroll
-        for (int h = 0; h < NH; h++)
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                S[h][nt] = (v4i2_t){0, 0, 0, 0};
-                T[h][nt] = (v4i2_t){0, 0, 0, 0};
-            }
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            v4i2_t am[NH];
-#pragma unroll
-            for (int h = 0; h < NH; h++) am[h] = __builtin_bit_cast(v4i2_t, x.a[h][ks]);
-            v4i2_t P1[NH];
-            if constexpr (F::mins) {
-                const v4i2_t ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-                const v4i2_t z = {0, 0, 0, 0};
-#pragma unroll
-                for (int h = 0; h < NH; h++) P1[h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[h], ones, z, 0, 0, 0);
-            }
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                const v4i2_t b = operand(s, ks, nt);
-                int sv, mv;
-                scale(s, ks, nt, sv, mv);
-#pragma unroll
-                for (int h = 0; h < NH; h++) {
-                    const v4i2_t z = {0, 0, 0, 0};
-                    const v4i2_t P = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[h], b, z, 0, 0, 0);
-                    // |P|, |P1| < 2^17 and |s|, |m| <= 128: 24-bit products
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        S[h][nt][i] += __mul24(sv, P[i]);
-                        if constexpr (F::mins) T[h][nt][i] += __mul24(mv, P1[h][i]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            // mins formats: d in the low, dmin in the high half; Q3_K, Q6_K:
-            // the word of rows 2 (r16 / 2), + 1
-            const uint32_t dword = s.d[nt];
-            const float dw = half_to_float(F::mins ? (dword & 0xffffu) : (dword >> (16 * (r16 & 1))) & 0xffffu);
-            const float ndm = F::mins ? -half_to_float(dword >> 16) : 0.0f;
-#pragma unroll
-            for (int h = 0; h < NH; h++) {
-                const float dxv[4] = {x.dx[h].x, x.dx[h].y, x.dx[h].z, x.dx[h].w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    if constexpr (F::mins) {
-                        const float u = fma_f32(dw, (float)S[h][nt][i], ndm * (float)T[h][nt][i]);
-                        y[h][nt][i] = fma_f32(dxv[i], u, y[h][nt][i]);
-                    } else {
-                        y[h][nt][i] = fma_f32(dxv[i] * dw, (float)S[h][nt][i], y[h][nt][i]);
-                    }
-                }
-            }
-        }
-    };
+    auto compute = [&](const WStage &s, const XStage &x) { ks_compute<FMT, NH>(s, x, r16, y); };
     // rings of register sets: super-block c computes from weight set j %
     // SW and activation set j % 2 while the weights of the next SW - 1
     // super-blocks of this wave (from HBM) and the activations of the next
@@ -517,19 +559,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmks_kernel(GKSArgs A) {
             }
         }
     }
-    // add the 4 lane groups (each holds the sums over its own slots):
-    // partners l ^ 16, then l ^ 32, the same order in every lane
-#pragma unroll
-    for (int h = 0; h < NH; h++)
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float v = y[h][nt][i];
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
-                y[h][nt][i] = v;
-            }
+    ks_add_groups<NH>(y);
     if (wave > 0) {
 #pragma unroll
         for (int h = 0; h < NH; h++)

@@ -24,6 +24,7 @@
 #include "gemm2.h"
 #include "gemm2s.h"
 #include "gemmks.h"
+#include "gemmkf.h"
 #include "gemm6.h"
 #include "gemmh.h"
 #include "gemmq.h"
@@ -53,6 +54,8 @@ struct Options {
     int64_t gemmks_max_m = -1; // largest M on the small-M K-quant GEMM, 0: none (rule: 16)
     int64_t gemmks_q4k = -1;   // Q4_K small M on gemmks.h (1) or gemm2s.h (0) (rule: 0)
     int64_t gemms_waves = -1;  // waves per workgroup of the small-M GEMMs, 4 or 8 (rule: by rows)
+    int64_t gemmkf_max_m = -1; // largest M on the fused small-M K-quant launch, 0: none (rule: 8)
+    int64_t gemmkf_sbk = -1;   // its K-slice length in super-blocks, 0: fewest slices (rule: by tiles)
     int64_t q80_scalar = -1;   // Q8_0 activations by the scalar quantizer (reference
                                // kernels.c:542-558, its SI_SCALAR mode), 1: on (rule: off)
 };
@@ -73,6 +76,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM2S_MAX_M", &Options::gemm2s_max_m}, {"GEMMKS_MAX_M", &Options::gemmks_max_m},
     {"GEMMKS_Q4K", &Options::gemmks_q4k},
     {"GEMMS_WAVES", &Options::gemms_waves},
+    {"GEMMKF_MAX_M", &Options::gemmkf_max_m}, {"GEMMKF_SBK", &Options::gemmkf_sbk},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -976,6 +980,11 @@ static int build_gemm2_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
 }
 
 static int64_t gemmks_max_m(const Options &o, uint32_t type);
+// Largest M on the fused small-M K-quant launch (gemmkf.h, at most
+// kKFMaxM); option GEMMKF_MAX_M, 0 turns it off.
+static int64_t gemmkf_max_m(const Options &o) {
+    return o.gemmkf_max_m >= 0 ? (o.gemmkf_max_m < kKFMaxM ? o.gemmkf_max_m : kKFMaxM) : kKFMaxM;
+}
 
 // The near-GGUF-size K-quant copy of the small-M GEMM (gemmks.h).
 static int build_gemmks_copy(sihip_ctx *ctx, sihip_weight *w, hipStream_t st) {
@@ -1023,8 +1032,10 @@ extern "C" int sihip_weight_prepare_gemm(sihip_ctx *ctx, sihip_weight *w) {
         const int rc = build_gemm2_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
-    if (is_kquant(w->L.type) && gemmks_max_m(ctx->opt, w->L.type) > 0 && !w->gsmall &&
-        !(w->L.type == T_Q4_K && ctx->opt.gemmks_q4k != 1)) {
+    if (is_kquant(w->L.type) && !w->gsmall &&
+        (gemmkf_max_m(ctx->opt) > 0 ||
+         (gemmks_max_m(ctx->opt, w->L.type) > 0 &&
+          !(w->L.type == T_Q4_K && ctx->opt.gemmks_q4k != 1)))) {
         const int rc = build_gemmks_copy(ctx, w, ctx->stream);
         if (rc) return rc;
     }
@@ -1647,12 +1658,195 @@ static int build_plan_copy(sihip_ctx *ctx, sihip_weight *w, const GemmPlan &p, h
     return p.v2 ? build_gemm2_copy(ctx, w, st) : build_gemm_copy(ctx, w, st);
 }
 
+// ---- the fused small-M K-quant launch (gemmkf.h) ------------------------------
+
+template <uint32_t F0, uint32_t F1>
+static void launch_gemmkf_nh(int nh, dim3 grid, size_t lds, hipStream_t st, const GKFArgs &A) {
+    if (nh == 1)
+        hipLaunchKernelGGL((gemmkf_kernel<F0, F1, 1>), grid, dim3(kKFThreads), lds, st, A);
+    else
+        hipLaunchKernelGGL((gemmkf_kernel<F0, F1, 2>), grid, dim3(kKFThreads), lds, st, A);
+}
+
+// The instances: one format, or the pairs of the K-quant mixes whose
+// matrices share an activation (Q4_K_M and Q5_K_M put Q6_K beside Q4_K or
+// Q5_K, Q3_K_M Q5_K beside Q3_K, Q2_K Q3_K beside Q2_K). false: no instance.
+static bool launch_gemmkf(uint32_t t0, uint32_t t1, int nh, dim3 grid, size_t lds, hipStream_t st,
+                          const GKFArgs &A) {
+    if (t0 > t1) std::swap(t0, t1);
+    if (t0 == t1) {
+        switch (t0) {
+            case T_Q2_K: launch_gemmkf_nh<T_Q2_K, T_Q2_K>(nh, grid, lds, st, A); return true;
+            case T_Q3_K: launch_gemmkf_nh<T_Q3_K, T_Q3_K>(nh, grid, lds, st, A); return true;
+            case T_Q4_K: launch_gemmkf_nh<T_Q4_K, T_Q4_K>(nh, grid, lds, st, A); return true;
+            case T_Q5_K: launch_gemmkf_nh<T_Q5_K, T_Q5_K>(nh, grid, lds, st, A); return true;
+            case T_Q6_K: launch_gemmkf_nh<T_Q6_K, T_Q6_K>(nh, grid, lds, st, A); return true;
+            default: return false;
+        }
+    }
+    static_assert(T_Q2_K < T_Q3_K && T_Q3_K < T_Q4_K && T_Q4_K < T_Q5_K && T_Q5_K < T_Q6_K,
+                  "pairs below are listed in type order");
+    if (t0 == T_Q4_K && t1 == T_Q6_K) launch_gemmkf_nh<T_Q4_K, T_Q6_K>(nh, grid, lds, st, A);
+    else if (t0 == T_Q5_K && t1 == T_Q6_K) launch_gemmkf_nh<T_Q5_K, T_Q6_K>(nh, grid, lds, st, A);
+    else if (t0 == T_Q3_K && t1 == T_Q5_K) launch_gemmkf_nh<T_Q3_K, T_Q5_K>(nh, grid, lds, st, A);
+    else if (t0 == T_Q2_K && t1 == T_Q3_K) launch_gemmkf_nh<T_Q2_K, T_Q3_K>(nh, grid, lds, st, A);
+    else return false;
+    return true;
+}
+
+// Whether weights over one X take the fused launch: K-quants of one row
+// length, M on the matrix cores and at most gemmkf_max_m.
+static bool gemmkf_eligible(const sihip_ctx *ctx, int count, const sihip_weight *const *w,
+                            int64_t M) {
+    if (count < 1 || M < gemm_min_m(ctx->opt) || M > gemmkf_max_m(ctx->opt)) return false;
+    for (int i = 0; i < count; i++)
+        if (!is_kquant(w[i]->L.type) || w[i]->L.n_in != w[0]->L.n_in || w[i]->L.n_in % 256)
+            return false;
+    return true;
+}
+
+// Tiles of one segment: kKFWaves 32-row blocks each.
+static int64_t gemmkf_tiles(const Layout &L) {
+    return ((L.n_out + 31) / 32 + kKFWaves - 1) / kKFWaves;
+}
+
+// K slices of a fused launch over `tiles` tiles: as many as keep the grid
+// within two workgroups per CU, at least two super-blocks each (a slice's
+// fixed cost, its partial sums and the last workgroup's sum, outweighs one
+// super-block: Llama-3-8B wo 4096 x 4096 at M = 8 takes 13.0 us per call in
+// 16 slices of one, 9.7 in 8 of two, 10.6 in 4 of four), and at most
+// kKFMaxSBK super-blocks per slice (its LDS image); the GEMMKF_SBK option
+// sets the slice length (0: the fewest slices).
+static void gemmkf_slices(const sihip_ctx *ctx, int64_t tiles, int64_t nb, int &S, int &SBK) {
+    int64_t s = 2 * (int64_t)ctx->n_cu / (tiles > 0 ? tiles : 1);
+    if (s < 1) s = 1;
+    if (s > (nb + 1) / 2) s = (nb + 1) / 2;
+    int64_t sbk = (nb + s - 1) / s;
+    if (ctx->opt.gemmkf_sbk == 0) sbk = nb;
+    else if (ctx->opt.gemmkf_sbk > 0) sbk = ctx->opt.gemmkf_sbk;
+    if (sbk > kKFMaxSBK) sbk = kKFMaxSBK;
+    if (sbk > nb) sbk = nb;
+    SBK = (int)sbk;
+    S = (int)((nb + sbk - 1) / sbk);
+}
+
+// One fused launch (every weight's gemmks.h copy exists, at most two
+// formats with an instance, count <= kKFMaxSegs); the partial sums and
+// counters were sized by the caller.
+static int launch_gemmkf_group(sihip_ctx *ctx, int count, const sihip_weight *const *w,
+                               const float *X, int64_t M, float *const *Y, float *part,
+                               uint32_t *cnt, hipStream_t st, bool &done) {
+    done = false;
+    const int64_t nb = w[0]->L.n_in / 256;
+    int64_t tiles = 0;
+    for (int i = 0; i < count; i++) tiles += gemmkf_tiles(w[i]->L);
+    int S, SBK;
+    gemmkf_slices(ctx, tiles, nb, S, SBK);
+    GKFArgs A{};
+    A.x = X;
+    A.ldx = w[0]->L.n_in;
+    A.M = M;
+    A.nb = (int)nb;
+    A.nseg = count;
+    uint32_t t0 = w[0]->L.type, t1 = t0;
+    int64_t wg = 0, pofs = 0, cofs = 0;
+    for (int i = 0; i < count; i++) {
+        const Layout &L = w[i]->L;
+        if (L.type != t0) {
+            if (t1 != t0 && L.type != t1) return SIHIP_OK;  // a third format: not done
+            t1 = L.type;
+        }
+        GKFSeg &g = A.seg[i];
+        g.w = w[i]->gsmall;
+        g.y = Y[i];
+        g.ldy = L.n_out;
+        g.n_out = L.n_out;
+        g.type = L.type;
+        g.nblk = (int)((L.n_out + 31) / 32);
+        g.ntile = (int)gemmkf_tiles(L);
+        g.S = S;
+        g.SBK = SBK;
+        g.wg0 = (int)wg;
+        g.part = S > 1 ? part + pofs : nullptr;
+        g.cnt = S > 1 ? cnt + cofs : nullptr;
+        wg += (int64_t)g.ntile * S;
+        pofs += (int64_t)S * kKFMp * g.ntile * kKFRows;
+        cofs += g.ntile;
+    }
+    const size_t lds = (size_t)SBK * kKFRec;
+    if (!launch_gemmkf(t0, t1, (int)((M + 3) / 4), dim3((unsigned)wg), lds, st, A)) return SIHIP_OK;
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+    done = true;
+    return SIHIP_OK;
+}
+
+// Weights over one X on the fused launch: one launch for all of them where
+// their formats have an instance, else one per format (each quantizes X
+// itself). Copies are built on first use and the partial sums grown as
+// needed (outside graph capture).
+static int run_gemmkf(sihip_ctx *ctx, int count, const sihip_weight *const *wc, const float *X,
+                      int64_t M, float *const *Y, hipStream_t st) {
+    const int64_t nb = wc[0]->L.n_in / 256;
+    size_t part = 0;
+    int64_t counters = 0;
+    for (int i = 0; i < count; i++) {
+        sihip_weight *w = const_cast<sihip_weight *>(wc[i]);  // the GEMM copies are caches of w
+        if (!w->gsmall) {
+            const int rc = build_gemmks_copy(ctx, w, st);
+            if (rc) return rc;
+        }
+    }
+    // partial sums: a segment's slices in any launch are at most those of a
+    // launch of that segment alone (fewer tiles, more slices)
+    for (int i = 0; i < count; i++) {
+        const int64_t t = gemmkf_tiles(wc[i]->L);
+        int S, SBK;
+        gemmkf_slices(ctx, t, nb, S, SBK);
+        part += (size_t)S * kKFMp * t * kKFRows * sizeof(float);
+        counters += t;
+    }
+    if (counters > kGemmCounters)
+        return set_err(ctx, SIHIP_EINVAL, "gemm: %lld output tiles exceed the %lld counters",
+                       (long long)counters, (long long)kGemmCounters);
+    int rc = ensure(ctx, &ctx->d_gpart, &ctx->d_gpart_cap, part, st);
+    if (rc) return rc;
+    rc = order_before(ctx, ctx->order, st);
+    if (rc) return rc;
+    bool done = false;
+    rc = launch_gemmkf_group(ctx, count, wc, X, M, Y, (float *)ctx->d_gpart, ctx->d_gcnt, st, done);
+    if (rc) return rc;
+    if (!done) {  // one launch per format
+        bool used[kKFMaxSegs] = {};
+        for (int i = 0; i < count; i++) {
+            if (used[i]) continue;
+            const sihip_weight *gw[kKFMaxSegs];
+            float *gy[kKFMaxSegs];
+            int n = 0;
+            for (int j = i; j < count; j++)
+                if (!used[j] && wc[j]->L.type == wc[i]->L.type) {
+                    used[j] = true;
+                    gw[n] = wc[j];
+                    gy[n] = Y[j];
+                    n++;
+                }
+            rc = launch_gemmkf_group(ctx, n, gw, X, M, gy, (float *)ctx->d_gpart, ctx->d_gcnt, st,
+                                     done);
+            if (rc) return rc;
+            if (!done) return set_err(ctx, SIHIP_EINVAL, "gemm: no fused instance for a format");
+        }
+    }
+    return order_after(ctx, ctx->order, st);
+}
+
 // The MFMA GEMM on the context's workspaces (grown as needed, outside
 // graph capture) and the weight's GEMM copy (built on first use). The
 // activation planes live in the context, so calls on one context must not
 // overlap.
 static int run_gemm_mfma(sihip_ctx *ctx, const sihip_weight *wc, const float *X, int64_t ldx,
                          int64_t M, float *Y, int64_t ldy, hipStream_t st) {
+    if (ldx == wc->L.n_in && ldy == wc->L.n_out && gemmkf_eligible(ctx, 1, &wc, M))
+        return run_gemmkf(ctx, 1, &wc, X, M, &Y, st);
     sihip_weight *w = const_cast<sihip_weight *>(wc);  // the GEMM copies are caches of w
     const GemmPlan p = plan_gemm(ctx, w->L, M);
     int rc = build_plan_copy(ctx, w, p, st);
@@ -1696,6 +1890,8 @@ static XKey xkey(const Layout &L, const GemmPlan &p) {
 // launches after the first of a layout read its planes.
 static int run_gemm_multi(sihip_ctx *ctx, int count, const sihip_weight *const *wc,
                           const float *X, int64_t M, float *const *Y, hipStream_t st) {
+    if (count <= kKFMaxSegs && gemmkf_eligible(ctx, count, wc, M))
+        return run_gemmkf(ctx, count, wc, X, M, Y, st);
     GemmPlan plan[kMaxSegs];
     XKey key[kMaxSegs];
     for (int i = 0; i < count; i++) {
@@ -1904,12 +2100,34 @@ extern "C" int sihip_gemm_dev_noalloc(sihip_ctx *ctx, const sihip_weight *w, con
     const hipStream_t st = (hipStream_t)stream;
     if (!gemm_on_mfma(ctx, w, M))
         return run_matvec(ctx, w, X, w->L.n_in, nullptr, 0, M, Y, w->L.n_out, w->L.n_out, st);
+    const size_t room = kNoAllocBytes - kNoAllocCntBytes;
+    if (gemmkf_eligible(ctx, 1, &w, M)) {
+        // the fused small-M launch: its partial sums from offset 0
+        if (!w->gsmall)
+            return set_err(ctx, SIHIP_EINVAL,
+                           "gemm_dev_noalloc: the weight has no GEMM copy; call "
+                           "sihip_weight_prepare_gemm first");
+        const int64_t t = gemmkf_tiles(w->L);
+        int S, SBK;
+        gemmkf_slices(ctx, t, w->L.n_in / 256, S, SBK);
+        const size_t part = (size_t)S * kKFMp * t * kKFRows * sizeof(float);
+        if (part > room)
+            return set_err(ctx, SIHIP_ERANGE,
+                           "gemm_dev_noalloc: %lld output rows in %d K slices need %zu bytes of "
+                           "partial sums; the static scratch holds %zu",
+                           (long long)w->L.n_out, S, part, room);
+        bool done = false;
+        float *Yp = Y;
+        const int rc = launch_gemmkf_group(ctx, 1, &w, X, M, &Yp, (float *)ctx->scratch,
+                                           (uint32_t *)(ctx->scratch + room), st, done);
+        if (rc) return rc;
+        return done ? SIHIP_OK : set_err(ctx, SIHIP_EINVAL, "gemm_dev_noalloc: no fused instance");
+    }
     GemmPlan p = plan_gemm(ctx, w->L, M);
     if (!plan_copy(w, p))
         return set_err(ctx, SIHIP_EINVAL,
                        "gemm_dev_noalloc: the weight has no GEMM copy; call "
                        "sihip_weight_prepare_gemm first");
-    const size_t room = kNoAllocBytes - kNoAllocCntBytes;
     if ((size_t)p.ws_bytes > room)
         return set_err(ctx, SIHIP_ERANGE,
                        "gemm_dev_noalloc: M = %lld x n_in = %lld needs %lld bytes of activation "

@@ -1,12 +1,14 @@
-"""GPU parity of the small-M GEMMs (the batched decode step): gemm2s_q4k_kernel
-(Q4_K, 3 <= M <= 16) and gemmks_kernel (Q2_K, Q5_K up to M = 8, Q3_K, Q6_K up
-to M = 12, by option every K-quant up to 16) against the oracle, every
-output, |gpu - ref| <= 1e-5 * sum|terms| + 1e-6; the M values past a
-format's rule run its larger GEMM. Shapes cover a single super-block per row (fewer super-blocks than
+"""GPU parity of the small-M GEMMs (the batched decode step): the fused
+launch gemmkf_kernel (every K-quant, 3 <= M <= 8, the rule), and with it
+turned off (GEMMKF_MAX_M = 0) gemm2s_q4k_kernel (Q4_K, 3 <= M <= 16) and
+gemmks_kernel (Q2_K, Q5_K up to M = 8, Q3_K, Q6_K up to M = 12, by option
+every K-quant up to 16) against the oracle, every output, |gpu - ref| <=
+1e-5 * sum|terms| + 1e-6; the M values past a format's rule run its larger
+GEMM. Shapes cover a single super-block per row (fewer super-blocks than
 waves per workgroup), super-block counts that the waves do not divide,
 row counts that leave a 32-row block part empty, every 4-row activation
-group count (M = 3 to 16), each waves-per-workgroup choice, and
-rows at the ends of each format's operand range."""
+group count (M = 3 to 16), each waves-per-workgroup choice, and rows at
+the ends of each format's operand range."""
 import numpy as np
 import pytest
 
@@ -50,14 +52,20 @@ def _check(dev, oracle, wt, n_out, n_in, M, seed, what):
 @pytest.mark.parametrize("wt", KQ, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 12, 16])
 @pytest.mark.parametrize("n_out,n_in", [(33, 256), (200, 1024), (96, 2304)])
-def test_small_m_vs_oracle(dev, oracle, wt, M, n_out, n_in):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "separate"])
+def test_small_m_vs_oracle(dev, oracle, option, wt, M, n_out, n_in, fused):
+    if fused and M > 8:
+        pytest.skip("the fused launch takes M <= 8; the separate case covers this M")
+    if not fused:
+        option("GEMMKF_MAX_M", 0)
     _check(dev, oracle, wt, n_out, n_in, M, 7000 + 97 * wt + 13 * M + n_in,
-           f"{sa.NAMES[wt]} {n_out}x{n_in} M={M}")
+           f"{sa.NAMES[wt]} {n_out}x{n_in} M={M} {'fused' if fused else 'separate'}")
 
 
 @pytest.mark.parametrize("wt", KQ, ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("waves", [2, 4, 8])
 def test_small_m_waves_per_workgroup(dev, oracle, option, wt, waves):
+    option("GEMMKF_MAX_M", 0)
     option("GEMMS_WAVES", waves)
     _check(dev, oracle, wt, 160, 2560, 8, 7100 + wt + waves, f"{sa.NAMES[wt]} waves={waves}")
 
@@ -77,15 +85,19 @@ def test_small_m_wide_groups_by_option(dev, oracle, option, wt, M):
 def test_small_m_q4k_on_the_generic_kernel(dev, oracle, option, M):
     """Q4_K at small M on gemmks.h (the GEMMKS_Q4K option) as well as on
     gemm2s.h (the rule)."""
+    option("GEMMKF_MAX_M", 0)
     option("GEMMKS_Q4K", 1)
     _check(dev, oracle, sa.Q4_K, 200, 1024, M, 7200 + M, f"Q4_K gemmks M={M}")
 
 
-def test_small_m_graph_replays_match_eager(dev):
-    """A captured small-M call (Q4_K on gemm2s.h, Q6_K and Q3_K on gemmks.h)
-    replays bit-identically to the eager call, several times with eager
-    calls in between."""
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "separate"])
+def test_small_m_graph_replays_match_eager(dev, option, fused):
+    """A captured small-M call (the fused launch, or Q4_K on gemm2s.h, Q6_K
+    and Q3_K on gemmks.h) replays bit-identically to the eager call,
+    several times with eager calls in between."""
     from .test_gpu_slices import _HipGraph, bits
+    if not fused:
+        option("GEMMKF_MAX_M", 0)
     rng = np.random.default_rng(7300)
     n_out, n_in, M = 4096, 4096, 8
     ws = [dev.upload(wt, n_out, n_in, synth.make_weights(wt, n_out, n_in, rng))
