@@ -209,6 +209,54 @@ __device__ inline void kf_compute_u2(const KSWStage<FMT> &s, const uint4 (&a)[4]
     }
 }
 
+// One super-block for Q2_K, whose 2-bit quant times its 4-bit group scale
+// fits an int8 (q s <= 45): the scale is folded into the weight operand
+// (one 32-bit multiply per operand dword: bytes below 256, no carries) and
+// the activation operand is not masked, so the MFMAs accumulate the scaled
+// sums over the whole super-block themselves, for up to 16 activation rows:
+//   S = sum_ks MFMA(x_ks, q s),  T = sum_ks MFMA(x_ks, m)   (exact integers)
+// with m the lane's group min in all 16 of its slots. Result register i of
+// lane l is complete for activation row 4 (l / 16) + i; rows 8..15 are
+// zeros here (M <= 8). y[nt][i] += dx_i * (d * S - dmin * T).
+__device__ inline void kf_compute_fold(const KSWStage<T_Q2_K> &s, const uint4 (&a)[4], float4 dx,
+                                       v4f2_t (&y)[2]) {
+    v4i2_t S[2], T[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        S[nt] = (v4i2_t){0, 0, 0, 0};
+        T[nt] = (v4i2_t){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const v4i2_t am = __builtin_bit_cast(v4i2_t, a[ks]);
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const v4i2_t q = ks_operand<T_Q2_K>(s, ks, nt);
+            // group 4 ks + g at byte ks: the scale in the low, the min in
+            // the high nibble
+            const uint32_t b = (s.sc[nt][0] >> (8 * ks)) & 0xffu;
+            const uint32_t sv = b & 15u;
+            const int mb = (int)((b >> 4) * 0x01010101u);
+            const v4i2_t qs = {(int)((uint32_t)q[0] * sv), (int)((uint32_t)q[1] * sv),
+                               (int)((uint32_t)q[2] * sv), (int)((uint32_t)q[3] * sv)};
+            S[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qs, S[nt], 0, 0, 0);
+            T[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, (v4i2_t){mb, mb, mb, mb}, T[nt], 0, 0, 0);
+        }
+    }
+    const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        const uint32_t dword = s.d[nt];  // d in the low, dmin in the high half
+        const float dw = half_to_float(dword & 0xffffu);
+        const float ndm = -half_to_float(dword >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float u = fma_f32(dw, (float)S[nt][i], ndm * (float)T[nt][i]);
+            y[nt][i] = fma_f32(dxv[i], u, y[nt][i]);
+        }
+    }
+}
+
 // The workgroup's share of segment sg: tile t % ntile, slice t / ntile.
 template <uint32_t FMT, int NH>
 __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_t *lds) {
@@ -237,11 +285,13 @@ __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     // unit-scale formats: the two-way masked operand of all 8 rows (one
-    // result tile per n tile); the others: gemmks.h's four-way masked
-    // operand of 4 rows per MFMA, NH of them
+    // result tile per n tile); Q2_K: the unmasked operand (scales folded
+    // into the weights); the others: gemmks.h's four-way masked operand of
+    // 4 rows per MFMA, NH of them
     constexpr bool U2 = F::unit32;
-    constexpr int YH = U2 ? 1 : NH;
-    kf_prologue<U2 ? 8 : 4 * NH>(A, c0, c1 - c0, xf, lds);
+    constexpr bool FOLD = FMT == T_Q2_K;
+    constexpr int YH = U2 || FOLD ? 1 : NH;
+    kf_prologue<U2 || FOLD ? 8 : 4 * NH>(A, c0, c1 - c0, xf, lds);
     __syncthreads();
 
     v4f2_t y[YH][2];
@@ -251,8 +301,9 @@ __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_
         for (int nt = 0; nt < 2; nt++) y[h][nt] = (v4f2_t){0.0f, 0.0f, 0.0f, 0.0f};
     // four-way (gemmks.h): lane l carries row 4 h + l % 4 of lane group
     // l / 16's K slots when l % 16 / 4 == l / 16, else zeros; two-way: row
-    // l % 8 when l % 16 / 8 == l / 32, else zeros
-    const bool own = U2 ? (r16 >> 3) == (g >> 1) : (r16 >> 2) == g;
+    // l % 8 when l % 16 / 8 == l / 32, else zeros; unmasked: row l % 16
+    // (zeros past row 7)
+    const bool own = FOLD ? r16 < 8 : U2 ? (r16 >> 3) == (g >> 1) : (r16 >> 2) == g;
     auto load_x = [&](int c, KSXStage<NH> &x) {
         const uint8_t *R = lds + (c - c0) * kKFRec;
 #pragma unroll
@@ -274,6 +325,16 @@ __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_
         }
         dx = *reinterpret_cast<const float4 *>(R + kKFDx + 16 * (g & 1));
     };
+    auto load_x1 = [&](int c, uint4 (&a)[4], float4 &dx) {
+        const uint8_t *R = lds + (c - c0) * kKFRec;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(R + kf_q_off(ks, g, r16 & 7));
+            a[ks] = own ? v : make_uint4(0, 0, 0, 0);
+        }
+        // rows 4 g .. 4 g + 3 (lane groups 2 and 3 hold padding rows)
+        dx = *reinterpret_cast<const float4 *>(R + kKFDx + 16 * (g & 1));
+    };
     if (has) {
         for (int cb = c0; cb < c1; cb += SW) {
 #pragma unroll
@@ -283,7 +344,12 @@ __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_
                 asm volatile("" ::: "memory");
                 __builtin_amdgcn_sched_barrier(0);
                 if (c < c1) {
-                    if constexpr (U2) {
+                    if constexpr (FOLD) {
+                        uint4 a[4];
+                        float4 dx;
+                        load_x1(c, a, dx);
+                        kf_compute_fold(ws[j % SW], a, dx, y[0]);
+                    } else if constexpr (U2) {
                         uint4 a[4];
                         float4 dx;
                         load_x2(c, a, dx);
@@ -296,7 +362,9 @@ __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_
                 }
             }
         }
-        if constexpr (U2) {  // the two units of a K-step: lanes l and l ^ 32
+        if constexpr (FOLD) {
+            // complete in every lane
+        } else if constexpr (U2) {  // the two units of a K-step: lanes l and l ^ 32
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
 #pragma unroll
@@ -307,10 +375,10 @@ __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_
     }
     // activation row of result i of y[h]: four-way, lane group h holds rows
     // 4 h .. 4 h + 3 (every lane group has them after the additions);
-    // two-way, lane groups 0 and 1 hold rows 0..3 and 4..7
+    // two-way and unmasked, lane groups 0 and 1 hold rows 0..3 and 4..7
     const int64_t n0 = (int64_t)blk * 32;
-    auto holds = [&](int h) { return U2 ? g < 2 : g == h; };
-    auto row_of = [&](int h, int i) { return U2 ? 4 * (g & 1) + i : 4 * h + i; };
+    auto holds = [&](int h) { return U2 || FOLD ? g < 2 : g == h; };
+    auto row_of = [&](int h, int i) { return U2 || FOLD ? 4 * (g & 1) + i : 4 * h + i; };
     if (sg.S == 1) {
         if (has) {
 #pragma unroll

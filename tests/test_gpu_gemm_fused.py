@@ -27,6 +27,14 @@ pytestmark = pytest.mark.gpu
 KQ = [sa.Q2_K, sa.Q3_K, sa.Q4_K, sa.Q5_K, sa.Q6_K]
 
 
+@pytest.fixture(autouse=True)
+def _fused_for_every_format(option):
+    """GEMMKF_MAX_M set explicitly: every K-quant takes the fused launch,
+    Q3_K with short rows included (the rule sends those to the separate
+    launches)."""
+    option("GEMMKF_MAX_M", 8)
+
+
 def _multi(dev, ws, X):
     M = X.shape[0]
     xd = dev.to_device(X)

@@ -56,8 +56,7 @@ def _check(dev, oracle, wt, n_out, n_in, M, seed, what):
 def test_small_m_vs_oracle(dev, oracle, option, wt, M, n_out, n_in, fused):
     if fused and M > 8:
         pytest.skip("the fused launch takes M <= 8; the separate case covers this M")
-    if not fused:
-        option("GEMMKF_MAX_M", 0)
+    option("GEMMKF_MAX_M", 8 if fused else 0)
     _check(dev, oracle, wt, n_out, n_in, M, 7000 + 97 * wt + 13 * M + n_in,
            f"{sa.NAMES[wt]} {n_out}x{n_in} M={M} {'fused' if fused else 'separate'}")
 
@@ -96,8 +95,7 @@ def test_small_m_graph_replays_match_eager(dev, option, fused):
     and Q3_K on gemmks.h) replays bit-identically to the eager call,
     several times with eager calls in between."""
     from .test_gpu_slices import _HipGraph, bits
-    if not fused:
-        option("GEMMKF_MAX_M", 0)
+    option("GEMMKF_MAX_M", 8 if fused else 0)
     rng = np.random.default_rng(7300)
     n_out, n_in, M = 4096, 4096, 8
     ws = [dev.upload(wt, n_out, n_in, synth.make_weights(wt, n_out, n_in, rng))
