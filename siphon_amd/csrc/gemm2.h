@@ -201,21 +201,30 @@ __global__ __launch_bounds__(256) void gemm2_layout_q4k(Layout L, const uint8_t 
 
 // ---- the GEMM -----------------------------------------------------------------
 
-struct G2Args {
+// One matrix of a launch: several Q4_K matrices over one X (q and k, gate
+// and up) share a grid, their n blocks one after another.
+constexpr int kG2MaxSegs = 4;
+struct G2Seg {
     const uint8_t *w;     // weight chunks [nblk32][nb]
-    const uint8_t *x;     // activation records [MB][nb]
     float *y;             // Y[m * ldy + n]
-    int64_t ldy;
-    int64_t n_out, M, Mp;
-    int nb, MB, NB;       // super-blocks; m blocks of BM rows; n blocks of 128 rows
+    int64_t ldy, n_out;
     float yscale;         // 2^-E
+    int nb0;              // the segment's first n block in the grid
+};
+
+struct G2Args {
+    const uint8_t *x;     // activation records [MB][nb]
+    int64_t M, Mp;
+    int nb, MB, NB;       // super-blocks; m blocks of BM rows; n blocks of 128 rows (all segments)
     // K slices: S == 1, one workgroup per output tile; S > 1, slice s covers
     // super-blocks [s SBK, (s + 1) SBK) and its partial sums (already scaled
-    // by 2^-E) go to part[(s Mp + m) * NB * 128 + n], the tile's arrivals to
-    // cnt[mblk * NB + nblk] (zero between launches)
+    // by 2^-E) go to part[(s Mp + m) * NB * 128 + 128 nblk + n % 128], the
+    // tile's arrivals to cnt[mblk * NB + nblk] (zero between launches)
     int S, SBK;
     float *part;
     uint32_t *cnt;
+    int nseg;
+    G2Seg seg[kG2MaxSegs];
 };
 
 // q * f bytewise for bytes and products below 256 (no carries between
@@ -250,6 +259,15 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     const int nblk = (t / per) * 8 + xcd, rest = t % per;
     const int slice = rest / A.MB, mblk = rest % A.MB;
     if (nblk >= A.NB) return;
+    // the tile's segment, its fields read with constant indices (wave-
+    // uniform selects; a reference into the argument array at a computed
+    // index made the compiler keep the arguments in scratch memory, and
+    // the main loop spilled)
+    G2Seg sg = A.seg[0];
+#pragma unroll
+    for (int k = 1; k < kG2MaxSegs; k++)
+        if (k < A.nseg && nblk >= A.seg[k].nb0) sg = A.seg[k];
+    const int lblk = nblk - sg.nb0;  // n block within the segment's matrix
     const int c0 = slice * A.SBK;
     const int c1 = c0 + A.SBK < A.nb ? c0 + A.SBK : A.nb;  // this slice's super-blocks
     // wave index as a scalar: the buffer resources below derive from it
@@ -260,7 +278,7 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     // activation records: per-lane offsets are constants, the super-block
     // moves the scalar offset, so no address arithmetic runs on the VALU
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(A.w + (int64_t)(nblk * 4 + wave) * A.nb * kG2ChunkQ4K), (short)0,
+        (void *)(sg.w + (int64_t)(lblk * 4 + wave) * A.nb * kG2ChunkQ4K), (short)0,
         A.nb * kG2ChunkQ4K, 0x00020000);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(A.x + (int64_t)mblk * A.nb * kRec), (short)0, A.nb * kRec, 0x00020000);
@@ -394,10 +412,10 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     // result register i of lane l: row 4 (l / 16) + i of the m tile,
     // column l % 16 of the n tile; whole tiles inside M and n_out store
     // without per-element tests
-    const int64_t n0 = (int64_t)nblk * kG2BN + 32 * wave;
+    const int64_t n0 = (int64_t)lblk * kG2BN + 32 * wave;  // within the segment's matrix
     const int64_t m0 = (int64_t)mblk * BM;
     if (A.S == 1) {
-        const bool full = n0 + 32 <= A.n_out && m0 + BM <= A.M;
+        const bool full = n0 + 32 <= sg.n_out && m0 + BM <= A.M;
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
             const int64_t n = n0 + 16 * nt + r16;
@@ -406,15 +424,17 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int64_t m = m0 + 16 * mt + 4 * g + i;
-                    if (full || (m < A.M && n < A.n_out)) A.y[m * A.ldy + n] = y[mt][nt][i] * A.yscale;
+                    if (full || (m < A.M && n < sg.n_out)) sg.y[m * sg.ldy + n] = y[mt][nt][i] * sg.yscale;
                 }
         }
         return;
     }
     // K slices: partial sums through agent-scope stores (they write through
     // and are read past the per-XCD L2s), then the tile's arrival and the
-    // last workgroup's slice-order sum
+    // last workgroup's slice-order sum; the segment's columns of the
+    // partial-sum rows start at 128 nb0
     const int64_t ldp = (int64_t)A.NB * kG2BN;
+    float *const part = A.part + (int64_t)sg.nb0 * kG2BN;
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
         const int64_t n = n0 + 16 * nt + r16;
@@ -424,13 +444,13 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
             for (int i = 0; i < 4; i++) {
                 const int64_t m = m0 + 16 * mt + 4 * g + i;
                 if (m < A.M)
-                    __hip_atomic_store(A.part + ((int64_t)slice * A.Mp + m) * ldp + n,
-                                       y[mt][nt][i] * A.yscale, __ATOMIC_RELAXED,
+                    __hip_atomic_store(part + ((int64_t)slice * A.Mp + m) * ldp + n,
+                                       y[mt][nt][i] * sg.yscale, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
             }
     }
-    slices_finish<BM, kG2BN, kG2Threads>(A.part, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, A.Mp,
-                                         ldp, m0, A.M, (int64_t)nblk * kG2BN, A.n_out, A.y, A.ldy);
+    slices_finish<BM, kG2BN, kG2Threads>(part, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, A.Mp,
+                                         ldp, m0, A.M, (int64_t)lblk * kG2BN, sg.n_out, sg.y, sg.ldy);
 }
 
 }  // namespace sihip

@@ -56,6 +56,7 @@ struct Options {
     int64_t gemms_waves = -1;  // waves per workgroup of the small-M GEMMs, 4 or 8 (rule: by rows)
     int64_t gemmkf_max_m = -1; // largest M on the fused small-M K-quant launch, 0: none (rule: 8)
     int64_t gemmkf_sbk = -1;   // its K-slice length in super-blocks, 0: fewest slices (rule: by tiles)
+    int64_t gemm_group = -1;   // Q4_K matrices over one X in one 16x16 GEMM launch, 0: off (rule: on)
     int64_t q80_scalar = -1;   // Q8_0 activations by the scalar quantizer (reference
                                // kernels.c:542-558, its SI_SCALAR mode), 1: on (rule: off)
 };
@@ -77,6 +78,7 @@ static const OptionName kOptionNames[] = {
     {"GEMMKS_Q4K", &Options::gemmks_q4k},
     {"GEMMS_WAVES", &Options::gemms_waves},
     {"GEMMKF_MAX_M", &Options::gemmkf_max_m}, {"GEMMKF_SBK", &Options::gemmkf_sbk},
+    {"GEMM_GROUP", &Options::gemm_group},
 };
 
 // Order of launches that share mutable device state across streams: a
@@ -1292,32 +1294,41 @@ struct GemmBufs {
     int q80s = 0;  // the scalar Q8_0 quantizer (Q80_SCALAR option)
 };
 
-// Y[m, :] = W x[m, :] for m < M on the matrix cores, with the workspaces
-// in B (sized by plan_gemm); the weight's GEMM copy must exist.
+// Y_i[m, :] = W_i x[m, :] for m < M on the matrix cores, for `count` Q4_K
+// weights over one X in one grid (their n blocks one after another), with
+// the workspaces in B (sized by plan_gemm for their n blocks together); the
+// weights' GEMM copies must exist.
 template <int MT, int W>
-static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
-                               const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
-                               hipStream_t st) {
+static hipError_t launch_gemm2_multi(int count, const sihip_weight *const *w, const GemmPlan &p,
+                                     const GemmBufs &B, const float *X, int64_t ldx, int64_t M,
+                                     float *const *Y, const int64_t *ldy, hipStream_t st) {
     uint8_t *ws = B.ws;
     constexpr int BM = 16 * MT;
-    const Layout &L = w->L;
-    const int64_t nb = L.n_in / 256;
+    if (count < 1 || count > kG2MaxSegs) return hipErrorInvalidValue;
+    const int64_t nb = w[0]->L.n_in / 256;
     const int64_t blocks = p.Mp * nb;
     if (B.quant)
         hipLaunchKernelGGL(gemm2_quantize_x<BM>, dim3((unsigned)gemm2_quantize_grid(blocks)),
                            dim3(kG2Threads), 0, st, X, ldx, M, p.Mp, nb, ws);
-    G2Args A;
-    A.w = w->gemm2;
+    G2Args A{};
     A.x = ws;
-    A.y = Y;
-    A.ldy = ldy;
-    A.n_out = L.n_out;
     A.M = M;
     A.Mp = p.Mp;
     A.nb = (int)nb;
     A.MB = (int)(p.Mp / BM);
-    A.NB = (int)((L.n_out + kG2BN - 1) / kG2BN);
-    A.yscale = std::ldexp(1.0f, -w->gexp);
+    int NB = 0;
+    for (int i = 0; i < count; i++) {
+        G2Seg &g = A.seg[i];
+        g.w = w[i]->gemm2;
+        g.y = Y[i];
+        g.ldy = ldy[i];
+        g.n_out = w[i]->L.n_out;
+        g.yscale = std::ldexp(1.0f, -w[i]->gexp);
+        g.nb0 = NB;
+        NB += (int)((w[i]->L.n_out + kG2BN - 1) / kG2BN);
+    }
+    A.nseg = count;
+    A.NB = NB;
     A.S = p.S;
     A.SBK = p.SBK;
     A.part = p.S > 1 ? B.part : nullptr;
@@ -1325,6 +1336,13 @@ static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const G
     const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
     hipLaunchKernelGGL((gemm2_q4k_kernel<MT, W>), grid, dim3(kG2Threads), 0, st, A);
     return hipGetLastError();
+}
+
+template <int MT, int W>
+static hipError_t launch_gemm2(const sihip_weight *w, const GemmPlan &p, const GemmBufs &B,
+                               const float *X, int64_t ldx, int64_t M, float *Y, int64_t ldy,
+                               hipStream_t st) {
+    return launch_gemm2_multi<MT, W>(1, &w, p, B, X, ldx, M, &Y, &ldy, st);
 }
 
 template <uint32_t FMT, int MT>
@@ -1901,10 +1919,33 @@ static int run_gemm_multi(sihip_ctx *ctx, int count, const sihip_weight *const *
                           const float *X, int64_t M, float *const *Y, hipStream_t st) {
     if (count <= kKFMaxSegs && gemmkf_eligible(ctx, count, wc, M))
         return run_gemmkf(ctx, count, wc, X, M, Y, st);
+    // the Q4_K weights on the 16x16 kernel (M >= gemm2_min_m) share one
+    // launch, planned as one matrix of their n blocks together (the
+    // GEMM_GROUP option at 0 turns this off)
+    bool grp[kMaxSegs] = {};
+    int ngrp = 0;
+    Layout Lg{};
+    if (M >= gemm2_min_m(ctx->opt) && ctx->opt.gemm_group != 0) {
+        int64_t nblk = 0;
+        for (int i = 0; i < count; i++)
+            if (wc[i]->L.type == T_Q4_K && ngrp < kG2MaxSegs) {
+                grp[i] = true;
+                if (ngrp++ == 0) Lg = wc[i]->L;
+                nblk += (wc[i]->L.n_out + kG2BN - 1) / kG2BN;
+            }
+        Lg.n_out = nblk * kG2BN;
+        if (ngrp < 2) {
+            for (int i = 0; i < count; i++) grp[i] = false;
+            ngrp = 0;
+        }
+    }
+    auto plan_of = [&](int i, int force_mt) {
+        return grp[i] ? plan_gemm(ctx, Lg, M, force_mt) : plan_gemm(ctx, wc[i]->L, M, force_mt);
+    };
     GemmPlan plan[kMaxSegs];
     XKey key[kMaxSegs];
     for (int i = 0; i < count; i++) {
-        plan[i] = plan_gemm(ctx, wc[i]->L, M);
+        plan[i] = plan_of(i, 0);
         key[i] = xkey(wc[i]->L, plan[i]);
     }
     for (int i = 0; i < count; i++) {
@@ -1912,10 +1953,22 @@ static int run_gemm_multi(sihip_ctx *ctx, int count, const sihip_weight *const *
         for (int j = 0; j < count; j++)
             if (key[j].fam == key[i].fam && plan[j].mt > mt) mt = plan[j].mt;
         if (mt != plan[i].mt) {
-            const GemmPlan q = plan_gemm(ctx, wc[i]->L, M, mt);
+            const GemmPlan q = plan_of(i, mt);
             if (q.mt == mt && q.v2 == plan[i].v2) {
                 plan[i] = q;
                 key[i] = xkey(wc[i]->L, q);
+            }
+        }
+    }
+    if (ngrp) {  // the group's plan is the 16x16 kernel's, the same for every member
+        int g0 = 0;
+        while (!grp[g0]) g0++;
+        if (!plan[g0].v2 || plan[g0].small || plan[g0].mt < 2) {
+            for (int i = 0; i < count; i++) grp[i] = false;
+            ngrp = 0;
+            for (int i = 0; i < count; i++) {
+                plan[i] = plan_gemm(ctx, wc[i]->L, M);
+                key[i] = xkey(wc[i]->L, plan[i]);
             }
         }
     }
@@ -1949,9 +2002,37 @@ static int run_gemm_multi(sihip_ctx *ctx, int count, const sihip_weight *const *
     }
     rc = order_before(ctx, ctx->order, st);
     if (rc) return rc;
+    bool grp_done = false;
     for (int i = 0; i < count; i++) {
         GemmBufs B{(uint8_t *)ctx->d_ws + off[i], (float *)ctx->d_gpart, ctx->d_gcnt};
         B.quant = first[i];
+        if (grp[i]) {
+            if (grp_done) continue;
+            grp_done = true;
+            const sihip_weight *gw[kG2MaxSegs];
+            float *gy[kG2MaxSegs];
+            int64_t gld[kG2MaxSegs];
+            int n = 0;
+            for (int j = i; j < count; j++)
+                if (grp[j]) {
+                    gw[n] = wc[j];
+                    gy[n] = Y[j];
+                    gld[n] = wc[j]->L.n_out;
+                    n++;
+                }
+            const bool w1 = ctx->opt.gemm2_waves == 1;
+            const int64_t ldx = wc[i]->L.n_in;
+            hipError_t e;
+            switch (plan[i].mt) {
+                case 2: e = launch_gemm2_multi<2, 2>(n, gw, plan[i], B, X, ldx, M, gy, gld, st); break;
+                case 4: e = w1 ? launch_gemm2_multi<4, 1>(n, gw, plan[i], B, X, ldx, M, gy, gld, st)
+                               : launch_gemm2_multi<4, 2>(n, gw, plan[i], B, X, ldx, M, gy, gld, st); break;
+                default: e = w1 ? launch_gemm2_multi<8, 1>(n, gw, plan[i], B, X, ldx, M, gy, gld, st)
+                                : launch_gemm2_multi<8, 2>(n, gw, plan[i], B, X, ldx, M, gy, gld, st); break;
+            }
+            if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "gemm launch: %s", hipGetErrorString(e));
+            continue;
+        }
         rc = launch_gemm_mfma(ctx, wc[i], plan[i], B, X, wc[i]->L.n_in, M, Y[i], wc[i]->L.n_out, st);
         if (rc) return rc;
     }

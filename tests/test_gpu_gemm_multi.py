@@ -1,9 +1,12 @@
 """sihip_gemm_multi_dev: the GEMMs of several weights that share one X (the
 q/k/v and gate/up matrices of the batched forward), the activation
-quantized once per record layout. Every output is checked against the
-oracle to the path's bar; a weight whose plan is its single-call plan must
-also give the bits of sihip_gemm_dev (same kernels, same planes), while a
-weight given its group's m-tile count may slice K differently (same bar)."""
+quantized once per record layout, and from M = 384 the Q4_K weights in one
+launch of the 16x16 kernel (their n blocks one after another in one grid,
+planned together). Every output is checked against the oracle to the
+path's bar; a weight whose plan is its single-call plan must also give the
+bits of sihip_gemm_dev (same kernels, same planes), while a weight given
+its group's m-tile count, or planned with its group, may slice K
+differently (same bar)."""
 import numpy as np
 import pytest
 
@@ -42,7 +45,11 @@ def _run(dev, ws, X, multi=True):
 # record layouts (Q5_0, Q8_0, F16, Q4_K), and a batch below every
 # matrix-core threshold (the matvec kernel per weight)
 GROUPS = [
-    ("qkv-q4km-M512", [(sa.Q4_K, 4096), (sa.Q4_K, 1024), (sa.Q6_K, 1024)], 4096, 512, (0, 2)),
+    ("qkv-q4km-M512", [(sa.Q4_K, 4096), (sa.Q4_K, 1024), (sa.Q6_K, 1024)], 4096, 512, (2,)),
+    ("gate-up-q4k-M512", [(sa.Q4_K, 2816), (sa.Q4_K, 2816)], 1024, 512, ()),
+    # two Q4_K segments with K slices (the second's partial sums at column
+    # 128 x 3 of the shared rows) and a row count inside its last block
+    ("q4k-sliced-M384", [(sa.Q4_K, 300), (sa.Q6_K, 128), (sa.Q4_K, 200)], 2048, 384, ()),
     ("gate-up-q4k-M8", [(sa.Q4_K, 2048), (sa.Q4_K, 2048)], 2048, 8, (0, 1)),
     ("mixed-M40", [(sa.Q5_0, 640), (sa.Q8_0, 384), (sa.F16, 512), (sa.Q4_K, 300)], 2048, 40, ()),
     ("matvec-M2", [(sa.Q4_K, 700), (sa.Q6_K, 300), (sa.Q5_0, 260)], 1024, 2, (0, 1, 2)),
@@ -134,3 +141,29 @@ def test_gemm_multi_refuses_bad_groups(dev):
             buf.free()
         a.free()
         b.free()
+
+
+def test_gemm_multi_q4k_group_vs_separate(dev, oracle, option):
+    """The grouped Q4_K launch against the same weights launched one by one
+    (GEMM_GROUP = 0): both within the bar of the oracle, and the group's
+    results do not depend on the order of its weights."""
+    rng = np.random.default_rng(9100)
+    n_in, M = 2048, 512
+    mats = [(sa.Q4_K, 1536), (sa.Q4_K, 384), (sa.Q4_K, 130)]
+    Ws = [synth.make_weights(wt, n, n_in, rng) for wt, n in mats]
+    ws = [dev.upload(wt, n, n_in, W) for (wt, n), W in zip(mats, Ws)]
+    try:
+        X = _rows(rng, M, n_in)
+        grouped = _run(dev, ws, X)
+        rev = _run(dev, ws[::-1], X)[::-1]
+        option("GEMM_GROUP", 0)
+        separate = _run(dev, ws, X)
+        for i, ((wt, n_out), W) in enumerate(zip(mats, Ws)):
+            ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+            for label, Y in (("grouped", grouped[i]), ("separate", separate[i])):
+                assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
+                             f"{label} weight {i}")
+            assert np.array_equal(bits(grouped[i]), bits(rev[i])), f"weight {i}: order matters"
+    finally:
+        for w in ws:
+            w.free()
