@@ -36,7 +36,7 @@ typedef struct {
 } with_gemm;
 
 /* ---- the reference CPU backend with the gemm slot the integration adds:
- * one reference gemv per row (INTEGRATION.md's cpu_gemm) -------------- */
+ * one reference gemv per row (the cpu_gemm fill of backend.c) ---------- */
 
 static void cpu_gemv_fwd(si_backend *be, const si_tensor *w, const float *x, float *y,
                          int64_t n_out, si_tp *tp) {

@@ -42,7 +42,7 @@ def test_open_reports_no_device_or_opens(harness):
 
 def test_cpu_vtable_gemm_slot(harness, oracle):
     """The gemm slot as the CPU backend fills it (one gemv per activation
-    row; the line INTEGRATION.md adds to the reference backend.c) gives the
+    row, the fill a maintainer adds to the reference backend.c) gives the
     rows of M separate gemv calls, for every weight type."""
     be = harness.cpu()
     rng = np.random.default_rng(41)
