@@ -49,13 +49,15 @@ def _check(dev, oracle, wt, n_out, n_in, M, seed, what):
     assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
 
 
+# (M, fused launch): the fused launch takes M <= 8
+M_CASES = [(m, True) for m in (3, 4, 5, 8)] + [(m, False) for m in (3, 4, 5, 8, 9, 12, 16)]
+
+
 @pytest.mark.parametrize("wt", KQ, ids=lambda t: sa.NAMES[t])
-@pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 12, 16])
+@pytest.mark.parametrize("M,fused", M_CASES,
+                         ids=[f"M{m}-{'fused' if f else 'separate'}" for m, f in M_CASES])
 @pytest.mark.parametrize("n_out,n_in", [(33, 256), (200, 1024), (96, 2304)])
-@pytest.mark.parametrize("fused", [True, False], ids=["fused", "separate"])
 def test_small_m_vs_oracle(dev, oracle, option, wt, M, n_out, n_in, fused):
-    if fused and M > 8:
-        pytest.skip("the fused launch takes M <= 8; the separate case covers this M")
     option("GEMMKF_MAX_M", 8 if fused else 0)
     _check(dev, oracle, wt, n_out, n_in, M, 7000 + 97 * wt + 13 * M + n_in,
            f"{sa.NAMES[wt]} {n_out}x{n_in} M={M} {'fused' if fused else 'separate'}")
