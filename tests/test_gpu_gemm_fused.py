@@ -184,3 +184,23 @@ def test_fused_group_graph_replays(dev):
             b.free()
         for w in ws:
             w.free()
+
+
+@pytest.mark.parametrize("wt,n_in", [(sa.Q6_K, 1024), (sa.Q4_K, 1536)],
+                         ids=["Q6_K-head", "Q4_K-head"])
+def test_fused_output_head(dev, oracle, wt, n_in):
+    """A 151936-row output head at M = 8 (config 1's vocabulary): 1187
+    tiles in one grid, every output against the oracle."""
+    print(f"fused head {sa.NAMES[wt]} 151936x{n_in}", flush=True)
+    rng = np.random.default_rng(8600 + wt)
+    n_out, M = 151936, 8
+    W = synth.make_weights(wt, n_out, n_in, rng)
+    X = _rows(rng, M, n_in)
+    w = dev.upload(wt, n_out, n_in, W)
+    try:
+        Y = dev.gemm(w, X)
+    finally:
+        w.free()
+    ref, L1 = oracle.gemm(wt, W, n_out, n_in, X)
+    assert_close(Y.reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1),
+                 f"{sa.NAMES[wt]} head {n_out}x{n_in}")
