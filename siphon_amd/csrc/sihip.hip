@@ -397,21 +397,31 @@ static int choose_G(const Options &o, uint32_t type, int64_t n_out, int64_t n_in
         return G;
     }
     const int64_t target = wave_target(o);
-    auto pick = [&](int pct) {
-        int best = 1;
+    // Two lanes per row at least (one lane per row lost 4-8% on 151936-row
+    // heads of 4 and 28 columns) and 16 rounds per lane at most (a lane that
+    // walks 80 units of a 27648 x 5120 Q5_0 or F16 row lost 3-32% to tiles
+    // 16 wide); a row of one column keeps one lane.
+    const int min_g = ncols >= 2 ? 2 : 1;
+    auto pick = [&](int pct, int64_t max_rounds) {
+        int best = 0;
         int64_t best_tiles = 0;
-        for (int G = 1; G <= 64; G *= 2) {
+        for (int G = min_g; G <= 64; G *= 2) {
             const int64_t S = (ncols + G - 1) / G;
             if (ncols * 100 < S * G * pct) continue;  // too few lanes busy
+            if (S > max_rounds) continue;
             const int64_t tiles = (n_out + 64 / G - 1) / (64 / G);
             if (tiles > best_tiles) { best = G; best_tiles = tiles; }
             if (tiles >= target) break;
         }
         return std::make_pair(best, best_tiles);
     };
-    auto [G, tiles] = pick(80);
-    if (tiles < 256) G = pick(50).first;
-    return G;
+    auto choose = [&](int64_t max_rounds) {
+        auto [G, tiles] = pick(80, max_rounds);
+        if (tiles < 256) G = pick(50, max_rounds).first;
+        return G;
+    };
+    const int G = choose(16);
+    return G > 0 ? G : std::max(choose(INT64_MAX), 1);
 }
 
 // Exponent E of the Q4_K 16x16 GEMM's min operand (gemm2.h): the largest
@@ -1354,7 +1364,6 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     const int64_t nk = L.n_in / 128;
     const int64_t threads = p.Mp * L.n_in / 32;
     constexpr int bias = FMT == T_Q4_0 ? 8 : FMT == T_Q5_0 ? 16 : 0;
-    const int64_t NB = (L.n_out + kG2BN - 1) / kG2BN;
     // record mode: with up to 32-row m blocks and a K slice whose records
     // fit kGQSliceLds, the slice's records go to LDS up front (mode 1: 2-7%
     // faster than the ring at M = 8-16, e.g. kv 1024 x 5120 13.1 against
