@@ -257,6 +257,71 @@ __device__ inline void kf_compute_fold(const KSWStage<T_Q2_K> &s, const uint4 (&
     }
 }
 
+// End of a K-sliced tile after each wave has issued the agent-scope stores
+// of its slice's partial sums in the registers' order: the 1024 floats of
+// slice s at pt + s * per_slice, float 256 w + 32 (4 nt + i) + l holding
+// result register i of lane l (< 32) of wave w's n tile nt, which is
+// activation row 4 (l / 16) + i, column 32 w + 16 nt + l % 16 of the tile.
+// Stored that way each store instruction writes whole 128-byte lines and
+// the last workgroup reads a slice with one 16-byte load per thread (the
+// same partial sums scattered row by row as 64-byte pieces took 1.8 us more
+// per launch at M = 8). Counting and ordering as slices_finish (agent.h):
+// each wave's stores complete before the barrier that precedes the count,
+// the last of the S workgroups adds the slices in slice order and resets
+// the counter.
+__device__ inline void kf_finish(const float *pt, int64_t per_slice, uint32_t *cnt, int S,
+                                 int64_t M, int64_t n0, int64_t n_out, float *y, int64_t ldy) {
+    static_assert(kKFThreads * 4 == kKFWaves * 256, "one float4 of a slice per thread");
+    __shared__ uint32_t last_flag;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)S - 1;
+    __syncthreads();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (!last_flag) return;
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(pt), (short)0, (int)(((int64_t)(S - 1) * per_slice + kKFWaves * 256) * 4),
+        0x00020000);
+    const uint32_t t4 = threadIdx.x * 16u;  // this thread's 16 bytes of a slice
+    // slices in groups of 8 whose loads are issued together (each group
+    // costs one round trip: agent-scope loads miss the XCD's L2), added in
+    // slice order
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        uint4 pv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int s = s0 + k < S ? s0 + k : S - 1;
+            pv[k] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, (int)((int64_t)s * per_slice * 4 + t4), 0, 16));
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (s0 + k < S) {
+                v[0] += __uint_as_float(pv[k].x);
+                v[1] += __uint_as_float(pv[k].y);
+                v[2] += __uint_as_float(pv[k].z);
+                v[3] += __uint_as_float(pv[k].w);
+            }
+    }
+    // floats 4 t .. 4 t + 3: wave w, register (nt, i), lanes l .. l + 3 (one
+    // lane group): row 4 (l / 16) + i, columns 32 w + 16 nt + l % 16 + j
+    const int k = 4 * (int)threadIdx.x;
+    const int w = k >> 8, r = k & 255;
+    const int nt = r >> 7, i = (r >> 5) & 3, l = r & 31;
+    const int64_t m = 4 * (l >> 4) + i;
+    const int64_t n = n0 + 32 * w + 16 * nt + (l & 15);
+    if (m < M) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (n + j < n_out) y[m * ldy + n + j] = v[j];
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The workgroup's share of segment sg: tile t % ntile, slice t / ntile.
 template <uint32_t FMT, int NH>
 __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_t *lds) {
@@ -397,26 +462,24 @@ __device__ inline void kf_body(const GKFArgs &A, const GKFSeg &sg, int t, uint8_
         }
         return;
     }
-    const int64_t ldp = (int64_t)sg.ntile * kKFRows;
-    if (has) {
+    // K slices: the partial tile in the registers' order (kf_finish), lanes
+    // 0..31 of each result register one 128-byte line; lane group g (< 2)
+    // holds activation rows 4 g .. 4 g + 3 (four-way: of y[g])
+    const int64_t per_slice = (int64_t)sg.ntile * kKFWaves * 256;
+    float *const pt = sg.part + (int64_t)tile * (kKFWaves * 256);
+    if (has && lane < 32) {
+        float *const pw = pt + slice * per_slice + wave * 256 + lane;
 #pragma unroll
-        for (int h = 0; h < YH; h++) {
-            if (!holds(h)) continue;
+        for (int nt = 0; nt < 2; nt++)
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                const int64_t n = n0 + 16 * nt + r16;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int64_t m = row_of(h, i);
-                    if (m < A.M)
-                        __hip_atomic_store(sg.part + ((int64_t)slice * kKFMp + m) * ldp + n,
-                                           y[h][nt][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+            for (int i = 0; i < 4; i++) {
+                const float v = YH == 1 || g == 0 ? y[0][nt][i] : y[YH - 1][nt][i];
+                __hip_atomic_store(pw + (nt * 4 + i) * 32, v, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
-        }
     }
-    slices_finish<kKFMp, kKFRows, kKFThreads>(sg.part, sg.cnt + tile, sg.S, kKFMp, ldp, 0, A.M,
-                                              (int64_t)tile * kKFRows, sg.n_out, sg.y, sg.ldy);
+    kf_finish(pt, per_slice, sg.cnt + tile, sg.S, A.M, (int64_t)tile * kKFRows, sg.n_out, sg.y,
+              sg.ldy);
 }
 
 // Grid: sum over segments of ntile * S workgroups of kKFThreads; dynamic
