@@ -510,14 +510,15 @@ def bench_prefill_pass(dev, torch, stream, layers, M=512, reps=5):
                          "frac": per[dom]["frac_int8_peak"]}}
 
 
-def bench_batch_decode(dev, torch, stream, layers, M=8, reps=10):
+def bench_batch_decode(dev, torch, stream, layers, M=8, reps=20, warmup=5):
     """A decode step of M sequences at once through the 32 decode-pass
     layers: per layer q/k/v and gate/up in one gemm_multi_dev call each
     (activation quantized once), wo and down one gemm_dev call, on M
     activation rows resident in HBM; 128 calls in one HIP graph, replays
     checked against the eager results. tokens/s = M / pass time; GB/s = the
     pass's GGUF weight bytes / pass time (each weight streamed once per
-    step, whatever M)."""
+    step, whatever M). `warmup` untimed replays precede the `reps` timed
+    ones."""
     from siphon_amd import synth
     sp = stream.cuda_stream
     for l in layers:
@@ -550,6 +551,10 @@ def bench_batch_decode(dev, torch, stream, layers, M=8, reps=10):
         torch.cuda.synchronize()
         for n in names:
             assert torch.equal(Y[n], eager[n]), f"batch decode graph replay differs on {n}"
+    for _ in range(warmup):  # untimed, back to back like the timed replays
+        with torch.cuda.stream(stream):
+            g.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(reps):

@@ -82,8 +82,10 @@ struct Q8KRow {
 // 16*lane16 .. 16*lane16+15 (x16). The abs-max key is (|x| bits, 255 - index,
 // sign): its maximum is the largest |x| at its first occurrence, exactly the
 // reference's "if (ax > amax)" scan; |x| of a non-negative float orders like
-// its bit pattern, and NaN never enters (it is never > amax).
-__device__ inline Q8KRow q8k_block_row16(const float x16[16], int lane16) {
+// its bit pattern, and NaN never enters (it is never > amax). This is the
+// general routine; q8k_block_row16 below takes it for the blocks of a wave
+// that its shorter path does not cover.
+__device__ inline Q8KRow q8k_block_row16_scan(const float x16[16], int lane16) {
     uint32_t abits = 0, key = 0;
     for (int k = 0; k < 16; k++) {
         const float a = fabsf(x16[k]);
@@ -116,6 +118,80 @@ __device__ inline Q8KRow q8k_block_row16(const float x16[16], int lane16) {
         v = v < 127 ? v : 127;
         s += (int)(int8_t)(uint8_t)(v & 0xff);
         w[k >> 2] |= (uint32_t)(v & 0xff) << (8 * (k & 3));
+    }
+    r.q = make_uint4(w[0], w[1], w[2], w[3]);
+    r.d = 1.0f / iscale;
+    r.gsum = s;
+    return r;
+}
+
+// The same block quantization (bit for bit) with fewer instructions, for
+// blocks whose 16 elements of every lane are finite and whose lanes do not
+// hold both +a and -a for their largest |x| = a; when any block of the
+// wave misses that, the whole wave takes q8k_block_row16_scan.
+//   abs-max: the largest positive value is the signed integer maximum of
+//   the bit patterns, the largest-magnitude negative one the unsigned
+//   maximum; the larger magnitude of the two is the lane's |x| maximum,
+//   and its sign is the sign at the lane's first occurrence unless both
+//   signs reach it. Across the 16 lanes the lowest lane with the block's
+//   maximum has its first occurrence (lane16 holds the lower indices).
+//   quants: with every element finite, |iscale * x| rounds to at most 127
+//   (or is +-inf or 0 * inf = NaN when -127 / vmax overflows), so
+//   t = iscale * x + 12582912 lies in [2^23, 2^24), or is +-inf or a NaN
+//   without payload, and the reference's quant (t's low 23 bits - 2^22,
+//   capped at 127, taken as a byte) is the low byte of t's bits: the cap
+//   never applies. The bytes are packed with two permutes and an or, and
+//   each packed word is summed with one 4-way byte dot product.
+__device__ inline Q8KRow q8k_block_row16(const float x16[16], int lane16) {
+    int pmax = (int)__float_as_uint(x16[0]);
+    uint32_t nmax = __float_as_uint(x16[0]);
+#pragma unroll
+    for (int k = 1; k < 16; k++) {
+        const uint32_t b = __float_as_uint(x16[k]);
+        pmax = (int)b > pmax ? (int)b : pmax;
+        nmax = b > nmax ? b : nmax;
+    }
+    const uint32_t pa = pmax >= 0 ? (uint32_t)pmax : 0u;              // largest x >= +0
+    const uint32_t na = nmax >= 0x80000000u ? nmax & 0x7fffffffu : 0u;  // largest |x| of x <= -0
+    const uint32_t lane_abits = pa > na ? pa : na;
+    const bool general = lane_abits >= 0x7f800000u || (pa == na && pa != 0u);
+    if (__builtin_amdgcn_ballot_w64(general) != 0) return q8k_block_row16_scan(x16, lane16);
+    const int ctrls[4] = {kDppXor1, kDppXor2, kDppHalfMirror, kDppMirror};
+    uint32_t abits = lane_abits;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t a2 = dpp_u32(abits, ctrls[i]);
+        abits = a2 > abits ? a2 : abits;
+    }
+    // the lowest lane holding the maximum, and its sign
+    uint32_t key = lane_abits == abits ? ((uint32_t)(15 - lane16) << 1) | (na > pa ? 1u : 0u) : 0u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t k2 = dpp_u32(key, ctrls[i]);
+        key = k2 > key ? k2 : key;
+    }
+    Q8KRow r;
+    if (abits == 0) {
+        r.q = make_uint4(0, 0, 0, 0);
+        r.d = 0.0f;
+        r.gsum = 0;
+        return r;
+    }
+    const float vmax = __uint_as_float(abits | ((key & 1u) << 31));
+    const float iscale = -127.0f / vmax;
+    uint32_t w[4];
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t t[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            t[k] = __float_as_uint(__fadd_rn(__fmul_rn(iscale, x16[4 * j + k]), 12582912.0f));
+        // bytes 0 of t[0], t[1] into bytes 0, 1; of t[2], t[3] into 2, 3
+        const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(t[3], t[2], 0x04000c0cu);
+        w[j] = lo | hi;
+        s = __builtin_amdgcn_sdot4((int)w[j], 0x01010101, s, false);
     }
     r.q = make_uint4(w[0], w[1], w[2], w[3]);
     r.d = 1.0f / iscale;
