@@ -227,6 +227,99 @@ struct G2Args {
     G2Seg seg[kG2MaxSegs];
 };
 
+// ---- K slices of the 16x16-tile GEMMs (this file, gemm6.h, gemmh.h, gemmq.h)
+//
+// A workgroup of 4 waves computes a BM x 128 output tile: wave w columns
+// 32 w .. 32 w + 31 as two 16-column n tiles, MT = BM / 16 m tiles; result
+// register i of lane l of tile (mt, nt) is row 16 mt + 4 (l / 16) + i,
+// column 32 w + 16 nt + l % 16. A K slice's partial tile is stored in that
+// register order, float ((w MT + mt) 2 + nt) 256 + 64 i + l of the tile's
+// BM * 128 floats (at part + ((slice MB + mblk) NB + nblk) BM 128), so each
+// store instruction writes 256 contiguous bytes and the last workgroup
+// reads a slice with 16-byte loads. Stored row by row (four 64-byte pieces
+// per instruction) the partial sums cost the Llama-3-8B prefill at M = 512
+// 2.3-3.5 us per sliced call (a timing copy without them).
+template <int MT>
+__device__ inline void g2_store_partial(float *pt, int wave, int lane, const v4f2_t (&y)[MT][2],
+                                        float scale) {
+    float *const pw = pt + wave * (MT * 512) + lane;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                __hip_atomic_store(pw + ((mt * 2 + nt) * 4 + i) * 64, y[mt][nt][i] * scale,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// End of a K-sliced tile after every wave has issued g2_store_partial for
+// its slice (pt: the tile's partial in slice 0, per_slice floats between
+// slices): the arrival count and ordering of slices_finish (agent.h); the
+// last of the S workgroups adds the slices in slice order into y[m * ldy + n]
+// for rows m0 + r below M and columns n0 + c below n_out, and resets the
+// counter.
+template <int MT>
+__device__ inline void g2_slices_finish(const float *pt, int64_t per_slice, uint32_t *cnt, int S,
+                                        int64_t m0, int64_t M, int64_t n0, int64_t n_out, float *y,
+                                        int64_t ldy) {
+    constexpr int kQ = MT * 2;  // float4s per thread of a slice's tile (256 threads)
+    __shared__ uint32_t last_flag;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)S - 1;
+    __syncthreads();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (!last_flag) return;
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(pt), (short)0,
+        (int)(((int64_t)(S - 1) * per_slice + MT * 2048) * 4), 0x00020000);
+    float v[kQ][4];
+#pragma unroll
+    for (int q = 0; q < kQ; q++) v[q][0] = v[q][1] = v[q][2] = v[q][3] = 0.0f;
+    // one slice's loads issued together (one round trip per slice: agent-
+    // scope loads miss the XCD's L2), the slices added in slice order
+    for (int s = 0; s < S; s++) {
+        uint4 pv[kQ];
+#pragma unroll
+        for (int q = 0; q < kQ; q++)
+            pv[q] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                           pr, (int)(((int64_t)s * per_slice + (q * 256 + (int)threadIdx.x) * 4) * 4), 0,
+                           16));
+#pragma unroll
+        for (int q = 0; q < kQ; q++) {
+            v[q][0] += __uint_as_float(pv[q].x);
+            v[q][1] += __uint_as_float(pv[q].y);
+            v[q][2] += __uint_as_float(pv[q].z);
+            v[q][3] += __uint_as_float(pv[q].w);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < kQ; q++) {
+        // floats k .. k + 3: wave w, tile (mt, nt), register i, lanes l .. l + 3
+        const int k = (q * 256 + (int)threadIdx.x) * 4;
+        const int w = k / (MT * 512), rem = k % (MT * 512);
+        const int mt = rem >> 9, nt = (rem >> 8) & 1, i = (rem >> 6) & 3, l = rem & 63;
+        const int64_t m = m0 + 16 * mt + 4 * (l >> 4) + i;
+        const int64_t n = n0 + 32 * w + 16 * nt + (l & 15);
+        if (m < M) {
+            float *const dst = y + m * ldy + n;
+            if (n + 3 < n_out && ((uintptr_t)dst & 15) == 0) {
+                *reinterpret_cast<float4 *>(dst) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (n + j < n_out) dst[j] = v[q][j];
+            }
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // q * f bytewise for bytes and products below 256 (no carries between
 // bytes); f2 holds the factor in both 16-bit halves.
 __device__ inline uint32_t g2_bytes_times(uint32_t q, uint32_t f2) {
@@ -429,28 +522,15 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
         }
         return;
     }
-    // K slices: partial sums through agent-scope stores (they write through
-    // and are read past the per-XCD L2s), then the tile's arrival and the
-    // last workgroup's slice-order sum; the segment's columns of the
-    // partial-sum rows start at 128 nb0
-    const int64_t ldp = (int64_t)A.NB * kG2BN;
-    float *const part = A.part + (int64_t)sg.nb0 * kG2BN;
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int64_t n = n0 + 16 * nt + r16;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int64_t m = m0 + 16 * mt + 4 * g + i;
-                if (m < A.M)
-                    __hip_atomic_store(part + ((int64_t)slice * A.Mp + m) * ldp + n,
-                                       y[mt][nt][i] * sg.yscale, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
-    }
-    slices_finish<BM, kG2BN, kG2Threads>(part, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, A.Mp,
-                                         ldp, m0, A.M, (int64_t)lblk * kG2BN, sg.n_out, sg.y, sg.ldy);
+    // K slices: the partial tile (already scaled by 2^-E) in register order
+    // through agent-scope stores (they write through and are read past the
+    // per-XCD L2s), then the tile's arrival and the last workgroup's
+    // slice-order sum into the segment's columns
+    const int64_t per_slice = (int64_t)A.MB * A.NB * (BM * kG2BN);
+    float *const pt = A.part + ((int64_t)mblk * A.NB + nblk) * (BM * kG2BN);  // slice 0
+    g2_store_partial<MT>(pt + slice * per_slice, wave, lane, y, sg.yscale);
+    g2_slices_finish<MT>(pt, per_slice, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, m0, A.M,
+                         (int64_t)lblk * kG2BN, sg.n_out, sg.y, sg.ldy);
 }
 
 }  // namespace sihip

@@ -26,7 +26,7 @@
 // reloaded K-step by K-step for the next super-block as soon as each
 // K-step's MFMAs are issued. K slices
 // (S > 1) split the super-blocks of a tile over S workgroups whose partial
-// sums are added in slice order (slices_finish), for shapes whose output
+// sums are added in slice order (g2_slices_finish), for shapes whose output
 // tiles alone would leave CUs idle.
 #pragma once
 
@@ -288,25 +288,14 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemm6_q6k_kernel(G6Args A) {
         }
         return;
     }
-    // K slices: partial sums through agent-scope stores (they write through
-    // and are read past the per-XCD L2s), then the tile's arrival and the
-    // last workgroup's slice-order sum
-    const int64_t ldp = (int64_t)A.NB * kG2BN;
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int64_t n = n0 + 16 * nt + r16;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int64_t m = m0 + 16 * mt + 4 * g + i;
-                if (m < A.M)
-                    __hip_atomic_store(A.part + ((int64_t)slice * A.Mp + m) * ldp + n, y[mt][nt][i],
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-    }
-    slices_finish<BM, kG2BN, kG2Threads>(A.part, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, A.Mp,
-                                         ldp, m0, A.M, (int64_t)nblk * kG2BN, A.n_out, A.y, A.ldy);
+    // K slices: the partial tile in register order through agent-scope
+    // stores (they write through and are read past the per-XCD L2s), then
+    // the tile's arrival and the last workgroup's slice-order sum
+    const int64_t per_slice = (int64_t)A.MB * A.NB * (BM * kG2BN);
+    float *const pt = A.part + ((int64_t)mblk * A.NB + nblk) * (BM * kG2BN);  // slice 0
+    g2_store_partial<MT>(pt + slice * per_slice, wave, threadIdx.x & 63, y, 1.0f);
+    g2_slices_finish<MT>(pt, per_slice, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, m0, A.M,
+                         (int64_t)nblk * kG2BN, A.n_out, A.y, A.ldy);
 }
 
 }  // namespace sihip

@@ -22,7 +22,7 @@
 //     chunks and no partial sums meet inside the workgroup. With S > 1
 //     slices the slices' partial tiles go through agent-scope stores and
 //     the last workgroup of a tile adds them in slice order
-//     (slices_finish), so the result does not depend on arrival order.
+//     (kf_finish), so the result does not depend on arrival order.
 #pragma once
 
 #include "agent.h"
@@ -53,7 +53,7 @@ struct GKFSeg {
     const uint8_t *w;   // gemmks.h chunks [nblk][nb]
     float *y;           // Y[m * ldy + n]
     int64_t ldy, n_out;
-    float *part;        // S > 1: partial sums [S][kKFMp][ntile * kKFRows]
+    float *part;        // S > 1: partial sums [S][ntile][kKFMp * kKFRows], register order (kf_finish)
     uint32_t *cnt;      // S > 1: arrival counters [ntile], zero between launches
     uint32_t type;
     int nblk;           // 32-row blocks
@@ -315,9 +315,14 @@ __device__ inline void kf_finish(const float *pt, int64_t per_slice, uint32_t *c
     const int64_t m = 4 * (l >> 4) + i;
     const int64_t n = n0 + 32 * w + 16 * nt + (l & 15);
     if (m < M) {
+        float *const dst = y + m * ldy + n;
+        if (n + 3 < n_out && ((uintptr_t)dst & 15) == 0) {
+            *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (n + j < n_out) y[m * ldy + n + j] = v[j];
+            for (int j = 0; j < 4; j++)
+                if (n + j < n_out) dst[j] = v[j];
+        }
     }
     if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
