@@ -681,6 +681,7 @@ def probe_rotated(dev, torch, stream, nbytes, copies):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
     del g, buf
+    torch.cuda.empty_cache()  # see probe_floors
     return us
 
 
@@ -717,6 +718,11 @@ def probe_floors(dev, torch, stream, sizes, reps=10):
         out[label] = e0.elapsed_time(e1) * 1e3 / (reps * N_LAYERS)
         del g
     del buf
+    # hand the probe's buffer (2.1 GB) back to the device: kept in torch's
+    # cache, it made the batch-8 step measured after it 3% slower (1.71
+    # against 1.66 ms, one box), the library's GEMM copies then being
+    # allocated around it
+    torch.cuda.empty_cache()
     return out
 
 
