@@ -51,6 +51,19 @@ __host__ __device__ constexpr int gq_rec_bytes(int BM) { return 160 * BM; }
 __host__ __device__ constexpr int gq_rec_dx(int BM) { return 128 * BM; }
 __host__ __device__ constexpr int gq_rec_bs(int BM) { return 144 * BM; }
 
+// Block j of a step, row mr of its m block, into the step's record R.
+template <int BM, int BIAS>
+__device__ inline void gq_put_block(uint8_t *R, int mr, int j, const Q80Block &q) {
+    // lane group g of the fragment takes elements 8 g .. 8 g + 7 (words 2g, 2g+1)
+    uint8_t *frag = R + (4 * (mr >> 4) + j) * 512;
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+        *reinterpret_cast<uint64_t *>(frag + (16 * g + (mr & 15)) * 8) =
+            (uint64_t)q.q[2 * g] | ((uint64_t)q.q[2 * g + 1] << 32);
+    reinterpret_cast<float *>(R + gq_rec_dx(BM))[j * BM + mr] = q.d;
+    reinterpret_cast<int *>(R + gq_rec_bs(BM))[j * BM + mr] = -BIAS * q.sum;
+}
+
 // Q8_0 block i (row m = i / (n_in / 32), block kb) of X into its record;
 // rows M..Mp-1 are zero.
 template <int BM, int BIAS>
@@ -70,15 +83,7 @@ __device__ inline void gq_quantize_one(const float *x, int64_t ldx, int64_t M, i
     }
     const int64_t mb = m / BM;
     const int mr = (int)(m % BM);
-    uint8_t *R = rec + (mb * (n_in / 128) + c) * gq_rec_bytes(BM);
-    // lane group g of the fragment takes elements 8 g .. 8 g + 7 (words 2g, 2g+1)
-    uint8_t *frag = R + (4 * (mr >> 4) + j) * 512;
-#pragma unroll
-    for (int g = 0; g < 4; g++)
-        *reinterpret_cast<uint64_t *>(frag + (16 * g + (mr & 15)) * 8) =
-            (uint64_t)q.q[2 * g] | ((uint64_t)q.q[2 * g + 1] << 32);
-    reinterpret_cast<float *>(R + gq_rec_dx(BM))[j * BM + mr] = q.d;
-    reinterpret_cast<int *>(R + gq_rec_bs(BM))[j * BM + mr] = -BIAS * q.sum;
+    gq_put_block<BM, BIAS>(rec + (mb * (n_in / 128) + c) * gq_rec_bytes(BM), mr, j, q);
 }
 
 // One thread per Q8_0 block (row m, block kb); rows M..Mp-1 are zero.
@@ -239,6 +244,8 @@ struct GQArgs {
     float *part;
     uint32_t *cnt;
     int q80s;             // the scalar Q8_0 quantizer (q80_block_sel)
+    const float *xf;      // XM 2: X[m * ldx + k], f32, quantized by the launch itself
+    int64_t ldx;
 };
 
 // steps in flight per wave: a ring of gq_depth(MT) register sets (two at
@@ -261,11 +268,17 @@ constexpr int64_t kGQSliceLds = 64 * 1024;
 //   0: through the register ring into two LDS buffers, a step ahead;
 //   1: all records of its K slice copied into LDS (dynamic, gq_lds_bytes)
 //      before the first step, so the steps read LDS only, with no record
-//      loads, LDS stores or barriers between them.
+//      loads, LDS stores or barriers between them;
+//   2: as 1, but the workgroup quantizes its K slice of X (f32, A.xf) into
+//      the same LDS image itself, one Q8_0 block per thread and pass (the
+//      quantizer of the separate launch, so the records are the same
+//      bytes), and no quantization launch runs before it. Each thread's
+//      first block of X is requested before the ring's first weights, so
+//      the quantization waits only for X (loads retire in issue order).
 template <uint32_t FMT, int MT, int XM>
 __global__ __launch_bounds__(kG2Threads)
 __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
-    static_assert(XM == 0 || XM == 1, "record modes 0 and 1");
+    static_assert(XM == 0 || XM == 1 || XM == 2, "record modes 0, 1 and 2");
     constexpr int BM = 16 * MT;
     constexpr int kRec = gq_rec_bytes(BM);
     constexpr int kXP = kRec / 16;
@@ -458,7 +471,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
             if (c + u < c1)
                 step(c + u, o[u], o[(u + kD - 1) % kD], o[(u + 1) % kD], (u & 1) ? sx1 : sx0,
                      (u & 1) ? sx0 : sx1);
-    } else {
+    } else if constexpr (XM == 1) {
         // the first weights go out first
 #pragma unroll
         for (int u = 0; u + 1 < kD; u++) load_wt(c0 + u < c1 ? c0 + u : c1 - 1, o[u]);
@@ -471,6 +484,58 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmq_kernel(GQArgs A) {
                 xr, (__attribute__((address_space(3))) void *)(gq_slice + i * 1024), 16, lane * 16,
                 c0 * kRec + i * 1024, 0, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int c = c0; c < c1; c += kD) {
+#pragma unroll
+            for (int u = 0; u < kD; u++)
+                if (c + u < c1) step_lds(c + u, o[u], o[(u + kD - 1) % kD]);
+        }
+    } else {
+        // the slice's blocks: nq = BM rows x 4 per step, block i = row i / nb4,
+        // block i % nb4 of the slice; rows past M are zero
+        const int nb4 = 4 * (c1 - c0), nq = BM * nb4;
+        const int64_t m0q = (int64_t)mblk * BM;
+        auto src = [&](int i, int &mr, int &kb) -> const float * {
+            mr = i / nb4;
+            kb = i - mr * nb4;
+            return A.xf + (m0q + mr) * A.ldx + (int64_t)c0 * 128 + 32 * kb;
+        };
+        auto put = [&](int mr, int kb, const Q80Block &q) {
+            gq_put_block<BM, bias>(gq_slice + (kb >> 2) * kRec, mr, kb & 3, q);
+        };
+        // this thread's first block before the weights
+        const int i0 = (int)threadIdx.x;
+        int mr0 = 0, kb0 = 0;
+        const float *s0 = i0 < nq ? src(i0, mr0, kb0) : A.xf;
+        const bool live0 = i0 < nq && m0q + mr0 < A.M;
+        float v0[32];
+        if (live0) q80_load(s0, v0);
+#pragma unroll
+        for (int u = 0; u + 1 < kD; u++) load_wt(c0 + u < c1 ? c0 + u : c1 - 1, o[u]);
+        if (i0 < nq) {
+            Q80Block q;
+            if (live0) {
+                q = q80_block_sel_v(v0, A.q80s);
+            } else {
+                q.d = 0.0f;
+                q.sum = 0;
+                for (int t = 0; t < 8; t++) q.q[t] = 0;
+            }
+            put(mr0, kb0, q);
+        }
+        for (int i = i0 + kG2Threads; i < nq; i += kG2Threads) {
+            int mr, kb;
+            const float *sx = src(i, mr, kb);
+            Q80Block q;
+            if (m0q + mr < A.M) {
+                q = q80_block_sel(sx, A.q80s);
+            } else {
+                q.d = 0.0f;
+                q.sum = 0;
+                for (int t = 0; t < 8; t++) q.q[t] = 0;
+            }
+            put(mr, kb, q);
+        }
         __syncthreads();
         for (int c = c0; c < c1; c += kD) {
 #pragma unroll

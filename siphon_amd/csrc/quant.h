@@ -220,13 +220,7 @@ struct Q80Block {
     uint32_t q[8];    // quants, byte k of q[t] = element 4t+k
 };
 
-__device__ inline Q80Block q80_block(const float *x) {
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 t = reinterpret_cast<const float4 *>(x)[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
+__device__ inline Q80Block q80_block_v(const float (&v)[32]) {
     float lane[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
@@ -264,6 +258,20 @@ __device__ inline Q80Block q80_block(const float *x) {
     return b;
 }
 
+__device__ inline void q80_load(const float *x, float (&v)[32]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 t = reinterpret_cast<const float4 *>(x)[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+__device__ inline Q80Block q80_block(const float *x) {
+    float v[32];
+    q80_load(x, v);
+    return q80_block_v(v);
+}
+
 // The portable scalar Q8_0 quantizer (reference src/kernels.c:542-558),
 // which the reference selects instead of the SIMD one when SI_SCALAR is set
 // (kernels.c:80-83): amax by the running comparison amax > |v| ? amax : |v|
@@ -271,13 +279,7 @@ __device__ inline Q80Block q80_block(const float *x) {
 // d == 0) and q = roundf(x * id), halves away from zero. |x * id| stays
 // within 127 (plus rounding), so the clamp below never changes a value; it
 // only keeps the conversion defined.
-__device__ inline Q80Block q80_block_scalar(const float *x) {
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 t = reinterpret_cast<const float4 *>(x)[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
+__device__ inline Q80Block q80_block_scalar_v(const float (&v)[32]) {
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; j++) {
@@ -307,10 +309,19 @@ __device__ inline Q80Block q80_block_scalar(const float *x) {
     return b;
 }
 
+__device__ inline Q80Block q80_block_scalar(const float *x) {
+    float v[32];
+    q80_load(x, v);
+    return q80_block_scalar_v(v);
+}
+
 // The Q8_0 quantizer a launch uses: the SIMD semantics (q80_block), or
 // the scalar ones when `scalar` is set (a wave-uniform launch argument).
 __device__ inline Q80Block q80_block_sel(const float *x, int scalar) {
     return scalar ? q80_block_scalar(x) : q80_block(x);
+}
+__device__ inline Q80Block q80_block_sel_v(const float (&v)[32], int scalar) {
+    return scalar ? q80_block_scalar_v(v) : q80_block_v(v);
 }
 
 }  // namespace sihip

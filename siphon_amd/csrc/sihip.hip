@@ -50,6 +50,7 @@ struct Options {
     int64_t gemmh_min_m = -1;  // smallest M on the F16 GEMM (rule: kGemmhMinM)
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
     int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0 or 1 (gemmq_kernel XM; rule: 1 where it fits)
+    int64_t gemmq_fuse = -1;   // Q8_0-pair GEMM quantizing X itself (XM 2) at 16-row m blocks, 0: off (rule: on)
     int64_t gemm2s_max_m = -1; // largest M on the small-M Q4_K GEMM, 0: none (rule: 16)
     int64_t gemmks_max_m = -1; // largest M on the small-M K-quant GEMM, 0: none (rule: 16)
     int64_t gemmks_q4k = -1;   // Q4_K small M on gemmks.h (1) or gemm2s.h (0) (rule: 0)
@@ -74,6 +75,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
     {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
     {"GEMMQ_XMODE", &Options::gemmq_xmode}, {"Q80_SCALAR", &Options::q80_scalar},
+    {"GEMMQ_FUSE", &Options::gemmq_fuse},
     {"GEMM2S_MAX_M", &Options::gemm2s_max_m}, {"GEMMKS_MAX_M", &Options::gemmks_max_m},
     {"GEMMKS_Q4K", &Options::gemmks_q4k},
     {"GEMMS_WAVES", &Options::gemms_waves},
@@ -1120,6 +1122,7 @@ struct GemmPlan {
     int64_t steps;     // K steps of a tile: super-blocks, or 128-element
                        // steps for the F16 and Q8_0-pair kernels
     int64_t part_bytes;
+    bool fuseq = false;  // Q8_0-pair GEMM that quantizes X itself (gemmq_kernel XM 2)
 };
 
 // K slices of the 16x16 GEMMs: when the output tiles would fill at most
@@ -1191,6 +1194,17 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
                         p.mt <= 4 ? 3 * ctx->n_cu / 4 : 0);
         else
             plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, 5, (p.mt == 1 ? 2 : 3) * ctx->n_cu);
+        // 16-row m blocks whose K slice holds at most two Q8_0 blocks of X
+        // per thread: the launch quantizes X itself (gemmq_kernel XM 2), no
+        // quantization launch before it. At M = 8: config 0 Q4_0 5632 x
+        // 2048 (slices of 6 steps) 13.1 -> 9.2 us, config 4 Q5_0 5120 x 5120
+        // and 1024 x 5120 (5 steps) 16.6 -> 13.7 and 13.4 -> 10.8; with 18-20
+        // steps (2.3-2.5 blocks per thread, 27648 x 5120 and 5120 x 27648)
+        // no faster than the separate launch (32.2 against 32.3, 35.7
+        // against 35.1)
+        p.fuseq = L.type != T_F16 && p.mt == 1 && gq_lds_bytes(16, p.SBK) <= kGQSliceLds &&
+                  std::min<int64_t>(M, 16) * 4 * p.SBK <= 2 * kG2Threads &&
+                  ctx->opt.gemmq_xmode != 0 && ctx->opt.gemmq_fuse != 0;
         return p;
     }
     // (Q4_K: gemm2s.h below, unless the GEMMKS_Q4K option is 1; on the
@@ -1293,8 +1307,8 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
 // the launch first writes the activation planes from X; false when an
 // earlier launch on the stream wrote the same planes (several weights
 // sharing one X and one record layout, sihip_gemm_multi_dev).
-// xmode: the Q8_0-pair GEMM's record mode (gemmq_kernel XM; -1: its rule).
-// Its fused mode uses the last two counters.
+// xmode: the Q8_0-pair GEMM's record mode (gemmq_kernel XM; -1: its rule;
+// the plan's fuseq takes mode 2).
 struct GemmBufs {
     uint8_t *ws;
     float *part;
@@ -1371,7 +1385,8 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     const int64_t lds = gq_lds_bytes(BM, p.SBK);
     int xm = MT <= 2 && lds <= kGQSliceLds ? 1 : 0;
     if (B.xmode == 0) xm = 0;
-    if (B.quant)
+    const bool fused = MT == 1 && p.fuseq;
+    if (B.quant && !fused)
         hipLaunchKernelGGL((gemmq_quantize_x<BM, bias>), dim3((unsigned)((threads + 255) / 256)),
                            dim3(256), 0, st, X, ldx, M, p.Mp, L.n_in, B.ws, B.q80s);
     GQArgs A{};
@@ -1391,6 +1406,15 @@ static hipError_t launch_gemmq(const sihip_weight *w, const GemmPlan &p, const G
     A.part = p.S > 1 ? B.part : nullptr;
     A.cnt = p.S > 1 ? B.cnt : nullptr;
     const int64_t cons = (int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S;
+    if constexpr (MT == 1) {
+        if (fused) {
+            A.xf = X;
+            A.ldx = ldx;
+            hipLaunchKernelGGL((gemmq_kernel<FMT, MT, 2>), dim3((unsigned)cons), dim3(kG2Threads),
+                               (unsigned)lds, st, A);
+            return hipGetLastError();
+        }
+    }
     if constexpr (MT <= 2) {
         if (xm == 1) {
             hipLaunchKernelGGL((gemmq_kernel<FMT, MT, 1>), dim3((unsigned)cons), dim3(kG2Threads),
@@ -1981,6 +2005,10 @@ static int run_gemm_multi(sihip_ctx *ctx, int count, const sihip_weight *const *
             }
         }
     }
+    // a launch that quantizes X itself writes no planes: its key is its own,
+    // so no later launch of its record layout counts on them
+    for (int i = 0; i < count; i++)
+        if (plan[i].fuseq) key[i] = XKey{100 + i, 0, 0};
     // one planes buffer per distinct key, 256-byte aligned, one after another
     size_t off[kMaxSegs], total = 0, part = 0;
     bool first[kMaxSegs];

@@ -437,10 +437,12 @@ def test_gemmq_vs_oracle(dev, oracle, option, wt, n_out, n_in, M, mt, sbk):
 @pytest.mark.parametrize("wt", [sa.Q4_0, sa.Q5_0, sa.Q8_0], ids=lambda t: sa.NAMES[t])
 def test_gemmq_record_modes_match(dev, option, wt):
     """The Q8_0-pair GEMM's record modes give the same bits, call after
-    call: records through the register ring (mode 0) and a K slice's records
-    in LDS up front (1); on weights
-    whose n blocks leave idle workgroups (300 rows), with and without K
-    slices, 16- and 32-row m blocks, and M past a multiple of 8."""
+    call: records through the register ring (mode 0), a K slice's records
+    in LDS up front (1, GEMMQ_FUSE 0) and, with 16-row m blocks, the slice
+    quantized by the launch itself into LDS (1 with its rule: mode 2, no
+    quantization launch); on weights whose n blocks leave idle workgroups
+    (300 rows), with and without K slices, 16- and 32-row m blocks, and M
+    past a multiple of 8."""
     option("GEMMQ_MIN_M", "1")
     rng = np.random.default_rng(4040 + wt)
     cases = [(300, 1280, 5, -1), (27648, 5120, 8, -1), (5120, 27648, 13, -1), (1024, 5120, 16, 0),
@@ -451,8 +453,9 @@ def test_gemmq_record_modes_match(dev, option, wt):
         try:
             option("GEMM_SBK", str(sbk))
             outs = []
-            for mode in ("0", "1", "0"):
+            for mode, fuse in (("0", "-1"), ("1", "0"), ("1", "-1"), ("0", "-1")):
                 option("GEMMQ_XMODE", mode)
+                option("GEMMQ_FUSE", fuse)
                 X = _rows(np.random.default_rng(n_out + M), M, n_in)
                 outs.append(dev.gemm(w, X).view(np.uint32))
             what = f"{sa.NAMES[wt]} {n_out}x{n_in} M={M} SBK={sbk}"

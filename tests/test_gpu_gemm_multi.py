@@ -42,8 +42,9 @@ def _run(dev, ws, X, multi=True):
 # plan): the Llama-3-8B Q4_K_M q/k/v group on the 16x16 kernels (wq and wv
 # in 64-row blocks; wk, 32-row blocks on its own, joins them),
 # a gate/up pair at a batch size on the 32-row kernel, a group of four
-# record layouts (Q5_0, Q8_0, F16, Q4_K), and a batch below every
-# matrix-core threshold (the matvec kernel per weight)
+# record layouts (Q5_0, Q8_0, F16, Q4_K), a batch below every
+# matrix-core threshold (the matvec kernel per weight), and a Q8_0-pair
+# launch that quantizes X itself ahead of one that needs the planes
 GROUPS = [
     ("qkv-q4km-M512", [(sa.Q4_K, 4096), (sa.Q4_K, 1024), (sa.Q6_K, 1024)], 4096, 512, (2,)),
     ("gate-up-q4k-M512", [(sa.Q4_K, 2816), (sa.Q4_K, 2816)], 1024, 512, ()),
@@ -53,6 +54,10 @@ GROUPS = [
     ("gate-up-q4k-M8", [(sa.Q4_K, 2048), (sa.Q4_K, 2048)], 2048, 8, (0, 1)),
     ("mixed-M40", [(sa.Q5_0, 640), (sa.Q8_0, 384), (sa.F16, 512), (sa.Q4_K, 300)], 2048, 40, ()),
     ("matvec-M2", [(sa.Q4_K, 700), (sa.Q6_K, 300), (sa.Q5_0, 260)], 1024, 2, (0, 1, 2)),
+    # one record layout, a launch that quantizes X itself (640 rows: K
+    # slices of 6 steps in LDS) before one that reads the shared planes
+    # (13312 rows: slices of 32 steps, past the LDS image)
+    ("q50-fused-then-ring-M5", [(sa.Q5_0, 640), (sa.Q5_0, 13312)], 16384, 5, (0, 1)),
 ]
 
 

@@ -66,7 +66,8 @@ def oracle_rows(oracle, wt, W, n_in, xq):
 @pytest.mark.parametrize("M", [1, 8])
 def test_gemv_gemm_scalar_activations(dev, oracle, option, wt, M):
     """Batch 1 runs the matvec kernel (the quantizer in its prologue),
-    batch 8 the matrix-core GEMM (its quantization launch)."""
+    batch 8 the matrix-core GEMM (16-row m blocks: the quantizer in the
+    GEMM launch's own prologue)."""
     rng = np.random.default_rng(400 + wt + M)
     n_out, n_in = 96, 1024
     W = synth.make_weights(wt, n_out, n_in, rng)
