@@ -5,7 +5,8 @@
 #include <stdint.h>
 
 // The cross-workgroup hand-off of K-slice and column-slice partial sums
-// (slices_finish here, split_reduce in matvec.h) relies on what gfx950 does,
+// (slices_finish here, g2_slices_finish in gemm2.h, kf_finish in gemmkf.h,
+// split_reduce in matvec.h) relies on what gfx950 does,
 // not on the HIP memory model: sc1 stores and loads bypass the per-XCD L2,
 // s_waitcnt vmcnt(0) waits for a wave's stores to complete before its
 // workgroup counts its arrival with a relaxed agent-scope atomic, and the
