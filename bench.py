@@ -348,8 +348,11 @@ def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
     rows and runs the MFMA GEMM; enough weight copies rotate that more than
     `rotate_bytes` of GGUF bytes (fewer than any GEMM-ordered copy holds)
     stream between two reads of one copy, so the 256 MB Infinity Cache cannot
-    serve them. The first call per copy builds its GEMM-ordered copy and is
-    excluded (warm-up)."""
+    serve them. The first call per copy builds its GEMM-ordered copy; three
+    untimed passes over the copies precede the four timed ones (a copy's
+    kernel time drifts down by up to 13% over the first hundred calls after
+    a pause, so a short window would time the drift, not the sustained
+    rate)."""
     import siphon_amd as sa
     from siphon_amd import synth
     n_out, n_in = 14336, 4096
@@ -362,10 +365,11 @@ def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
         X = torch.randn(M, n_in, device="cuda")
         Y = torch.empty(M, n_out, device="cuda")
         with torch.cuda.stream(stream):
-            for w in ws:
-                dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
+            for _ in range(3):
+                for w in ws:
+                    dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
         torch.cuda.synchronize()
-        reps = 2 * len(ws)
+        reps = 4 * len(ws)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         with torch.cuda.stream(stream):
@@ -391,10 +395,11 @@ def bench_gemm(dev, torch, stream, rng, rotate_bytes=512 << 20):
         Wf = synth.make_weights(wt, n_out, n_in, rng)
         wf = [dev.upload(wt, n_out, n_in, Wf) for _ in range(-(-rotate_bytes // Wf.nbytes) + 1)]
         with torch.cuda.stream(stream):
-            for w in wf:
-                dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
+            for _ in range(3):
+                for w in wf:
+                    dev.gemm_dev(w, X.data_ptr(), M, Y.data_ptr(), sp)
         torch.cuda.synchronize()
-        reps = 2 * len(wf)
+        reps = 4 * len(wf)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         with torch.cuda.stream(stream):
