@@ -1771,16 +1771,29 @@ static int64_t gemmkf_tiles(const Layout &L) {
 }
 
 // K slices of a fused launch over `tiles` tiles: as many as keep the grid
-// within two workgroups per CU, at least two super-blocks each (a slice's
-// fixed cost, its partial sums and the last workgroup's sum, outweighs one
-// super-block: Llama-3-8B wo 4096 x 4096 at M = 8 takes 13.0 us per call in
-// 16 slices of one, 9.7 in 8 of two, 10.6 in 4 of four), and at most
-// kKFMaxSBK super-blocks per slice (its LDS image); the GEMMKF_SBK option
-// sets the slice length (0: the fewest slices).
+// within one workgroup per CU, or within two where one per CU would leave
+// slices of more than 16 super-blocks; at least two super-blocks each (a
+// slice's fixed cost, its partial sums and the last workgroup's sum,
+// outweighs one super-block: Llama-3-8B wo 4096 x 4096 at M = 8 takes 10.4
+// us per call in 16 slices of one, 7.7 in 8 of two, 8.1 in 4 of four), and
+// at most kKFMaxSBK super-blocks per slice (its LDS image); the GEMMKF_SBK
+// option sets the slice length (0: the fewest slices). Measured at M = 8
+// with the partial tiles in register order: one workgroup per CU against
+// two, q/k/v 10.3 against 10.8 us (4 slices against 8), gate + up 17.6
+// against 18.2 (no slices against 2), ffn_down 15.9 against 17.5 (8 slices
+// against 14), config 4 attn 5120 x 5120 Q2_K 8.6 against 10.5; the 108
+// super-blocks of config 4's 5120 x 27648 ffn_down in 6 slices of 18 took
+// 21.6 against 19.8 us in 12 of 9 (Q2_K), hence two per CU past 16.
 static void gemmkf_slices(const sihip_ctx *ctx, int64_t tiles, int64_t nb, int &S, int &SBK) {
-    int64_t s = 2 * (int64_t)ctx->n_cu / (tiles > 0 ? tiles : 1);
-    if (s < 1) s = 1;
-    if (s > (nb + 1) / 2) s = (nb + 1) / 2;
+    const int64_t t = tiles > 0 ? tiles : 1;
+    auto slices = [&](int64_t per_cu) {
+        int64_t v = per_cu * (int64_t)ctx->n_cu / t;
+        if (v < 1) v = 1;
+        if (v > (nb + 1) / 2) v = (nb + 1) / 2;
+        return v;
+    };
+    int64_t s = slices(1);
+    if ((nb + s - 1) / s > 16) s = slices(2);
     int64_t sbk = (nb + s - 1) / s;
     if (ctx->opt.gemmkf_sbk == 0) sbk = nb;
     else if (ctx->opt.gemmkf_sbk > 0) sbk = ctx->opt.gemmkf_sbk;
