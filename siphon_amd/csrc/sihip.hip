@@ -1243,8 +1243,10 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
         // digits streamed) about one workgroup per CU is fastest (M = 8:
         // ffn_down 4096 x 14336 in 224 workgroups 25.6 us against 29.5 in
         // 448; 27648 x 5120 unsliced 48.4 against 54.8), with 64-row blocks
-        // two (ffn_down at M = 512: 83.8 us in 512 against 107 in 256)
-        plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB, 2, p.mt <= 2 ? ctx->n_cu : 0);
+        // two (ffn_down at M = 512: 83.8 us in 512 against 107 in 256), at
+        // least 4 super-blocks per slice (wv 1024 x 4096 at M = 512: 20.3 us
+        // in 4 slices of 4 against 22.8 in 8 of 2)
+        plan_slices(ctx, p, (p.Mp / BM) * NB, nb, NB, 4, p.mt <= 2 ? ctx->n_cu : 0);
         return p;
     }
     if (L.type == T_Q4_K && M <= gemm2s_max_m(ctx->opt)) {
