@@ -409,13 +409,14 @@ def test_f16_rows_not_multiple_of_128_take_the_matvec(dev, oracle):
 @pytest.mark.parametrize("wt", [sa.Q4_0, sa.Q5_0, sa.Q8_0], ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("n_out,n_in,M,mt,sbk", [
     (27648, 5120, 8, -1, -1), (5120, 27648, 8, -1, -1), (300, 1280, 70, 4, 0), (129, 384, 33, 2, 1),
-    (4864, 896, 16, -1, -1), (64, 896, 3, 1, -1),
+    (4864, 896, 16, -1, -1), (64, 896, 3, 1, -1), (200, 1024, 40, 1, -1),
 ])
 def test_gemmq_vs_oracle(dev, oracle, option, wt, n_out, n_in, M, mt, sbk):
     """The Q4_0 / Q5_0 / Q8_0 GEMM (gemmq.h) at the config-4 batch-8 shapes
     and config 1's 4864 x 896, every m-tile height, with and without K
-    slices, rows at the ends of the quant ranges, against the oracle; a
-    repeat gives the same bits."""
+    slices, the launch that quantizes X itself with one and with three
+    16-row m blocks (M = 40 at GEMM_MT 1), rows at the ends of the quant
+    ranges, against the oracle; a repeat gives the same bits."""
     option("GEMMQ_MIN_M", "1")
     option("GEMM_MT", str(mt))
     option("GEMM_SBK", str(sbk))
