@@ -112,9 +112,13 @@ struct MVArgs {
 // remaining passes. XP > 1 is used for long rows (n_in > 4096) by kernels
 // whose register budget has room for the extra values.
 
+// Passes of 64 Q8_0 blocks whose x values a thread loads together.
+constexpr int kQ80Passes = 4;
+
 template <int XP>
 struct XFirst {
-    float4 t[XP][4];
+    float4 t[XP][4];            // Q8_K: the first XP passes
+    float2 h[kQ80Passes][4];    // Q8_0 (4 lanes per block): the first passes
 };
 
 // 16 lanes quantize one block: thread tid owns block (tid >> 4) + 16 p of
@@ -134,6 +138,28 @@ __device__ inline void stage_q8k_first(const MVArgs &a, XFirst<XP> &xf, int64_t 
             for (int i = 0; i < 4; i++) xf.t[p][i] = src[i];
         }
     }
+}
+
+// Q8_0 from f32 with the SIMD quantizer: a quad of lanes quantizes one
+// block (q80_quad_v); thread tid owns block (tid >> 2) + 64 p of pass p,
+// and loads the x values of kQ80Passes passes together. The first ones are
+// loaded here, before the first weight batch, as for Q8_K.
+__device__ inline void q80_load_passes(const float *xc, int64_t p0, int64_t nbl,
+                                       float2 (&t)[kQ80Passes][4]) {
+#pragma unroll
+    for (int p = 0; p < kQ80Passes; p++) {
+        if (p0 + 64 * p < nbl) {  // wave-uniform
+            int64_t b = p0 + 64 * p + (threadIdx.x >> 2);
+            b = b < nbl ? b : nbl - 1;  // clamped: the load stays in the range
+            q80_quad_load(xc + b * 32, threadIdx.x & 3, t[p]);
+        }
+    }
+}
+
+template <int XP>
+__device__ inline void stage_q80_first(const MVArgs &a, XFirst<XP> &xf, int64_t b0, int64_t nbl) {
+    if (!a.x || a.q80s) return;
+    q80_load_passes(a.x + b0 * 32, 0, nbl, xf.h);
 }
 
 __device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int lane16,
@@ -199,6 +225,41 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             const int64_t nb = n / 32;
             float *dcol = reinterpret_cast<float *>(col + n);
             int *scol = reinterpret_cast<int *>(col + n + nb * 4);
+            if (a.x && !a.q80s) {
+                // every lane runs every pass (the quads exchange values), lanes
+                // past the last block on a clamped copy whose results are not
+                // stored
+                const int j = tid & 3;
+                const float *xc = a.x + c * a.ldx + b0 * 32;
+                for (int64_t p0 = 0; p0 < nbl; p0 += 64 * kQ80Passes) {
+                    float2 t[kQ80Passes][4];
+                    if (c == 0 && p0 == 0) {
+#pragma unroll
+                        for (int p = 0; p < kQ80Passes; p++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++) t[p][i] = xf.h[p][i];
+                    } else {
+                        q80_load_passes(xc, p0, nbl, t);
+                    }
+#pragma unroll
+                    for (int p = 0; p < kQ80Passes; p++) {
+                        if (p0 + 64 * p < nbl) {  // wave-uniform
+                            const int64_t b = p0 + 64 * p + (tid >> 2);
+                            const Q80Quad r = q80_quad_v(t[p]);
+                            if (b < nbl) {
+                                uint16_t *q16 = reinterpret_cast<uint16_t *>(col + b * 32);
+#pragma unroll
+                                for (int i = 0; i < 4; i++) q16[4 * i + j] = (uint16_t)r.q2[i];
+                                if (j == 0) {
+                                    dcol[b] = r.d;
+                                    scol[b] = r.sum;
+                                }
+                            }
+                        }
+                    }
+                }
+                continue;
+            }
             for (int64_t b = tid; b < nbl; b += kThreads) {
                 uint32_t q[8];
                 float d;
@@ -467,6 +528,7 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     Buf<FMT> bufA, bufB;
     XFirst<XP> xf;
     if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf, b0, b1 - b0);
+    if constexpr (PAIR == T_Q8_0) stage_q80_first<XP>(A, xf, b0, b1 - b0);
     issue(bufA);
     stage_activations<PAIR, XP>(A, lds, xf, b0, b1 - b0, n_loc);
     if (total == 1) {  // one round: no second buffer (it would reload the same round)

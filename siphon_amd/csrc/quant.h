@@ -315,6 +315,71 @@ __device__ inline Q80Block q80_block_scalar(const float *x) {
     return q80_block_scalar_v(v);
 }
 
+// q80_block_v spread over the 4 lanes of a quad (lanes 4i .. 4i+3 of a
+// wave, all active): lane j of the quad holds elements 8i + 2j and
+// 8i + 2j + 1 (i = 0..3), which are lanes 2j and 2j + 1 of the four 8-float
+// vectors the abs-max runs over, so those lanes' maxima are the quad lane's
+// own; the rest of the tree runs, in q80_block_v's order, in every lane on
+// the 8 values broadcast from the quad. Quants stay with their lanes:
+// q2[i] holds elements 8i + 2j (low byte) and 8i + 2j + 1. The sum is the
+// quad's total.
+struct Q80Quad {
+    uint16_t dbits;
+    float d;
+    int sum;
+    uint32_t q2[4];
+};
+
+__device__ inline void q80_quad_load(const float *blk, int j, float2 (&t)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) t[i] = *reinterpret_cast<const float2 *>(blk + 8 * i + 2 * j);
+}
+
+template <int J>
+__device__ inline float quad_bcast(float v) {  // quad_perm [J, J, J, J]
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), J * 0x55, 0xf, 0xf, false));
+}
+
+__device__ inline Q80Quad q80_quad_v(const float2 (&t)[4]) {
+    float a0 = fabsf(t[0].x), a1 = fabsf(t[0].y);
+#pragma unroll
+    for (int i = 1; i < 4; i++) {
+        a0 = vmaxsel(a0, fabsf(t[i].x));
+        a1 = vmaxsel(a1, fabsf(t[i].y));
+    }
+    const float lane[8] = {quad_bcast<0>(a0), quad_bcast<0>(a1), quad_bcast<1>(a0), quad_bcast<1>(a1),
+                           quad_bcast<2>(a0), quad_bcast<2>(a1), quad_bcast<3>(a0), quad_bcast<3>(a1)};
+    float m4[4], m2[2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) m4[k] = vmaxsel(lane[4 + k], lane[k]);
+#pragma unroll
+    for (int k = 0; k < 2; k++) m2[k] = vmaxsel(m4[k], m4[k + 2]);
+    const float mx = vmaxsel(m2[0], m2[1]);
+    Q80Quad b;
+    b.dbits = f32_to_f16_bits(mx / 127.0f);
+    b.d = f16_bits_to_f32(b.dbits);
+    const float id = (mx != 0.0f) ? 127.0f / mx : 0.0f;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float e[2] = {t[i].x, t[i].y};
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const float r = __builtin_rintf(__fmul_rn(e[k], id));
+            int q = cvt_i32_indef(r);
+            q = q > 127 ? 127 : (q < -128 ? -128 : q);
+            s += q;
+            w |= (uint32_t)(q & 0xff) << (8 * k);
+        }
+        b.q2[i] = w;
+    }
+    s += __builtin_amdgcn_mov_dpp(s, kDppXor1, 0xf, 0xf, false);
+    s += __builtin_amdgcn_mov_dpp(s, kDppXor2, 0xf, 0xf, false);
+    b.sum = s;
+    return b;
+}
+
 // The Q8_0 quantizer a launch uses: the SIMD semantics (q80_block), or
 // the scalar ones when `scalar` is set (a wave-uniform launch argument).
 __device__ inline Q80Block q80_block_sel(const float *x, int scalar) {

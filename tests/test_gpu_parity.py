@@ -138,6 +138,38 @@ def test_gemv_f32_vs_oracle(dev, oracle, wt):
         w.free()
 
 
+@pytest.mark.parametrize("wt", [sa.Q8_0, sa.Q5_0, sa.Q4_0], ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("n_in", [32, 896, 2048, 5120, 9216])
+def test_gemv_q80_prologue_bitexact(dev, oracle, option, wt, n_in):
+    """The matvec's own Q8_0 quantization of an f32 activation (a quad of
+    lanes per block, one or more passes of 64 blocks) stages the same LDS
+    image as the oracle's quantized activation: gemv from f32 is bit for bit
+    gemv_pair on oracle.quantize(x) with the same tile width, on the edge
+    vectors and on blocks holding inf and NaN."""
+    rng = np.random.default_rng(4100 + wt * 7 + n_in)
+    n_out = 96
+    W = synth.make_weights(wt, n_out, n_in, rng)
+    vecs = edge_vectors(rng, max(n_in, 512))
+    v = rng.standard_normal(n_in).astype(np.float32)
+    v[min(40, n_in - 1)] = np.inf
+    v[n_in - 3] = np.nan
+    vecs.append(v)
+    # rows of 9216 also unsliced: 288 blocks, two groups of four passes
+    for G, split in [(4, -1), (16, -1)] + ([(16, 0)] if n_in == 9216 else []):
+        option("TILE_COLS", str(G))
+        option("SPLIT_ELEMS", split)
+        w = dev.upload(wt, n_out, n_in, W)
+        try:
+            for i, x in enumerate(vecs):
+                x = x[:n_in].copy()
+                y = dev.gemv(w, x)
+                yp = dev.gemv_pair(wt, n_out, n_in, W, oracle.quantize(sa.Q8_0, x))
+                assert np.array_equal(y.view(np.uint32), yp.view(np.uint32)), \
+                    f"{sa.NAMES[wt]} n_in={n_in} G={G} split={split} vector {i}"
+        finally:
+            w.free()
+
+
 @pytest.mark.parametrize("wt", [sa.Q4_K, sa.Q5_K, sa.Q2_K, sa.Q3_K, sa.Q6_K, sa.Q8_0, sa.Q5_0, sa.Q4_0,
                                 sa.F16, sa.F32], ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("M", [1, 3, 8, 13])
