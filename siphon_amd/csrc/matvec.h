@@ -115,10 +115,14 @@ struct MVArgs {
 // Passes of 64 Q8_0 blocks whose x values a thread loads together.
 constexpr int kQ80Passes = 4;
 
+// float4s of an F16 activation a thread loads together.
+constexpr int kF16Vecs = 8;
+
 template <int XP>
 struct XFirst {
     float4 t[XP][4];            // Q8_K: the first XP passes
     float2 h[kQ80Passes][4];    // Q8_0 (4 lanes per block): the first passes
+    float4 f[kF16Vecs];         // F16: the first group
 };
 
 // 16 lanes quantize one block: thread tid owns block (tid >> 4) + 16 p of
@@ -160,6 +164,27 @@ template <int XP>
 __device__ inline void stage_q80_first(const MVArgs &a, XFirst<XP> &xf, int64_t b0, int64_t nbl) {
     if (!a.x || a.q80s) return;
     q80_load_passes(a.x + b0 * 32, 0, nbl, xf.h);
+}
+
+// F16 from f32: thread tid converts float4s tid + kThreads v of each group
+// of kThreads * kF16Vecs, whose loads it issues together; the first group
+// is loaded before the first weight batch.
+__device__ inline void f16_load_group(const float *xc, int64_t v0, int64_t nvec,
+                                      float4 (&f)[kF16Vecs]) {
+#pragma unroll
+    for (int v = 0; v < kF16Vecs; v++) {
+        if (v0 + kThreads * v < nvec) {  // wave-uniform
+            int64_t i = v0 + kThreads * v + threadIdx.x;
+            i = i < nvec ? i : nvec - 1;  // clamped: the load stays in the range
+            f[v] = reinterpret_cast<const float4 *>(xc)[i];
+        }
+    }
+}
+
+template <int XP>
+__device__ inline void stage_f16_first(const MVArgs &a, XFirst<XP> &xf, int64_t b0, int64_t nbl) {
+    if (!a.x) return;
+    f16_load_group(a.x + b0 * 32, 0, nbl * 8, xf.f);
 }
 
 __device__ inline void q8k_stage_block(uint8_t *col, int64_t n, int64_t b, int lane16,
@@ -293,8 +318,29 @@ __device__ inline void stage_activations(const MVArgs &a, uint8_t *lds, const XF
             uint16_t *h = reinterpret_cast<uint16_t *>(col);
             if (a.x) {
                 const float *xc = a.x + c * a.ldx + b0 * 32;
-                for (int64_t i = tid; i < nbl * 32; i += kThreads)
-                    h[i] = __builtin_bit_cast(uint16_t, (_Float16)xc[i]);
+                const int64_t nvec = nbl * 8;
+                for (int64_t v0 = 0; v0 < nvec; v0 += kThreads * kF16Vecs) {
+                    float4 f[kF16Vecs];
+                    if (c == 0 && v0 == 0) {
+#pragma unroll
+                        for (int v = 0; v < kF16Vecs; v++) f[v] = xf.f[v];
+                    } else {
+                        f16_load_group(xc, v0, nvec, f);
+                    }
+#pragma unroll
+                    for (int v = 0; v < kF16Vecs; v++) {
+                        const int64_t i = v0 + kThreads * v + tid;
+                        if (v0 + kThreads * v < nvec && i < nvec) {
+                            const uint32_t lo =
+                                (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[v].x) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[v].y) << 16);
+                            const uint32_t hi =
+                                (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[v].z) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[v].w) << 16);
+                            *reinterpret_cast<uint2 *>(h + 4 * i) = make_uint2(lo, hi);
+                        }
+                    }
+                }
             } else {
                 const uint16_t *src = reinterpret_cast<const uint16_t *>(a.xq + c * a.ldxq) + b0 * 32;
                 for (int64_t i = tid; i < nbl * 32; i += kThreads) h[i] = src[i];
@@ -529,6 +575,7 @@ __device__ inline void matvec_body(const MVArgs &A, const MVSeg &sg, uint8_t *ld
     XFirst<XP> xf;
     if constexpr (PAIR == T_Q8_K) stage_q8k_first<XP>(A, xf, b0, b1 - b0);
     if constexpr (PAIR == T_Q8_0) stage_q80_first<XP>(A, xf, b0, b1 - b0);
+    if constexpr (PAIR == T_F16) stage_f16_first<XP>(A, xf, b0, b1 - b0);
     issue(bufA);
     stage_activations<PAIR, XP>(A, lds, xf, b0, b1 - b0, n_loc);
     if (total == 1) {  // one round: no second buffer (it would reload the same round)

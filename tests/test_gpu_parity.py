@@ -138,14 +138,15 @@ def test_gemv_f32_vs_oracle(dev, oracle, wt):
         w.free()
 
 
-@pytest.mark.parametrize("wt", [sa.Q8_0, sa.Q5_0, sa.Q4_0], ids=lambda t: sa.NAMES[t])
+@pytest.mark.parametrize("wt", [sa.Q8_0, sa.Q5_0, sa.Q4_0, sa.F16], ids=lambda t: sa.NAMES[t])
 @pytest.mark.parametrize("n_in", [32, 896, 2048, 5120, 9216])
-def test_gemv_q80_prologue_bitexact(dev, oracle, option, wt, n_in):
-    """The matvec's own Q8_0 quantization of an f32 activation (a quad of
-    lanes per block, one or more passes of 64 blocks) stages the same LDS
-    image as the oracle's quantized activation: gemv from f32 is bit for bit
-    gemv_pair on oracle.quantize(x) with the same tile width, on the edge
-    vectors and on blocks holding inf and NaN."""
+def test_gemv_prologue_bitexact(dev, oracle, option, wt, n_in):
+    """The matvec's own conversion of an f32 activation (Q8_0: a quad of
+    lanes per block, passes of 64 blocks loaded four at a time; F16: groups
+    of 8 float4 per thread) stages the same LDS image as the oracle's
+    converted activation: gemv from f32 is bit for bit gemv_pair on
+    oracle.quantize(x) with the same tile width, on the edge vectors and on
+    blocks holding inf and NaN."""
     rng = np.random.default_rng(4100 + wt * 7 + n_in)
     n_out = 96
     W = synth.make_weights(wt, n_out, n_in, rng)
@@ -154,7 +155,8 @@ def test_gemv_q80_prologue_bitexact(dev, oracle, option, wt, n_in):
     v[min(40, n_in - 1)] = np.inf
     v[n_in - 3] = np.nan
     vecs.append(v)
-    # rows of 9216 also unsliced: 288 blocks, two groups of four passes
+    # rows of 9216 also unsliced: 288 blocks, two groups of four Q8_0 passes
+    # or of eight float4 per thread
     for G, split in [(4, -1), (16, -1)] + ([(16, 0)] if n_in == 9216 else []):
         option("TILE_COLS", str(G))
         option("SPLIT_ELEMS", split)
@@ -163,7 +165,7 @@ def test_gemv_q80_prologue_bitexact(dev, oracle, option, wt, n_in):
             for i, x in enumerate(vecs):
                 x = x[:n_in].copy()
                 y = dev.gemv(w, x)
-                yp = dev.gemv_pair(wt, n_out, n_in, W, oracle.quantize(sa.Q8_0, x))
+                yp = dev.gemv_pair(wt, n_out, n_in, W, oracle.quantize(sa.PAIR[wt], x))
                 assert np.array_equal(y.view(np.uint32), yp.view(np.uint32)), \
                     f"{sa.NAMES[wt]} n_in={n_in} G={G} split={split} vector {i}"
         finally:
