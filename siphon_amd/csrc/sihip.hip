@@ -404,6 +404,23 @@ static int choose_G(const Options &o, uint32_t type, int64_t n_out, int64_t n_in
     // walks 80 units of a 27648 x 5120 Q5_0 or F16 row lost 3-32% to tiles
     // 16 wide); a row of one column keeps one lane.
     const int min_g = ncols >= 2 ? 2 : 1;
+    // Unit columns (Q4_0, Q5_0, Q8_0, F16): where the narrowest tile with at
+    // most 6 rounds per lane (80% of the lanes busy) gives 512-4096 row
+    // tiles, it is taken. The tile-count rule below leaves 2 or 3 rounds
+    // there, or 10: Q8_0 4864 x 896 4.77 us at 16 wide against 4.14 at 8,
+    // Q5_0 5120 x 5120 9.47 at 16 against 8.01 at 32, Q5_0 and F16
+    // 1024 x 5120 5.45 and 6.32 at 64 against 5.28 and 5.83 at 32. Fewer
+    // tiles (896 x 896, 128 x 896: 4.0 and 3.8 us at 8 wide, 3.5 at 32) or
+    // more (27648-row and 151936-row matrices) keep the tile-count rule.
+    if (!is_kquant(type)) {
+        for (int G = min_g; G <= 64; G *= 2) {
+            const int64_t S = (ncols + G - 1) / G;
+            if (S > 6 || ncols * 100 < S * G * 80) continue;
+            const int64_t tiles = (n_out + 64 / G - 1) / (64 / G);
+            if (tiles >= 512 && tiles <= 4096) return G;
+            break;
+        }
+    }
     auto pick = [&](int pct, int64_t max_rounds) {
         int best = 0;
         int64_t best_tiles = 0;
