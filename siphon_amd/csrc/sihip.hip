@@ -1206,11 +1206,20 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
         // 5120 unsliced, 216 workgroups, 47.6 us against 53.6 in 432;
         // 5120 x 27648 in 160, 52.8 against 56.5 in 480; kv 1024 x 5120 in
         // 64, 8.6 against 12.6 in 160), 128-row blocks at two per CU.
+        // Q8_0 pairs in 16-row m blocks take slices of 3 steps or more, which
+        // on the shapes below makes them 4 steps (512 elements) long; rows of
+        // 896 (7 steps) get two. At M = 8, slices of 4 steps against the
+        // earlier 5-step floor: config 0 Q4_0 5632 x 2048 9.2 -> 8.5 us,
+        // 2048 x 2048 9.0 -> 8.2, 256 x 2048 8.7 -> 7.6, Q8_0 4864 x 896
+        // (unsliced before) 8.75 -> 8.14, 896 x 896 8.4 -> 7.8, 896 x 4864
+        // 10.7 -> 10.4, Q5_0 5120 x 5120 and 1024 x 5120 unchanged (13.6,
+        // 10.8); 2- and 3-step slices were slower on all but 896 x 896.
         if (L.type == T_F16)
             plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, p.mt <= 4 ? 5 : 2,
                         p.mt <= 4 ? 3 * ctx->n_cu / 4 : 0);
         else
-            plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, 5, (p.mt == 1 ? 2 : 3) * ctx->n_cu);
+            plan_slices(ctx, p, (p.Mp / BM) * NB, nk, NB, p.mt == 1 ? 3 : 5,
+                        (p.mt == 1 ? 2 : 3) * ctx->n_cu);
         // 16-row m blocks whose K slice holds at most two Q8_0 blocks of X
         // per thread: the launch quantizes X itself (gemmq_kernel XM 2), no
         // quantization launch before it. At M = 8: config 0 Q4_0 5632 x
