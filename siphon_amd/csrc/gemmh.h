@@ -103,11 +103,17 @@ struct GHArgs {
     int S, SBK;           // K slices: slice s covers steps [s SBK, (s + 1) SBK)
     float *part;          // part[(s Mp + m) * NB * 128 + n]
     uint32_t *cnt;        // cnt[mblk * NB + nblk], zero between launches
+    const float *xf;      // XF: X itself, f32, X[m * ldx + k]
+    int64_t ldx;
 };
 
 // At least two waves per SIMD, no upper bound: the register count (80
 // VGPRs at MT = 1 to 248 at MT = 8) sets the occupancy.
-template <int MT>
+//
+// XF: the workgroup converts its own steps of X (A.xf) into the records as
+// it stages them, with gemmh_convert_x's conversion and placement, instead
+// of reading records that a conversion launch wrote (A.x).
+template <int MT, bool XF>
 __global__ __launch_bounds__(kG2Threads)
 __attribute__((amdgpu_waves_per_eu(2))) void gemmh_f16_kernel(GHArgs A) {
     constexpr int BM = 16 * MT;
@@ -136,20 +142,45 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemmh_f16_kernel(GHArgs A) {
     const int v_op = lane * 16;
 
     uint4 xs[kXPT];
+    float4 xv[kXPT][2];  // XF
     auto load_x = [&](int c) {
 #pragma unroll
         for (int k = 0; k < kXPT; k++) {
             const int i = (int)threadIdx.x + kG2Threads * k;
-            if (kXP % kG2Threads == 0 || i < kXP)
-                xs[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      xr, (int)threadIdx.x * 16, c * kRec + 4096 * k, 0));
+            if (kXP % kG2Threads == 0 || i < kXP) {
+                if constexpr (XF) {
+                    // piece i of the record: fragment (mt, ks) = i / 64, lane
+                    // i % 64 (row 16 mt + l % 16, elements 32 ks + 8 (l / 16)
+                    // of the step); rows past M stay zero
+                    const int fr = i >> 6, l = i & 63;
+                    const int64_t m = (int64_t)mblk * BM + 16 * (fr >> 2) + (l & 15);
+                    xv[k][0] = xv[k][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (m < A.M) {
+                        const float *src = A.xf + m * A.ldx + 128 * c + 32 * (fr & 3) + 8 * (l >> 4);
+                        xv[k][0] = reinterpret_cast<const float4 *>(src)[0];
+                        xv[k][1] = reinterpret_cast<const float4 *>(src)[1];
+                    }
+                } else {
+                    xs[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          xr, (int)threadIdx.x * 16, c * kRec + 4096 * k, 0));
+                }
+            }
         }
     };
     auto store_x = [&](uint8_t *dst) {
 #pragma unroll
         for (int k = 0; k < kXPT; k++) {
             const int i = (int)threadIdx.x + kG2Threads * k;
-            if (kXP % kG2Threads == 0 || i < kXP) *reinterpret_cast<uint4 *>(dst + i * 16) = xs[k];
+            if (kXP % kG2Threads == 0 || i < kXP) {
+                if constexpr (XF) {
+                    const float4 a = xv[k][0], b = xv[k][1];
+                    *reinterpret_cast<v8hh_t *>(dst + i * 16) =
+                        (v8hh_t){(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                                 (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+                } else {
+                    *reinterpret_cast<uint4 *>(dst + i * 16) = xs[k];
+                }
+            }
         }
     };
     v8hh_t bw[4][2];

@@ -51,6 +51,7 @@ struct Options {
     int64_t gemmq_min_m = -1;  // smallest M on the Q4_0/Q5_0/Q8_0 GEMM (rule: kGemmqMinM)
     int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0 or 1 (gemmq_kernel XM; rule: 1 where it fits)
     int64_t gemmq_fuse = -1;   // Q8_0-pair GEMM quantizing X itself (XM 2) at 16-row m blocks, 0: off (rule: on)
+    int64_t gemmh_fuse = -1;   // F16 GEMM converting X itself (XF) at 16-row m blocks, 0: off (rule: on)
     int64_t gemm2s_max_m = -1; // largest M on the small-M Q4_K GEMM, 0: none (rule: 16)
     int64_t gemmks_max_m = -1; // largest M on the small-M K-quant GEMM, 0: none (rule: 16)
     int64_t gemmks_q4k = -1;   // Q4_K small M on gemmks.h (1) or gemm2s.h (0) (rule: 0)
@@ -75,7 +76,7 @@ static const OptionName kOptionNames[] = {
     {"GEMM2_WAVES", &Options::gemm2_waves}, {"GEMM6_MIN_M", &Options::gemm6_min_m},
     {"GEMMH_MIN_M", &Options::gemmh_min_m}, {"GEMMQ_MIN_M", &Options::gemmq_min_m},
     {"GEMMQ_XMODE", &Options::gemmq_xmode}, {"Q80_SCALAR", &Options::q80_scalar},
-    {"GEMMQ_FUSE", &Options::gemmq_fuse},
+    {"GEMMQ_FUSE", &Options::gemmq_fuse}, {"GEMMH_FUSE", &Options::gemmh_fuse},
     {"GEMM2S_MAX_M", &Options::gemm2s_max_m}, {"GEMMKS_MAX_M", &Options::gemmks_max_m},
     {"GEMMKS_Q4K", &Options::gemmks_q4k},
     {"GEMMS_WAVES", &Options::gemms_waves},
@@ -1139,7 +1140,8 @@ struct GemmPlan {
     int64_t steps;     // K steps of a tile: super-blocks, or 128-element
                        // steps for the F16 and Q8_0-pair kernels
     int64_t part_bytes;
-    bool fuseq = false;  // Q8_0-pair GEMM that quantizes X itself (gemmq_kernel XM 2)
+    bool fuseq = false;  // a GEMM that quantizes or converts X itself (gemmq_kernel XM 2,
+                         // gemmh_f16_kernel XF)
 };
 
 // K slices of the 16x16 GEMMs: when the output tiles would fill at most
@@ -1231,6 +1233,10 @@ static GemmPlan plan_gemm(const sihip_ctx *ctx, const Layout &L, int64_t M, int 
         p.fuseq = L.type != T_F16 && p.mt == 1 && gq_lds_bytes(16, p.SBK) <= kGQSliceLds &&
                   std::min<int64_t>(M, 16) * 4 * p.SBK <= 2 * kG2Threads &&
                   ctx->opt.gemmq_xmode != 0 && ctx->opt.gemmq_fuse != 0;
+        // F16 in 16-row m blocks converts X as it stages each step's record
+        // (a 4 KB record: one 32-byte f32 read per thread and step), with no
+        // conversion launch before it
+        if (L.type == T_F16) p.fuseq = p.mt == 1 && ctx->opt.gemmh_fuse != 0;
         return p;
     }
     // (Q4_K: gemm2s.h below, unless the GEMMKS_Q4K option is 1; on the
@@ -1473,7 +1479,8 @@ static hipError_t launch_gemmh(const sihip_weight *w, const GemmPlan &p, const G
     const Layout &L = w->L;
     const int64_t nk = L.n_in / 128;
     const int64_t threads = p.Mp * L.n_in / 8;
-    if (B.quant)
+    const bool fused = MT == 1 && p.fuseq;
+    if (B.quant && !fused)
         hipLaunchKernelGGL(gemmh_convert_x<BM>, dim3((unsigned)((threads + 255) / 256)), dim3(256),
                            0, st, X, ldx, M, p.Mp, L.n_in, B.ws);
     GHArgs A;
@@ -1491,8 +1498,13 @@ static hipError_t launch_gemmh(const sihip_weight *w, const GemmPlan &p, const G
     A.SBK = p.SBK;
     A.part = p.S > 1 ? B.part : nullptr;
     A.cnt = p.S > 1 ? B.cnt : nullptr;
+    A.xf = fused ? X : nullptr;
+    A.ldx = ldx;
     const dim3 grid((unsigned)((int64_t)8 * ((A.NB + 7) / 8) * A.MB * A.S));
-    hipLaunchKernelGGL((gemmh_f16_kernel<MT>), grid, dim3(kG2Threads), 0, st, A);
+    if (fused)
+        hipLaunchKernelGGL((gemmh_f16_kernel<MT, true>), grid, dim3(kG2Threads), 0, st, A);
+    else
+        hipLaunchKernelGGL((gemmh_f16_kernel<MT, false>), grid, dim3(kG2Threads), 0, st, A);
     return hipGetLastError();
 }
 

@@ -386,6 +386,37 @@ def test_gemmh_f16_vs_oracle(dev, oracle, option, n_out, n_in, M, mt, sbk):
     assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32)), what + ": repeat differs"
 
 
+def test_gemmh_converting_launch_matches(dev, oracle, option):
+    """At 16-row m blocks the F16 GEMM converts X itself as it stages each
+    step's record; the results are the bits of the launch after a
+    conversion launch (GEMMH_FUSE 0), call after call, with and without K
+    slices, M of 1, 7 and 16 (rows past M zero), one and two m blocks
+    (M = 20 at GEMM_MT 1), and within the bar of the oracle."""
+    option("GEMMH_MIN_M", "1")
+    rng = np.random.default_rng(4242)
+    for n_out, n_in, M, mt, sbk in [(1024, 5120, 7, -1, -1), (300, 1280, 16, -1, 0),
+                                    (5120, 5120, 1, -1, -1), (129, 384, 20, 1, 1),
+                                    (27648, 5120, 8, -1, -1)]:
+        W = synth.make_weights(sa.F16, n_out, n_in, rng)
+        X = _rows(rng, M, n_in)
+        w = dev.upload(sa.F16, n_out, n_in, W)
+        try:
+            option("GEMM_MT", str(mt))
+            option("GEMM_SBK", str(sbk))
+            outs = []
+            for fuse in ("-1", "0", "-1"):
+                option("GEMMH_FUSE", fuse)
+                outs.append(dev.gemm(w, X))
+        finally:
+            w.free()
+        what = f"F16 {n_out}x{n_in} M={M} MT={mt} SBK={sbk}"
+        for y in outs[1:]:
+            assert np.array_equal(y.view(np.uint32), outs[0].view(np.uint32)), what + ": launches differ"
+        if n_out <= 1024:
+            ref, L1 = oracle.gemm(sa.F16, W, n_out, n_in, X)
+            assert_close(outs[0].reshape(-1), ref.reshape(-1).astype(np.float64), L1.reshape(-1), what)
+
+
 def test_f16_rows_not_multiple_of_128_take_the_matvec(dev, oracle):
     """F16 rows whose length is not a multiple of 128 elements (288 = 9 x
     32) have no GEMM copy: batches run on the matvec kernel, within the
