@@ -238,10 +238,14 @@ struct G2Args {
 // store instruction writes 256 contiguous bytes and the last workgroup
 // reads a slice with 16-byte loads. Stored row by row (four 64-byte pieces
 // per instruction) the partial sums cost the Llama-3-8B prefill at M = 512
-// 2.3-3.5 us per sliced call (a timing copy without them).
+// 2.3-3.5 us per sliced call (a timing copy without them). In 16-row tiles
+// (MT = 1) rows at or past M (rows >= `rows` of the tile) are neither
+// stored nor read: at M = 8 that halves the hand-off's traffic. (Taller
+// tiles store and read them: the extra predicates made the MT = 8 kernels
+// spill.)
 template <int MT>
 __device__ inline void g2_store_partial(float *pt, int wave, int lane, const v4f2_t (&y)[MT][2],
-                                        float scale) {
+                                        float scale, int64_t rows) {
     float *const pw = pt + wave * (MT * 512) + lane;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
@@ -249,8 +253,9 @@ __device__ inline void g2_store_partial(float *pt, int wave, int lane, const v4f
         for (int nt = 0; nt < 2; nt++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                __hip_atomic_store(pw + ((mt * 2 + nt) * 4 + i) * 64, y[mt][nt][i] * scale,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (MT > 1 || 4 * (lane >> 4) + i < rows)
+                    __hip_atomic_store(pw + ((mt * 2 + nt) * 4 + i) * 64, y[mt][nt][i] * scale,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // End of a K-sliced tile after every wave has issued g2_store_partial for
@@ -277,43 +282,72 @@ __device__ inline void g2_slices_finish(const float *pt, int64_t per_slice, uint
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(pt), (short)0,
         (int)(((int64_t)(S - 1) * per_slice + MT * 2048) * 4), 0x00020000);
+    // floats 4 (q 256 + tid) .. + 3 of a slice's tile: wave w, tile
+    // (mt, nt), register i, lanes l .. l + 3, all of one row m; with MT = 1
+    // rows at or past M were not stored
+    // (recomputed where used: kept in arrays they spilled at MT = 8)
+    auto row_of = [&](int q) -> int64_t {
+        const int rem = ((q * 256 + (int)threadIdx.x) * 4) % (MT * 512);
+        return m0 + 16 * (rem >> 9) + 4 * ((rem & 63) >> 4) + ((rem >> 6) & 3);
+    };
+    auto col_of = [&](int q) -> int64_t {
+        const int k = (q * 256 + (int)threadIdx.x) * 4;
+        const int w = k / (MT * 512), rem = k % (MT * 512);
+        return n0 + 32 * w + 16 * ((rem >> 8) & 1) + (rem & 15);
+    };
     float v[kQ][4];
 #pragma unroll
     for (int q = 0; q < kQ; q++) v[q][0] = v[q][1] = v[q][2] = v[q][3] = 0.0f;
-    // one slice's loads issued together (one round trip per slice: agent-
-    // scope loads miss the XCD's L2), the slices added in slice order
-    for (int s = 0; s < S; s++) {
-        uint4 pv[kQ];
+    // the loads of kU slices issued together (agent-scope loads miss the
+    // XCD's L2: each group is one round trip), the slices added in slice
+    // order
+    constexpr int kU = kQ >= 8 ? 1 : 8 / kQ;
+    auto load = [&](int s, int q) {
+        return MT > 1 || row_of(q) < M ? __builtin_bit_cast(
+                              uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         pr, (int)(((int64_t)s * per_slice + (q * 256 + (int)threadIdx.x) * 4) * 4),
+                                         0, 16))
+                        : make_uint4(0, 0, 0, 0);
+    };
+    auto add = [&](int q, uint4 p) {
+        v[q][0] += __uint_as_float(p.x);
+        v[q][1] += __uint_as_float(p.y);
+        v[q][2] += __uint_as_float(p.z);
+        v[q][3] += __uint_as_float(p.w);
+    };
+    int s = 0;
+    for (; s + kU <= S; s += kU) {
+        uint4 pv[kU][kQ];
 #pragma unroll
-        for (int q = 0; q < kQ; q++)
-            pv[q] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                           pr, (int)(((int64_t)s * per_slice + (q * 256 + (int)threadIdx.x) * 4) * 4), 0,
-                           16));
+        for (int u = 0; u < kU; u++)
 #pragma unroll
-        for (int q = 0; q < kQ; q++) {
-            v[q][0] += __uint_as_float(pv[q].x);
-            v[q][1] += __uint_as_float(pv[q].y);
-            v[q][2] += __uint_as_float(pv[q].z);
-            v[q][3] += __uint_as_float(pv[q].w);
+            for (int q = 0; q < kQ; q++) pv[u][q] = load(s + u, q);
+#pragma unroll
+        for (int u = 0; u < kU; u++)
+#pragma unroll
+            for (int q = 0; q < kQ; q++) add(q, pv[u][q]);
+    }
+    if constexpr (kU > 1) {
+        for (; s < S; s++) {
+            uint4 pv[kQ];
+#pragma unroll
+            for (int q = 0; q < kQ; q++) pv[q] = load(s, q);
+#pragma unroll
+            for (int q = 0; q < kQ; q++) add(q, pv[q]);
         }
     }
 #pragma unroll
     for (int q = 0; q < kQ; q++) {
-        // floats k .. k + 3: wave w, tile (mt, nt), register i, lanes l .. l + 3
-        const int k = (q * 256 + (int)threadIdx.x) * 4;
-        const int w = k / (MT * 512), rem = k % (MT * 512);
-        const int mt = rem >> 9, nt = (rem >> 8) & 1, i = (rem >> 6) & 3, l = rem & 63;
-        const int64_t m = m0 + 16 * mt + 4 * (l >> 4) + i;
-        const int64_t n = n0 + 32 * w + 16 * nt + (l & 15);
+        const int64_t m = row_of(q);
         if (m < M) {
-            float *const dst = y + m * ldy + n;
-            if (n + 3 < n_out && ((uintptr_t)dst & 15) == 0) {
+            const int64_t n_ = col_of(q);
+            float *const dst = y + m * ldy + n_;
+            if (n_ + 3 < n_out && ((uintptr_t)dst & 15) == 0) {
                 *reinterpret_cast<float4 *>(dst) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (n + j < n_out) dst[j] = v[q][j];
+                    if (n_ + j < n_out) dst[j] = v[q][j];
             }
         }
     }
@@ -528,7 +562,7 @@ __attribute__((amdgpu_waves_per_eu(W, W))) void gemm2_q4k_kernel(G2Args A) {
     // slice-order sum into the segment's columns
     const int64_t per_slice = (int64_t)A.MB * A.NB * (BM * kG2BN);
     float *const pt = A.part + ((int64_t)mblk * A.NB + nblk) * (BM * kG2BN);  // slice 0
-    g2_store_partial<MT>(pt + slice * per_slice, wave, lane, y, sg.yscale);
+    g2_store_partial<MT>(pt + slice * per_slice, wave, lane, y, sg.yscale, A.M - m0);
     g2_slices_finish<MT>(pt, per_slice, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, m0, A.M,
                          (int64_t)lblk * kG2BN, sg.n_out, sg.y, sg.ldy);
 }

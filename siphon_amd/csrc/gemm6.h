@@ -293,7 +293,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void gemm6_q6k_kernel(G6Args A) {
     // the tile's arrival and the last workgroup's slice-order sum
     const int64_t per_slice = (int64_t)A.MB * A.NB * (BM * kG2BN);
     float *const pt = A.part + ((int64_t)mblk * A.NB + nblk) * (BM * kG2BN);  // slice 0
-    g2_store_partial<MT>(pt + slice * per_slice, wave, threadIdx.x & 63, y, 1.0f);
+    g2_store_partial<MT>(pt + slice * per_slice, wave, threadIdx.x & 63, y, 1.0f, A.M - m0);
     g2_slices_finish<MT>(pt, per_slice, A.cnt + (int64_t)mblk * A.NB + nblk, A.S, m0, A.M,
                          (int64_t)nblk * kG2BN, A.n_out, A.y, A.ldy);
 }
