@@ -777,6 +777,18 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
             nwg[i] = share < 1 ? 1 : (share < want[i] ? share : want[i]);
         }
     }
+    // A launch of several matrices that would need between one and two
+    // workgroups per CU halves the workgroups of its largest whole-row
+    // matrix (each wave then walks two of its tiles) where that brings it to
+    // one per CU: otherwise half the CUs run two workgroups and the rest one.
+    // Llama-3-8B q/k/v (256 + 64 + 64 workgroups): 6.34 -> 5.52 us.
+    if (count > 1 && want_sum > ctx->n_cu && want_sum <= wg_cap) {
+        int big = -1;
+        for (int i = 0; i < count; i++)
+            if (w[i]->split == 1 && (big < 0 || nwg[i] > nwg[big])) big = i;
+        if (big >= 0 && nwg[big] % 2 == 0 && want_sum - nwg[big] / 2 <= ctx->n_cu)
+            nwg[big] /= 2;
+    }
     for (int i = 0; i < count; i++) {
         if (w[i]->split > 1) {
             const int rc = order_before(ctx, w[i]->order, st);
@@ -792,7 +804,8 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
     // is a multiple of the narrowest matrix's is therefore cut into ranges
     // of consecutive row tiles of that many workgroups (a range is the same
     // matrix from a later tile: plane bases, y and rows offset), so every
-    // segment is equally wide: q/k/v runs as 6 x 64 workgroups.
+    // segment is equally wide: q/k/v runs as 4 x 64 workgroups, wq in two
+    // ranges whose waves walk two tiles each.
     int parts[kMaxSegs];
     int nsegs = 0;
     int64_t narrow = 0;
@@ -802,7 +815,7 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
         const int64_t ntiles = (n_out[i] + w[i]->L.R - 1) / w[i]->L.R;
         parts[i] = 1;
         if (count > 1 && w[i]->split == 1 && nwg[i] > narrow && nwg[i] % narrow == 0 &&
-            ntiles == nwg[i] * kWaves)
+            ntiles % (nwg[i] * kWaves) == 0)
             parts[i] = (int)(nwg[i] / narrow);
         nsegs += parts[i];
     }
