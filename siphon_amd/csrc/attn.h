@@ -7,6 +7,9 @@
 //   attn_scores_kernel   sc[h][j] = dot(K[hk][j], f16(q_h)) * kq_scale
 //   attn_softmax_kernel  p[h][j] = f16(softmax(sc[h])[j])
 //   attn_pv_kernel       out[h][c] = dot(V[hk][c][0..n), p[h])
+// or, for n <= kAttnFuseMax, two: attn_scores_kernel<VEC, true> ends with the
+// softmax of a KV head's query heads, run by the last of its workgroups to
+// finish (one wave per head, wave_softmax), then attn_pv_kernel.
 //
 // The f16 dot is evaluated in the reference's order. Its 32 f32
 // accumulators (accumulator a takes elements i with i % 32 == a, by FMA in
@@ -56,6 +59,7 @@ struct AttnArgs {
     uint16_t *p16;         // [n_head][ld] f16 probabilities (caller's, optional)
     float *sw;             // [n_head][lw] scaled scores (workspace)
     uint16_t *pw;          // [n_head][lw] f16 probabilities (workspace)
+    uint32_t *cnt;         // FUSE: [gridDim.y] arrival counters, zero between launches
     int64_t n_ctx, ld, lw;
     int n, hd, gqa, n_head;
     float kq_scale;
@@ -112,13 +116,95 @@ __device__ inline float expf_poly(float x) {
     return __builtin_fmaf(s2, p, s2) * s1;
 }
 
+constexpr int kAttnBlock = 4096;  // softmax positions per workgroup pass (16 per thread)
+
+// exp of a tail position's shifted score (positions past the last whole
+// 8-group): exp in double, rounded.
+__device__ inline float tail_exp(float x) { return (float)exp((double)x); }
+
+// The softmax of query head h's scores by one wave, for n <= kAttnFuseMax
+// (the fused scores launch): lane l holds the 8-group of positions
+// 8 l .. 8 l + 7, read with agent-scope loads since other workgroups wrote
+// them. The max, the exponentials, each group's float sum in the
+// reference's 8-lane order, 1 / total and the f16 probabilities are
+// attn_softmax_kernel's; only the order in which the groups' sums are
+// added in double differs (a 64-lane tree instead of a 256-thread one, both
+// within n 2^-53 relative of the reference's sequential sum). The tail
+// [gend, n) is added, and its probabilities written, by the lane whose
+// group holds it, with tail_exp. (One wave per head is 4 heads' softmax on
+// one CU where the softmax launch spreads them over 32: with 8 groups per
+// lane, n = 4096, the scores launch took 39.5 us against 7.8 + 7.2 for the
+// two launches, so longer rows keep the softmax launch.)
+constexpr int kAttnFuseMax = 512;
+
+__device__ inline void wave_softmax(const AttnArgs &A, int h, int lane) {
+    const int n = A.n, gend = n & ~7;
+    const int j0 = 8 * lane;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        A.sw + (int64_t)h * A.lw, (short)0, (int)(A.lw * 4), 0x00020000);
+    float v[8];
+    {
+        const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, j0 * 4, 0, 16));
+        const uint4 b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, j0 * 4 + 16, 0, 16));
+        v[0] = __uint_as_float(a.x), v[1] = __uint_as_float(a.y);
+        v[2] = __uint_as_float(a.z), v[3] = __uint_as_float(a.w);
+        v[4] = __uint_as_float(b.x), v[5] = __uint_as_float(b.y);
+        v[6] = __uint_as_float(b.z), v[7] = __uint_as_float(b.w);
+    }
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        if (j0 + e < n && v[e] > mx) mx = v[e];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float t = __shfl_xor(mx, o);
+        mx = t > mx ? t : mx;
+    }
+    const bool tail_owner = gend < n && j0 == gend;
+    float tv[8];  // the tail's scores, before the exponentials replace them
+#pragma unroll
+    for (int e = 0; e < 8; e++) tv[e] = v[e];
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = expf_poly(v[e] - mx);
+    double part = 0.0;
+    if (j0 + 8 <= gend)
+        part += (double)(((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7])));
+    if (tail_owner)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (gend + e < n) part += (double)tail_exp(tv[e] - mx);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+    const float scale = (float)(1.0 / part);
+    uint16_t *pw = A.pw + (int64_t)h * A.lw;
+    uint32_t pk[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        pk[e] = (uint32_t)f32_to_f16_bits(v[2 * e] * scale) |
+                ((uint32_t)f32_to_f16_bits(v[2 * e + 1] * scale) << 16);
+    *reinterpret_cast<uint4 *>(pw + j0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    if (A.p16)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (j0 + e < n) A.p16[(int64_t)h * A.ld + j0 + e] = (uint16_t)(pk[e >> 1] >> (16 * (e & 1)));
+    // the tail's probabilities replace the polynomial's (same lane, later stores)
+    if (tail_owner)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (gend + e < n) {
+                const uint16_t pb = f32_to_f16_bits(tail_exp(tv[e] - mx) * scale);
+                pw[gend + e] = pb;
+                if (A.p16) A.p16[(int64_t)h * A.ld + gend + e] = pb;
+            }
+}
+
 // Grid (ceil(n / kAttnRows), n_head_kv * ceil(gqa / kAttnHeads)): each
 // workgroup scores kAttnRows cached positions against up to kAttnHeads
 // query heads of one KV head, holding each key row in registers across
 // the heads.
 // VEC: hd % 4 == 0 and k 8-byte aligned (a lane's 4 key elements of a step
 // in one load).
-template <bool VEC>
+template <bool VEC, bool FUSE>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
     __shared__ uint16_t q16[kAttnHeads * kAttnMaxHd];
     const int chunks = (A.gqa + kAttnHeads - 1) / kAttnHeads;
@@ -166,13 +252,33 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
             for (int i = body; i < hd; i++)
                 total += (double)(f16_at(krow, i) * f16_bits_to_f32(qh[i]));
             const float v = (float)total * A.kq_scale;
-            A.sw[(int64_t)(h0 + hh) * A.lw + j] = v;
+            if constexpr (FUSE)  // read by another workgroup: past the XCD's L2
+                __hip_atomic_store(A.sw + (int64_t)(h0 + hh) * A.lw + j, v, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            else
+                A.sw[(int64_t)(h0 + hh) * A.lw + j] = v;
             if (A.sc) A.sc[(int64_t)(h0 + hh) * A.ld + j] = v;
         }
     }
+    if constexpr (FUSE) {
+        // the KV head's arrival count (the ordering of slices_finish in
+        // agent.h); its last workgroup runs the softmax of the heads
+        __shared__ uint32_t last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(A.cnt + blockIdx.y, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        __syncthreads();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (!last) return;
+        const int wave = threadIdx.x >> 6;
+        if (wave < nh) wave_softmax(A, h0 + wave, threadIdx.x & 63);
+        if (threadIdx.x == 0)
+            __hip_atomic_store(A.cnt + blockIdx.y, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
-
-constexpr int kAttnBlock = 4096;  // softmax positions per workgroup pass (16 per thread)
 
 // Positions b + 16t .. b + 16t + 15 of a row for thread t: two 8-groups.
 struct SoftBlock {
@@ -190,10 +296,6 @@ __device__ inline void load_soft_block(const float *row, int b, SoftBlock &blk) 
         blk.v[4 * i + 3] = f.w;
     }
 }
-
-// exp of a tail position's shifted score (positions past the last whole
-// 8-group): exp in double, rounded.
-__device__ inline float tail_exp(float x) { return (float)exp((double)x); }
 
 // Grid n_head: one workgroup per query head. The max, the total and the
 // f16 probabilities each take one pass over the row in blocks of

@@ -76,16 +76,25 @@ def test_golden_cases(dev):
     (6, 2, 256, 33, 0),         # position 0
     (3, 1, 8, 20, 17),          # head dim below one 32-element step
     (4, 2, 66, 40, 39),         # head dim not a multiple of 4: narrow key loads
+    (8, 2, 128, 700, 511),      # n = 512: the longest row of the two-launch path
+    (4, 1, 64, 520, 504),       # n = 505: the tail in the wave's last lane
+    (8, 2, 128, 700, 515),      # n = 516: three launches again
 ])
-def test_vs_oracle(dev, oracle, n_head, n_kv, hd, n_ctx, pos):
+@pytest.mark.parametrize("fuse", [-1, 0], ids=["two_launches", "three_launches"])
+def test_vs_oracle(dev, oracle, option, n_head, n_kv, hd, n_ctx, pos, fuse):
+    """Up to 512 positions the softmax runs by default at the end of the
+    scores launch (ATTN_FUSE 0: its own launch); both against the oracle,
+    twice in a row (the arrival counters return to zero)."""
+    option("ATTN_FUSE", fuse)
     rng = np.random.default_rng(n_head * 7919 + hd * 31 + pos)
     q = rng.standard_normal(n_head * hd).astype(np.float32)
     k = (rng.standard_normal(n_kv * n_ctx * hd) * 2).astype(np.float16).view(np.uint16)
     v = rng.standard_normal(n_kv * hd * n_ctx).astype(np.float16).view(np.uint16)
     kq = float(np.float32(1.0 / np.sqrt(np.float32(hd))))
     want = oracle.attn_decode(q, k, v, n_head, n_kv, hd, n_ctx, pos, kq)
-    got = run_attn(dev, q, k, v, n_head, n_kv, hd, n_ctx, pos, kq)
-    check(got, want, pos + 1, f"{n_head}/{n_kv} heads hd={hd} pos={pos}")
+    for _ in range(2):
+        got = run_attn(dev, q, k, v, n_head, n_kv, hd, n_ctx, pos, kq)
+        check(got, want, pos + 1, f"{n_head}/{n_kv} heads hd={hd} pos={pos} fuse={fuse}")
     # the context's workspace instead of caller buffers: the same output
     out_ws, _, _ = run_attn(dev, q, k, v, n_head, n_kv, hd, n_ctx, pos, kq,
                             caller_buffers=False)
@@ -103,3 +112,44 @@ def test_bad_arguments(dev):
                 dev.attn_decode_dev(p, p, p, n_head, n_kv, hd, n_ctx, pos, 1.0, p)
     finally:
         buf.free()
+
+
+def test_two_launch_graph_replays(dev, oracle):
+    """The two-launch attention (n <= 512) captured in a HIP graph: every
+    replay, with eager calls between the replays, gives the oracle's bits
+    (its per-KV-head arrival counters return to zero each time)."""
+    from .test_gpu_slices import _HipGraph
+
+    rng = np.random.default_rng(5120)
+    n_head, n_kv, hd, n_ctx, pos = 32, 8, 128, 1024, 300
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    k = (rng.standard_normal(n_kv * n_ctx * hd) * 2).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(n_kv * hd * n_ctx).astype(np.float16).view(np.uint16)
+    kq = float(np.float32(1.0 / np.sqrt(np.float32(hd))))
+    want = oracle.attn_decode(q, k, v, n_head, n_kv, hd, n_ctx, pos, kq)[0]
+    hg = _HipGraph()
+    bufs = []
+    try:
+        qd, kd, vd = dev.to_device(q), dev.to_device(k), dev.to_device(v)
+        nan = np.full(n_head * hd, np.nan, np.float32)
+        oe, og = dev.to_device(nan), dev.to_device(nan)
+        bufs = [qd, kd, vd, oe, og]
+        args = (qd.ptr, kd.ptr, vd.ptr, n_head, n_kv, hd, n_ctx, pos, kq)
+        dev.attn_decode_dev(*args, oe.ptr, None, None, hg.stream.value)
+        dev.synchronize()
+        assert np.array_equal(bits(oe.to_host(np.float32, n_head * hd)), bits(want))
+        hg.begin()
+        dev.attn_decode_dev(*args, og.ptr, None, None, hg.stream.value)
+        hg.end()
+        for _ in range(3):
+            og.fill(nan)
+            hg.replay()
+            assert np.array_equal(bits(og.to_host(np.float32, n_head * hd)), bits(want))
+            oe.fill(nan)
+            dev.attn_decode_dev(*args, oe.ptr, None, None, hg.stream.value)
+            dev.synchronize()
+            assert np.array_equal(bits(oe.to_host(np.float32, n_head * hd)), bits(want))
+    finally:
+        hg.close()
+        for b in bufs:
+            b.free()
