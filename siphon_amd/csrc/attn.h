@@ -7,9 +7,9 @@
 //   attn_scores_kernel   sc[h][j] = dot(K[hk][j], f16(q_h)) * kq_scale
 //   attn_softmax_kernel  p[h][j] = f16(softmax(sc[h])[j])
 //   attn_pv_kernel       out[h][c] = dot(V[hk][c][0..n), p[h])
-// or, for n <= kAttnFuseMax, two: attn_scores_kernel<VEC, true> ends with the
-// softmax of a KV head's query heads, run by the last of its workgroups to
-// finish (one wave per head, wave_softmax), then attn_pv_kernel.
+// or, for n <= kAttnFuseMax, two: attn_scores_kernel, then attn_pv_kernel
+// with NG > 0, each of whose waves computes the softmax of its query head
+// itself (wave_softmax) into LDS instead of loading probabilities.
 //
 // The f16 dot is evaluated in the reference's order. Its 32 f32
 // accumulators (accumulator a takes elements i with i % 32 == a, by FMA in
@@ -59,7 +59,6 @@ struct AttnArgs {
     uint16_t *p16;         // [n_head][ld] f16 probabilities (caller's, optional)
     float *sw;             // [n_head][lw] scaled scores (workspace)
     uint16_t *pw;          // [n_head][lw] f16 probabilities (workspace)
-    uint32_t *cnt;         // FUSE: [gridDim.y] arrival counters, zero between launches
     int64_t n_ctx, ld, lw;
     int n, hd, gqa, n_head;
     float kq_scale;
@@ -122,53 +121,63 @@ constexpr int kAttnBlock = 4096;  // softmax positions per workgroup pass (16 pe
 // 8-group): exp in double, rounded.
 __device__ inline float tail_exp(float x) { return (float)exp((double)x); }
 
-// The softmax of query head h's scores by one wave, for n <= kAttnFuseMax
-// (the fused scores launch): lane l holds the 8-group of positions
-// 8 l .. 8 l + 7, read with agent-scope loads since other workgroups wrote
-// them. The max, the exponentials, each group's float sum in the
-// reference's 8-lane order, 1 / total and the f16 probabilities are
-// attn_softmax_kernel's; only the order in which the groups' sums are
-// added in double differs (a 64-lane tree instead of a 256-thread one, both
-// within n 2^-53 relative of the reference's sequential sum). The tail
-// [gend, n) is added, and its probabilities written, by the lane whose
-// group holds it, with tail_exp. (One wave per head is 4 heads' softmax on
-// one CU where the softmax launch spreads them over 32: with 8 groups per
-// lane, n = 4096, the scores launch took 39.5 us against 7.8 + 7.2 for the
-// two launches, so longer rows keep the softmax launch.)
-constexpr int kAttnFuseMax = 512;
+// The softmax of query head h's scores by one wave, for n <= 512 NG (the
+// value launch of the two-launch path): lane l holds the 8-groups of
+// positions 512 g + 8 l .. + 7, g < NG. The max, the exponentials, each
+// group's float sum in the reference's 8-lane order, 1 / total and the f16
+// probabilities are attn_softmax_kernel's; only the order in which the
+// groups' sums are added in double differs (a 64-lane tree instead of a
+// 256-thread one, both within n 2^-53 relative of the reference's
+// sequential sum). The tail [gend, n) is added, and its probabilities
+// written, by the lane whose group holds it, with tail_exp. The
+// probabilities go to pdst[0 .. 512 NG) (positions past n hold values
+// that are not used), and to the caller's probs16 where p16_out.
+constexpr int kAttnFuseMax = 1024;
 
-__device__ inline void wave_softmax(const AttnArgs &A, int h, int lane) {
+template <int NG>
+__device__ inline void wave_softmax(const AttnArgs &A, int h, int lane, uint16_t *pdst,
+                                    bool p16_out) {
     const int n = A.n, gend = n & ~7;
-    const int j0 = 8 * lane;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        A.sw + (int64_t)h * A.lw, (short)0, (int)(A.lw * 4), 0x00020000);
-    float v[8];
-    {
-        const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, j0 * 4, 0, 16));
-        const uint4 b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, j0 * 4 + 16, 0, 16));
-        v[0] = __uint_as_float(a.x), v[1] = __uint_as_float(a.y);
-        v[2] = __uint_as_float(a.z), v[3] = __uint_as_float(a.w);
-        v[4] = __uint_as_float(b.x), v[5] = __uint_as_float(b.y);
-        v[6] = __uint_as_float(b.z), v[7] = __uint_as_float(b.w);
-    }
+    const float *row = A.sw + (int64_t)h * A.lw;  // lw >= 512 NG entries
+    float v[NG][8];
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+        if (512 * g < n) {  // wave-uniform
+            const float4 *p = reinterpret_cast<const float4 *>(row + 512 * g + 8 * lane);
+            const float4 a = p[0], b = p[1];
+            v[g][0] = a.x, v[g][1] = a.y, v[g][2] = a.z, v[g][3] = a.w;
+            v[g][4] = b.x, v[g][5] = b.y, v[g][6] = b.z, v[g][7] = b.w;
+        }
     float mx = -__builtin_inff();
 #pragma unroll
-    for (int e = 0; e < 8; e++)
-        if (j0 + e < n && v[e] > mx) mx = v[e];
+    for (int g = 0; g < NG; g++)
+        if (512 * g < n)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (512 * g + 8 * lane + e < n && v[g][e] > mx) mx = v[g][e];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float t = __shfl_xor(mx, o);
         mx = t > mx ? t : mx;
     }
-    const bool tail_owner = gend < n && j0 == gend;
-    float tv[8];  // the tail's scores, before the exponentials replace them
+    // the tail's scores, before the exponentials replace them
+    const bool tail_owner = gend < n && lane == (gend % 512) / 8;
+    float tv[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) tv[e] = v[e];
+    for (int g = 0; g < NG; g++)
+        if (g == gend / 512)
 #pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = expf_poly(v[e] - mx);
+            for (int e = 0; e < 8; e++) tv[e] = v[g][e];
     double part = 0.0;
-    if (j0 + 8 <= gend)
-        part += (double)(((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7])));
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+        if (512 * g < n) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[g][e] = expf_poly(v[g][e] - mx);
+            const float *x = v[g];
+            if (512 * g + 8 * lane + 8 <= gend)
+                part += (double)(((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7])));
+        }
     if (tail_owner)
 #pragma unroll
         for (int e = 0; e < 8; e++)
@@ -176,25 +185,30 @@ __device__ inline void wave_softmax(const AttnArgs &A, int h, int lane) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
     const float scale = (float)(1.0 / part);
-    uint16_t *pw = A.pw + (int64_t)h * A.lw;
-    uint32_t pk[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-        pk[e] = (uint32_t)f32_to_f16_bits(v[2 * e] * scale) |
-                ((uint32_t)f32_to_f16_bits(v[2 * e + 1] * scale) << 16);
-    *reinterpret_cast<uint4 *>(pw + j0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    if (A.p16)
+    for (int g = 0; g < NG; g++)
+        if (512 * g < n) {
+            const int j0 = 512 * g + 8 * lane;
+            uint32_t pk[4];
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-            if (j0 + e < n) A.p16[(int64_t)h * A.ld + j0 + e] = (uint16_t)(pk[e >> 1] >> (16 * (e & 1)));
+            for (int e = 0; e < 4; e++)
+                pk[e] = (uint32_t)f32_to_f16_bits(v[g][2 * e] * scale) |
+                        ((uint32_t)f32_to_f16_bits(v[g][2 * e + 1] * scale) << 16);
+            *reinterpret_cast<uint4 *>(pdst + j0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            if (A.p16 && p16_out)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (j0 + e < n)
+                        A.p16[(int64_t)h * A.ld + j0 + e] = (uint16_t)(pk[e >> 1] >> (16 * (e & 1)));
+        }
     // the tail's probabilities replace the polynomial's (same lane, later stores)
     if (tail_owner)
 #pragma unroll
         for (int e = 0; e < 8; e++)
             if (gend + e < n) {
                 const uint16_t pb = f32_to_f16_bits(tail_exp(tv[e] - mx) * scale);
-                pw[gend + e] = pb;
-                if (A.p16) A.p16[(int64_t)h * A.ld + gend + e] = pb;
+                pdst[gend + e] = pb;
+                if (A.p16 && p16_out) A.p16[(int64_t)h * A.ld + gend + e] = pb;
             }
 }
 
@@ -204,7 +218,7 @@ __device__ inline void wave_softmax(const AttnArgs &A, int h, int lane) {
 // the heads.
 // VEC: hd % 4 == 0 and k 8-byte aligned (a lane's 4 key elements of a step
 // in one load).
-template <bool VEC, bool FUSE>
+template <bool VEC>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
     __shared__ uint16_t q16[kAttnHeads * kAttnMaxHd];
     const int chunks = (A.gqa + kAttnHeads - 1) / kAttnHeads;
@@ -252,31 +266,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs A) {
             for (int i = body; i < hd; i++)
                 total += (double)(f16_at(krow, i) * f16_bits_to_f32(qh[i]));
             const float v = (float)total * A.kq_scale;
-            if constexpr (FUSE)  // read by another workgroup: past the XCD's L2
-                __hip_atomic_store(A.sw + (int64_t)(h0 + hh) * A.lw + j, v, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            else
-                A.sw[(int64_t)(h0 + hh) * A.lw + j] = v;
+            A.sw[(int64_t)(h0 + hh) * A.lw + j] = v;
             if (A.sc) A.sc[(int64_t)(h0 + hh) * A.ld + j] = v;
         }
-    }
-    if constexpr (FUSE) {
-        // the KV head's arrival count (the ordering of slices_finish in
-        // agent.h); its last workgroup runs the softmax of the heads
-        __shared__ uint32_t last;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(A.cnt + blockIdx.y, 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-        __syncthreads();
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if (!last) return;
-        const int wave = threadIdx.x >> 6;
-        if (wave < nh) wave_softmax(A, h0 + wave, threadIdx.x & 63);
-        if (threadIdx.x == 0)
-            __hip_atomic_store(A.cnt + blockIdx.y, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -398,7 +390,12 @@ constexpr int kAttnVPieces = kAttnPvRows * kAttnChunk / 8 / kAttnThreads;  // 16
 constexpr int kAttnPPieces = kAttnHeads * kAttnChunk / 8 / kAttnThreads;
 
 // VEC: n_ctx % 8 == 0 and v 16-byte aligned (16-byte value pieces).
-template <bool VEC>
+// NG > 0 (n <= 512 NG <= kAttnFuseMax, one chunk): wave w computes the
+// softmax of head h0 + w itself (wave_softmax<NG>, from the scores launch's
+// scores) into its LDS probability row while the value rows load, in place
+// of loading probabilities; the caller's probs16 is written by the
+// workgroups of blockIdx.x == 0.
+template <bool VEC, int NG>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs A) {
     __shared__ __attribute__((aligned(16))) uint16_t sv[kAttnPvRows * kAttnChunk];
     __shared__ __attribute__((aligned(16))) uint16_t sp[kAttnHeads * kAttnChunk];
@@ -419,11 +416,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs A) {
         // probability rows: whole pieces of the workspace (lw >= s0 + kAttnChunk);
         // heads past nh repeat head nh - 1
         uint4 pq[kAttnPPieces];
+        if constexpr (NG == 0) {
 #pragma unroll
-        for (int i = 0; i < kAttnPPieces; i++) {
-            const int t = threadIdx.x + kAttnThreads * i;
-            const int hh = min(t / (kAttnChunk / 8), nh - 1), pc = t % (kAttnChunk / 8);
-            pq[i] = reinterpret_cast<const uint4 *>(A.pw + (int64_t)(h0 + hh) * A.lw + s0)[pc];
+            for (int i = 0; i < kAttnPPieces; i++) {
+                const int t = threadIdx.x + kAttnThreads * i;
+                const int hh = min(t / (kAttnChunk / 8), nh - 1), pc = t % (kAttnChunk / 8);
+                pq[i] = reinterpret_cast<const uint4 *>(A.pw + (int64_t)(h0 + hh) * A.lw + s0)[pc];
+            }
         }
         if constexpr (VEC) {
             // value rows (rows past hd repeat row hd - 1); pieces past the
@@ -451,9 +450,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs A) {
                 sv[rr * kAttnChunk + i] = A.v[((int64_t)hk * A.hd + cr) * A.n_ctx + s0 + i];
             }
         }
+        if constexpr (NG > 0) {
+            if (active) wave_softmax<NG>(A, h0 + wave, lane, sp + wave * kAttnChunk, blockIdx.x == 0);
+        } else {
 #pragma unroll
-        for (int i = 0; i < kAttnPPieces; i++)
-            reinterpret_cast<uint4 *>(sp)[threadIdx.x + kAttnThreads * i] = pq[i];
+            for (int i = 0; i < kAttnPPieces; i++)
+                reinterpret_cast<uint4 *>(sp)[threadIdx.x + kAttnThreads * i] = pq[i];
+        }
         __syncthreads();
         // the accumulator chains over the chunk's whole 32-steps
         if (active) {

@@ -52,7 +52,7 @@ struct Options {
     int64_t gemmq_xmode = -1;  // Q8_0-pair GEMM record mode 0 or 1 (gemmq_kernel XM; rule: 1 where it fits)
     int64_t gemmq_fuse = -1;   // Q8_0-pair GEMM quantizing X itself (XM 2) at 16-row m blocks, 0: off (rule: on)
     int64_t gemmh_fuse = -1;   // F16 GEMM converting X itself (XF) at 16-row m blocks, 0: off (rule: on)
-    int64_t attn_fuse = -1;    // decode attention in two launches up to 512 positions (softmax in the scores launch), 0: three
+    int64_t attn_fuse = -1;    // decode attention in two launches up to 1024 positions (softmax in the value launch), 0: three
     int64_t gemm2s_max_m = -1; // largest M on the small-M Q4_K GEMM, 0: none (rule: 16)
     int64_t gemmks_max_m = -1; // largest M on the small-M K-quant GEMM, 0: none (rule: 16)
     int64_t gemmks_q4k = -1;   // Q4_K small M on gemmks.h (1) or gemm2s.h (0) (rule: 0)
@@ -2392,29 +2392,31 @@ extern "C" int sihip_attn_decode_dev(sihip_ctx *ctx, const float *q, const uint1
     // wide loads where rows stay aligned: keys 8 bytes, value rows 16
     const bool kvec = head_dim % 4 == 0 && (uintptr_t)k_cache % 8 == 0;
     const bool vvec = n_ctx % 8 == 0 && (uintptr_t)v_cache % 16 == 0;
-    // up to kAttnFuseMax positions the softmax runs at the end of the
-    // scores launch, by the last workgroup of each KV head (one wave per
-    // query head; counters: the GEMMs' arrival counters, zero between the
-    // context's launches). At the 8B shape, position 511: 14.1 against
-    // 15.1 us per layer.
-    const bool fuse = ctx->opt.attn_fuse != 0 && A.n <= kAttnFuseMax;
-    A.cnt = fuse ? ctx->d_gcnt : nullptr;
-    if (fuse) {
-        if (kvec)
-            hipLaunchKernelGGL((attn_scores_kernel<true, true>), gs, dim3(kAttnThreads), 0, st, A);
-        else
-            hipLaunchKernelGGL((attn_scores_kernel<false, true>), gs, dim3(kAttnThreads), 0, st, A);
-    } else {
-        if (kvec)
-            hipLaunchKernelGGL((attn_scores_kernel<true, false>), gs, dim3(kAttnThreads), 0, st, A);
-        else
-            hipLaunchKernelGGL((attn_scores_kernel<false, false>), gs, dim3(kAttnThreads), 0, st, A);
-        hipLaunchKernelGGL(attn_softmax_kernel, dim3((unsigned)n_head), dim3(kAttnThreads), 0, st, A);
-    }
-    if (vvec)
-        hipLaunchKernelGGL(attn_pv_kernel<true>, gv, dim3(kAttnThreads), 0, st, A);
+    if (kvec)
+        hipLaunchKernelGGL(attn_scores_kernel<true>, gs, dim3(kAttnThreads), 0, st, A);
     else
-        hipLaunchKernelGGL(attn_pv_kernel<false>, gv, dim3(kAttnThreads), 0, st, A);
+        hipLaunchKernelGGL(attn_scores_kernel<false>, gs, dim3(kAttnThreads), 0, st, A);
+    // up to kAttnFuseMax positions the value launch's waves compute their
+    // heads' softmax themselves: no softmax launch (8B shape: 11.6 against
+    // 15.1 us per layer at position 511)
+    const int64_t fmax = ctx->opt.attn_fuse > 0 ? std::min<int64_t>(ctx->opt.attn_fuse * 512, 2048)
+                                                : kAttnFuseMax;
+    const int ng = ctx->opt.attn_fuse == 0 || A.n > fmax ? 0 : (A.n + 511) / 512;
+    if (ng == 0)
+        hipLaunchKernelGGL(attn_softmax_kernel, dim3((unsigned)n_head), dim3(kAttnThreads), 0, st, A);
+#define SIHIP_PV(V)                                                                                 \
+    switch (ng) {                                                                                   \
+        case 0: hipLaunchKernelGGL((attn_pv_kernel<V, 0>), gv, dim3(kAttnThreads), 0, st, A); break; \
+        case 1: hipLaunchKernelGGL((attn_pv_kernel<V, 1>), gv, dim3(kAttnThreads), 0, st, A); break; \
+        case 2: hipLaunchKernelGGL((attn_pv_kernel<V, 2>), gv, dim3(kAttnThreads), 0, st, A); break; \
+        default: hipLaunchKernelGGL((attn_pv_kernel<V, 4>), gv, dim3(kAttnThreads), 0, st, A); break; \
+    }
+    if (vvec) {
+        SIHIP_PV(true)
+    } else {
+        SIHIP_PV(false)
+    }
+#undef SIHIP_PV
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(ctx, SIHIP_EDEVICE, "attention launch: %s", hipGetErrorString(e));
     return order_after(ctx, ctx->order, st);

@@ -76,15 +76,17 @@ def test_golden_cases(dev):
     (6, 2, 256, 33, 0),         # position 0
     (3, 1, 8, 20, 17),          # head dim below one 32-element step
     (4, 2, 66, 40, 39),         # head dim not a multiple of 4: narrow key loads
-    (8, 2, 128, 700, 511),      # n = 512: the longest row of the two-launch path
+    (8, 2, 128, 700, 511),      # n = 512: one 8-group per lane of a wave
     (4, 1, 64, 520, 504),       # n = 505: the tail in the wave's last lane
-    (8, 2, 128, 700, 515),      # n = 516: three launches again
+    (8, 2, 128, 700, 515),      # n = 516: a second group per lane, a tail
+    (8, 2, 128, 2048, 1800),    # n = 1801: four groups per lane (ATTN_FUSE 4)
 ])
-@pytest.mark.parametrize("fuse", [-1, 0], ids=["two_launches", "three_launches"])
+@pytest.mark.parametrize("fuse", [-1, 0, 4], ids=["rule", "three_launches", "two_to_2048"])
 def test_vs_oracle(dev, oracle, option, n_head, n_kv, hd, n_ctx, pos, fuse):
-    """Up to 512 positions the softmax runs by default at the end of the
-    scores launch (ATTN_FUSE 0: its own launch); both against the oracle,
-    twice in a row (the arrival counters return to zero)."""
+    """Up to 1024 positions (ATTN_FUSE k: 512 k) the value launch's waves
+    compute their heads' softmax themselves, with no softmax launch
+    (ATTN_FUSE 0: three launches); each against the oracle, twice in a
+    row."""
     option("ATTN_FUSE", fuse)
     rng = np.random.default_rng(n_head * 7919 + hd * 31 + pos)
     q = rng.standard_normal(n_head * hd).astype(np.float32)
@@ -115,9 +117,8 @@ def test_bad_arguments(dev):
 
 
 def test_two_launch_graph_replays(dev, oracle):
-    """The two-launch attention (n <= 512) captured in a HIP graph: every
-    replay, with eager calls between the replays, gives the oracle's bits
-    (its per-KV-head arrival counters return to zero each time)."""
+    """The two-launch attention captured in a HIP graph: every replay, with
+    eager calls between the replays, gives the oracle's bits."""
     from .test_gpu_slices import _HipGraph
 
     rng = np.random.default_rng(5120)
