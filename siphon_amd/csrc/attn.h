@@ -390,7 +390,7 @@ constexpr int kAttnVPieces = kAttnPvRows * kAttnChunk / 8 / kAttnThreads;  // 16
 constexpr int kAttnPPieces = kAttnHeads * kAttnChunk / 8 / kAttnThreads;
 
 // VEC: n_ctx % 8 == 0 and v 16-byte aligned (16-byte value pieces).
-// NG > 0 (n <= 512 NG <= kAttnFuseMax, one chunk): wave w computes the
+// NG > 0 (n <= 512 NG <= kAttnChunk, one chunk): wave w computes the
 // softmax of head h0 + w itself (wave_softmax<NG>, from the scores launch's
 // scores) into its LDS probability row while the value rows load, in place
 // of loading probabilities; the caller's probs16 is written by the
