@@ -1800,29 +1800,32 @@ static bool launch_gemmkf(uint32_t t0, uint32_t t1, int nh, dim3 grid, size_t ld
     return true;
 }
 
+// Tiles of one segment: kKFWaves 32-row blocks each.
+static int64_t gemmkf_tiles(const Layout &L) {
+    return ((L.n_out + 31) / 32 + kKFWaves - 1) / kKFWaves;
+}
+
 // Whether weights over one X take the fused launch: K-quants of one row
-// length, M on the matrix cores and at most gemmkf_max_m. Q3_K rows of at
-// most 32 super-blocks stay on the separate quantization and gemmks.h
-// launches, which need no K slices there (config 4 at M = 8, per call:
-// attn 5120 x 5120 12.0 us against 14.6 fused, ffn_up 27648 x 5120 27.3
-// against 29.6; its longer rows are faster fused: ffn_down 5120 x 27648
-// 30.0 against 32.2). Q3_K keeps the four-way masked operand there (its
-// scaled 3-bit operand does not fit an int8), whose scale arithmetic per
-// result needs the rows to be streamed by many waves at once.
+// length, M on the matrix cores and at most gemmkf_max_m. Q3_K matrices of
+// at least 128 tiles (16384 rows) whose rows hold at most 32 super-blocks
+// stay on the separate quantization and gemmks.h launches, which need no K
+// slices there (config 4 ffn_up 27648 x 5120 at M = 8: 25.6 us against 28.8
+// fused); smaller ones and longer rows are faster fused (attn 5120 x 5120
+// 11.05 against 11.46, kv 1024 x 5120 9.6 against 10.45, ffn_down
+// 5120 x 27648 27.8 against 28.1). Q3_K keeps the four-way masked operand
+// there (its scaled 3-bit operand does not fit an int8), whose scale
+// arithmetic per result needs many rows in flight.
 static bool gemmkf_eligible(const sihip_ctx *ctx, int count, const sihip_weight *const *w,
                             int64_t M) {
     if (count < 1 || M < gemm_min_m(ctx->opt) || M > gemmkf_max_m(ctx->opt)) return false;
     for (int i = 0; i < count; i++) {
         const Layout &L = w[i]->L;
         if (!is_kquant(L.type) || L.n_in != w[0]->L.n_in || L.n_in % 256) return false;
-        if (L.type == T_Q3_K && L.n_in / 256 <= 32 && ctx->opt.gemmkf_max_m < 0) return false;
+        if (L.type == T_Q3_K && L.n_in / 256 <= 32 && gemmkf_tiles(L) >= 128 &&
+            ctx->opt.gemmkf_max_m < 0)
+            return false;
     }
     return true;
-}
-
-// Tiles of one segment: kKFWaves 32-row blocks each.
-static int64_t gemmkf_tiles(const Layout &L) {
-    return ((L.n_out + 31) / 32 + kKFWaves - 1) / kKFWaves;
 }
 
 // K slices of a fused launch over `tiles` tiles: as many as keep the grid
