@@ -1134,12 +1134,13 @@ constexpr int64_t kGemmhMinM = 3;
 static int64_t gemmh_min_m(const Options &o) { return o.gemmh_min_m > 0 ? o.gemmh_min_m : kGemmhMinM; }
 
 // Smallest M that takes the Q4_0 / Q5_0 / Q8_0 GEMM (gemmq.h); option
-// GEMMQ_MIN_M. At M = 4 the GEMM is the faster on the large matrices
-// (config 4 ffn_up 27648 x 5120: 30.6 us against 49.3 on the matvec kernel,
-// ffn_down 33.4 against 40.7) and up to 2 us slower on the small ones (kv
-// 1024 x 5120: 13.3 against 11.3); at M = 2 the matvec kernel wins all but
-// ffn_up.
-constexpr int64_t kGemmqMinM = 4;
+// GEMMQ_MIN_M. At M = 3 (the matvec kernel: a launch of two columns and
+// one of one) the GEMM is the faster on every config shape (config 0 Q4_0
+// 7.9 against 10.2 us, config 1 Q8_0 8.2 against 9.6, config 4 Q5_0 attn
+// 12.5 against 19.5, kv 9.5 against 13.1, ffn_up 29.9 against 43.9); at
+// M = 2 the matvec kernel is (6.1 / 5.5 / 11.6 / 7.9 / 26.6 against 8.0 /
+// 8.3 / 12.4 / 9.5 / 29.8).
+constexpr int64_t kGemmqMinM = 3;
 static int64_t gemmq_min_m(const Options &o) { return o.gemmq_min_m > 0 ? o.gemmq_min_m : kGemmqMinM; }
 
 // Shape of one matrix-core GEMM call: tile height, padded rows, workspace
