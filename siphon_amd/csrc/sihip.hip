@@ -784,12 +784,22 @@ static int run_matvec_multi(sihip_ctx *ctx, int count, const sihip_weight *const
     // matrix (each wave then walks two of its tiles) where that brings it to
     // one per CU: otherwise half the CUs run two workgroups and the rest one.
     // Llama-3-8B q/k/v (256 + 64 + 64 workgroups): 6.34 -> 5.52 us.
+    // (Only where the halved matrix still cuts into ranges as wide as the
+    // narrowest matrix, below, so the grid keeps no surplus workgroups.)
     if (count > 1 && want_sum > ctx->n_cu && want_sum <= wg_cap) {
         int big = -1;
         for (int i = 0; i < count; i++)
             if (w[i]->split == 1 && (big < 0 || nwg[i] > nwg[big])) big = i;
-        if (big >= 0 && nwg[big] % 2 == 0 && want_sum - nwg[big] / 2 <= ctx->n_cu)
-            nwg[big] /= 2;
+        if (big >= 0 && nwg[big] % 2 == 0 && want_sum - nwg[big] / 2 <= ctx->n_cu) {
+            const int64_t half = nwg[big] / 2;
+            int64_t narrow_other = 0;
+            for (int i = 0; i < count; i++)
+                if (i != big && (narrow_other == 0 || nwg[i] < narrow_other)) narrow_other = nwg[i];
+            const int64_t ntiles = (n_out[big] + w[big]->L.R - 1) / w[big]->L.R;
+            if (narrow_other > 0 && half >= narrow_other && half % narrow_other == 0 &&
+                ntiles % (half * kWaves) == 0)
+                nwg[big] = half;
+        }
     }
     for (int i = 0; i < count; i++) {
         if (w[i]->split > 1) {
