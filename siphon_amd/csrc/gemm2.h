@@ -81,7 +81,11 @@ __global__ __launch_bounds__(kG2Threads) void gemm2_quantize_x(const float *x, i
     const int lane16 = threadIdx.x & 15;
     const int64_t blk = (int64_t)blockIdx.x * (kG2Threads / 16) + (threadIdx.x >> 4);
     if (blk >= Mp * nb) return;  // whole 16-lane rows leave together
-    const int64_t m = blk / nb, c = blk % nb;
+    // a workgroup takes 16 consecutive rows of one super-block column (Mp is
+    // a multiple of 16), so its record stores fill whole cache lines (16 rows
+    // x 16 bytes per piece) instead of 16-byte pieces of lines that other
+    // workgroups complete
+    const int64_t m = blk % Mp, c = blk / Mp;
     Q8KRow r;
     if (m < M) {
         const float4 *src = reinterpret_cast<const float4 *>(x + m * ldx + c * 256 + lane16 * 16);
