@@ -33,14 +33,17 @@ typedef _Float16 v8hh_t __attribute__((ext_vector_type(8)));
 __host__ __device__ constexpr int gh_rec_bytes(int BM) { return 256 * BM; }
 
 // One thread per 8 elements (16 bytes of a fragment); rows M..Mp-1 are
-// zero. Grid: ceil(Mp * n_in / 8 / 256) workgroups of 256.
+// zero. Grid: ceil(Mp * n_in / 8 / 256) workgroups of 256. Groups of 16
+// consecutive threads take 16 consecutive rows (Mp is a multiple of 16) of
+// one 8-element piece, so their stores fill 256 contiguous bytes.
 template <int BM>
 __global__ __launch_bounds__(256) void gemmh_convert_x(const float *x, int64_t ldx, int64_t M,
                                                        int64_t Mp, int64_t n_in, uint8_t *rec) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t per_row = n_in / 8;
     if (i >= Mp * per_row) return;
-    const int64_t m = i / per_row, k8 = i % per_row;
+    const int64_t grp = i >> 4;  // (row group of 16, piece)
+    const int64_t m = (grp / per_row) * 16 + (i & 15), k8 = grp % per_row;
     const int64_t k = k8 * 8;
     const int64_t c = k / 128;
     const int ks = (int)((k % 128) / 32), g = (int)((k % 32) / 8);

@@ -87,13 +87,16 @@ __device__ inline void gq_quantize_one(const float *x, int64_t ldx, int64_t M, i
 }
 
 // One thread per Q8_0 block (row m, block kb); rows M..Mp-1 are zero.
+// Consecutive threads take consecutive rows of one block column (Mp is a
+// multiple of 16), so the record stores of 16 threads fill whole lines
+// (16 rows x 8 bytes per fragment piece, 16 rows' scales and sums).
 template <int BM, int BIAS>
 __global__ __launch_bounds__(256) void gemmq_quantize_x(const float *x, int64_t ldx, int64_t M,
                                                         int64_t Mp, int64_t n_in, uint8_t *rec,
                                                         int scalar) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= Mp * (n_in / 32)) return;
-    gq_quantize_one<BM, BIAS>(x, ldx, M, n_in, rec, i, scalar);
+    gq_quantize_one<BM, BIAS>(x, ldx, M, n_in, rec, (i % Mp) * (n_in / 32) + i / Mp, scalar);
 }
 
 // ---- weight copy in the order of this kernel ----------------------------------
