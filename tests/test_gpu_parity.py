@@ -270,3 +270,24 @@ def test_dequant_rows_bitexact(dev, oracle, option, wt):
         finally:
             buf.free()
             w.free()
+
+
+@pytest.mark.parametrize("wt,n_out,n_in,G", [
+    (sa.Q8_0, 4864, 896, 8),      # narrowest tile with <= 6 rounds: 608 row tiles
+    (sa.Q5_0, 5120, 5120, 32),    # 5 rounds, 2560 row tiles
+    (sa.F16, 1024, 5120, 32),     # 5 rounds, 512 row tiles
+    (sa.Q4_0, 5632, 2048, 16),    # 4 rounds, 1408 row tiles
+    (sa.Q8_0, 896, 896, 32),      # 8 wide would give 112 row tiles: the tile-count rule
+    (sa.Q5_0, 27648, 5120, 16),   # 32 wide would give 13824 row tiles: the tile-count rule
+    (sa.Q4_K, 4096, 4096, 16),    # K-quants keep the tile-count rule
+])
+def test_tile_width_rule(dev, wt, n_out, n_in, G):
+    """The batch-1 tile width chosen at upload for unit-column formats: the
+    narrowest tile with at most 6 rounds per lane where that gives 512-4096
+    row tiles, the tile-count rule otherwise."""
+    rng = np.random.default_rng(n_out + n_in)
+    w = dev.upload(wt, n_out, n_in, synth.make_weights(wt, n_out, n_in, rng))
+    try:
+        assert w.tile_cols == G, (sa.NAMES[wt], n_out, n_in, w.tile_cols)
+    finally:
+        w.free()
